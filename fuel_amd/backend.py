@@ -1,0 +1,260 @@
+"""Python mirror of fuel's quantized seams over the C ABI.
+
+* ``RocmDevice``   -- ``DynBackendDevice`` + ``QuantizedDeviceKernels``
+  (fuel-backend-contract/src/quantized.rs:108-119: ``qzeros``, ``load_quantized``).
+* ``RocmStorage``  -- a device f32/f16/i32 buffer standing in for ``DynBackendStorage``.
+* ``RocmQStorage`` -- ``DynQuantizedStorage`` (quantized.rs:29-103: ``dtype``,
+  ``block_size``, ``storage_size_in_bytes``, ``dequantize``, ``dequantize_f16``,
+  ``data``, ``device_ptr``, ``fwd``).
+* ``qmatmul_f32_rocm_wrapper`` -- the ``KernelRef`` registered at
+  ``(OpKind::QMatMul, [F32, U32, F32], Rocm)`` (fuel-dispatch/src/dispatch.rs
+  :1638-1718), same argument meaning and error behaviour.
+
+Errors raise ``FuelRocmError`` (fuel's ``Err(Error::Msg(..))``).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Sequence
+
+import numpy as np
+
+from . import _native as N
+from ._native import FuelRocmError, check, lib
+
+_NP = {N.F32: np.float32, N.F16: np.uint16}
+
+
+def type_size(ggml_dtype: int) -> int:
+    return int(lib().frq_type_size(ggml_dtype))
+
+
+def block_size(ggml_dtype: int) -> int:
+    return int(lib().frq_block_size(ggml_dtype))
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    check(lib().frq_device_count(C.byref(n)))
+    return n.value
+
+
+class RocmDevice:
+    """One GPU with its own HIP stream and activation workspace."""
+
+    def __init__(self, ordinal: int = 0):
+        h = C.c_void_p()
+        check(lib().frq_device_open(ordinal, C.byref(h)))
+        self._h = h
+        self.ordinal = ordinal
+
+    @property
+    def handle(self) -> C.c_void_p:
+        if self._h is None:
+            raise FuelRocmError(N.FRQ_INVALID, "device is closed")
+        return self._h
+
+    def close(self) -> None:
+        if self._h is not None:
+            lib().frq_device_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def synchronize(self) -> None:
+        check(lib().frq_sync(self.handle))
+
+    def set_stream(self, hip_stream_ptr: int | None) -> None:
+        check(lib().frq_device_set_stream(self.handle, C.c_void_p(hip_stream_ptr or 0)))
+
+    @property
+    def cu_count(self) -> int:
+        n = C.c_int(0)
+        check(lib().frq_device_cu_count(self.handle, C.byref(n)))
+        return n.value
+
+    # ---- storages ----
+    def alloc(self, shape, dtype=np.float32) -> "RocmStorage":
+        return RocmStorage(self, tuple(int(s) for s in np.atleast_1d(shape)), np.dtype(dtype))
+
+    def from_numpy(self, a: np.ndarray) -> "RocmStorage":
+        a = np.ascontiguousarray(a)
+        s = RocmStorage(self, a.shape, a.dtype)
+        s.copy_from(a)
+        return s
+
+    # ---- QuantizedDeviceKernels ----
+    def qzeros(self, elem_count: int, ggml_dtype: int) -> "RocmQStorage":
+        h = C.c_void_p()
+        check(lib().frq_qstorage_zeros(self.handle, ggml_dtype, elem_count, C.byref(h)))
+        return RocmQStorage(self, h)
+
+    def load_quantized(self, ggml_dtype: int, data) -> "RocmQStorage":
+        buf = np.ascontiguousarray(np.frombuffer(memoryview(data).cast("B"), np.uint8))
+        h = C.c_void_p()
+        check(lib().frq_qstorage_load(self.handle, ggml_dtype, buf.ctypes.data_as(C.c_void_p),
+                                      buf.nbytes, C.byref(h)))
+        return RocmQStorage(self, h)
+
+
+class RocmStorage:
+    """A contiguous device buffer of `shape` and numpy `dtype`."""
+
+    def __init__(self, dev: RocmDevice, shape: tuple, dtype: np.dtype):
+        self.dev = dev
+        self.shape = tuple(shape)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        p = C.c_void_p()
+        check(lib().frq_malloc(dev.handle, self.nbytes, C.byref(p)))
+        self.ptr = p.value or 0
+
+    def free(self) -> None:
+        if self.ptr:
+            lib().frq_free(self.dev.handle, C.c_void_p(self.ptr))
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def copy_from(self, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a, dtype=self.dtype)
+        assert a.nbytes == self.nbytes, (a.nbytes, self.nbytes)
+        check(lib().frq_memcpy_htod(self.dev.handle, C.c_void_p(self.ptr),
+                                    a.ctypes.data_as(C.c_void_p), a.nbytes))
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        check(lib().frq_memcpy_dtoh(self.dev.handle, out.ctypes.data_as(C.c_void_p),
+                                    C.c_void_p(self.ptr), self.nbytes))
+        return out
+
+
+class RocmQStorage:
+    """``DynQuantizedStorage`` for the ROCm device (block bytes in HBM)."""
+
+    def __init__(self, dev: RocmDevice, handle: C.c_void_p):
+        self.dev = dev
+        self._h = handle
+
+    def __del__(self):
+        try:
+            if self._h:
+                lib().frq_qstorage_free(self._h)
+                self._h = None
+        except Exception:
+            pass
+
+    @property
+    def handle(self):
+        return self._h
+
+    def dtype(self) -> int:
+        return int(lib().frq_qstorage_dtype(self._h))
+
+    def block_size(self) -> int:
+        return int(lib().frq_qstorage_block_size(self._h))
+
+    def storage_size_in_bytes(self) -> int:
+        return int(lib().frq_qstorage_size_in_bytes(self._h))
+
+    def data(self) -> bytes:
+        n = self.storage_size_in_bytes()
+        out = np.empty(n, np.uint8)
+        check(lib().frq_qstorage_data(self._h, out.ctypes.data_as(C.c_void_p), n))
+        return out.tobytes()
+
+    def device_ptr(self) -> int:
+        p = C.c_void_p()
+        check(lib().frq_qstorage_device_ptr(self._h, C.byref(p)))
+        return p.value or 0
+
+    def dequantize(self, elem_count: int) -> RocmStorage:
+        y = self.dev.alloc((elem_count,), np.float32)
+        check(lib().frq_qstorage_dequantize(self._h, elem_count, C.c_void_p(y.ptr)))
+        return y
+
+    def dequantize_f16(self, elem_count: int) -> RocmStorage:
+        y = self.dev.alloc((elem_count,), np.uint16)
+        check(lib().frq_qstorage_dequantize_f16(self._h, elem_count, C.c_void_p(y.ptr)))
+        return y
+
+    def fwd(self, self_shape: Sequence[int], inp: RocmStorage):
+        """QMatMul forward: input [..., k] -> fresh output [..., n]
+        (fuel-cpu-backend/src/quantized.rs:85-142 semantics)."""
+        n, k = (int(d) for d in self_shape)
+        if inp.dtype != np.float32:
+            raise FuelRocmError(N.FRQ_UNSUPPORTED, f"fwd: expected f32 input, got {inp.dtype}")
+        if len(inp.shape) < 2:
+            raise FuelRocmError(N.FRQ_INVALID, f"input tensor has only one dimension {inp.shape}")
+        if inp.shape[-1] != k:
+            raise FuelRocmError(N.FRQ_INVALID, f"input tensor {inp.shape} incompatible with {tuple(self_shape)}")
+        out_shape = tuple(inp.shape[:-1]) + (n,)
+        y = self.dev.alloc(out_shape, np.float32)
+        m = int(np.prod(inp.shape[:-1]))
+        check(lib().frq_qstorage_fwd(self._h, n, k, C.c_void_p(inp.ptr), m, C.c_void_p(y.ptr)))
+        return y, out_shape
+
+
+@dataclass
+class QMatMulParams:
+    """``OpParams::QMatMul{quant_type, batch_count, m, n, k}`` (fuel-dispatch/src/kernel.rs:482-488);
+    quant_type is the GgmlDType code."""
+
+    quant_type: int
+    batch_count: int
+    m: int
+    n: int
+    k: int
+
+
+def qmatmul_f32_rocm_wrapper(inputs: Sequence[RocmStorage], outputs: Sequence[RocmStorage],
+                             params: QMatMulParams) -> None:
+    """KernelRef for (QMatMul, [F32, U32, F32], Rocm): inputs = [activations f32,
+    weight bytes U32-typed], outputs = [pre-allocated f32]; fully overwrites the output."""
+    if len(inputs) != 2:
+        raise FuelRocmError(N.FRQ_INVALID,
+                            f"qmatmul wrapper expects 2 inputs (activations, weight_bytes), got {len(inputs)}")
+    if len(outputs) != 1:
+        raise FuelRocmError(N.FRQ_INVALID, f"qmatmul wrapper expects 1 output, got {len(outputs)}")
+    act, w = inputs
+    out = outputs[0]
+    if w.dtype != np.uint32:
+        raise FuelRocmError(N.FRQ_INVALID,
+                            f"qmatmul: weight bytes must be U32-typed (raw block stream), got {w.dtype}")
+    p = params
+    check(lib().frq_qmatmul(act.dev.handle, p.quant_type, p.batch_count, p.m, p.n, p.k,
+                            C.c_void_p(act.ptr), act.nbytes, C.c_void_p(w.ptr), w.nbytes,
+                            C.c_void_p(out.ptr), out.nbytes))
+
+
+# ---- parity taps ----
+
+def quantize_q8k(dev: RocmDevice, x: RocmStorage, rows: int, k: int) -> np.ndarray:
+    """Device BlockQ8K quantization of x [rows, k]; returns the block bytes."""
+    out = dev.alloc((rows * (k // 256) * 292,), np.uint8)
+    check(lib().frq_quantize_q8k(dev.handle, C.c_void_p(x.ptr), rows, k, C.c_void_p(out.ptr)))
+    return out.numpy()
+
+
+def quantize_q8_0(dev: RocmDevice, x: RocmStorage, rows: int, k: int) -> np.ndarray:
+    out = dev.alloc((rows * (k // 32) * 34,), np.uint8)
+    check(lib().frq_quantize_q8_0(dev.handle, C.c_void_p(x.ptr), rows, k, C.c_void_p(out.ptr)))
+    return out.numpy()
+
+
+def block_isums(dev: RocmDevice, ggml_dtype: int, w: RocmStorage, x: RocmStorage, m: int, n: int, k: int):
+    kb = k // block_size(ggml_dtype)
+    isum = dev.alloc((m, n, kb), np.int32)
+    msum = dev.alloc((m, n, kb), np.int32)
+    check(lib().frq_block_isums(dev.handle, ggml_dtype, m, n, k, C.c_void_p(w.ptr), C.c_void_p(x.ptr),
+                                C.c_void_p(isum.ptr), C.c_void_p(msum.ptr)))
+    return isum.numpy(), msum.numpy()

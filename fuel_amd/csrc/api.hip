@@ -1,0 +1,459 @@
+// C ABI of the gfx950 quantized-matmul backend (include/fuel_rocm.h): device
+// handles, quantized storages (the DynQuantizedStorage / QuantizedDeviceKernels
+// mirror) and the KernelRef-shaped qmatmul.  Host code only.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/fuel_rocm.h"
+#include "common.hpp"
+#include "kernels.hpp"
+
+using namespace frq;
+
+struct frq_device {
+    int ordinal = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    int num_cus = 0;
+    void* ws = nullptr;  // activation workspace (quantized rows)
+    size_t ws_bytes = 0;
+};
+
+struct frq_qstorage {
+    frq_device* dev = nullptr;
+    int dtype = 0;
+    size_t nbytes = 0;
+    uint8_t* d_ptr = nullptr;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                   \
+    do {                                                                                \
+        hipError_t e_ = (expr);                                                         \
+        if (e_ != hipSuccess)                                                           \
+            return fail(FRQ_INTERNAL, "%s: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, \
+                        __LINE__);                                                      \
+    } while (0)
+
+size_t type_size(int t) {
+    switch (t) {
+        case GGML_Q8_0: return Q8_0_BYTES;
+        case GGML_Q4K: return Q4K_BYTES;
+        case GGML_Q6K: return Q6K_BYTES;
+        case GGML_Q8K: return Q8K_BYTES;
+        default: return 0;
+    }
+}
+
+size_t block_elems(int t) {
+    switch (t) {
+        case GGML_Q8_0: return QK8_0;
+        case GGML_Q4K:
+        case GGML_Q6K:
+        case GGML_Q8K: return QK_K;
+        default: return 0;
+    }
+}
+
+bool is_weight_type(int t) { return t == GGML_Q8_0 || t == GGML_Q4K || t == GGML_Q6K; }
+
+// Activation dtype a weight type is dotted against (GgmlType::VecDotType).
+int vec_dot_type(int t) { return t == GGML_Q8_0 ? GGML_Q8_0 : GGML_Q8K; }
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Byte size of the quantized-activation workspace for rows x k.
+size_t act_bytes(int vt, size_t rows, size_t k) {
+    const size_t kb = k / block_elems(vt);
+    size_t b = align256(rows * k);                       // qs
+    b += align256(rows * kb * sizeof(float));            // d
+    if (vt == GGML_Q8K) b += align256(rows * kb * 16 * sizeof(int16_t));  // bsums
+    return b;
+}
+
+ActView act_view(void* base, int vt, size_t rows, size_t k) {
+    const size_t kb = k / block_elems(vt);
+    uint8_t* p = static_cast<uint8_t*>(base);
+    ActView v;
+    v.qs = reinterpret_cast<int8_t*>(p);
+    p += align256(rows * k);
+    v.d = reinterpret_cast<float*>(p);
+    p += align256(rows * kb * sizeof(float));
+    v.bsums = vt == GGML_Q8K ? reinterpret_cast<int16_t*>(p) : nullptr;
+    return v;
+}
+
+int ensure_ws(frq_device* dev, size_t bytes) {
+    if (bytes <= dev->ws_bytes) return FRQ_OK;
+    size_t want = bytes < 2 * dev->ws_bytes ? 2 * dev->ws_bytes : bytes;
+    if (dev->ws) HIP_TRY(hipFree(dev->ws));  // hipFree waits for work that may use it
+    dev->ws = nullptr;
+    dev->ws_bytes = 0;
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, want);
+    if (e != hipSuccess)
+        return fail(FRQ_WORKSPACE, "workspace allocation of %zu bytes failed: %s", want,
+                    hipGetErrorString(e));
+    dev->ws = p;
+    dev->ws_bytes = want;
+    return FRQ_OK;
+}
+
+int use_device(frq_device* dev) {
+    if (!dev) return fail(FRQ_INVALID, "null device handle");
+    HIP_TRY(hipSetDevice(dev->ordinal));
+    return FRQ_OK;
+}
+
+// Quantize rows x [rows, k] into the workspace (and optionally into fuel's
+// block layout at `aos`), returning the workspace view.
+int quantize_rows(frq_device* dev, int vt, const float* x, size_t rows, size_t k, void* aos,
+                  ActView* view) {
+    int rc = ensure_ws(dev, act_bytes(vt, rows, k));
+    if (rc) return rc;
+    *view = act_view(dev->ws, vt, rows, k);
+    if (rows == 0) return FRQ_OK;
+    hipError_t e = vt == GGML_Q8K
+                       ? launch_quantize_q8k(x, (int)rows, (int)k, *view, (uint8_t*)aos, dev->stream)
+                       : launch_quantize_q8_0(x, (int)rows, (int)k, *view, (uint8_t*)aos, dev->stream);
+    HIP_TRY(e);
+    return FRQ_OK;
+}
+
+// y[rows, n] = x[rows, k] @ dequant(W[n, k])^T through the int8 path.
+int run_qmatmul(frq_device* dev, int t, const uint8_t* w, const float* x, size_t rows, size_t n,
+                size_t k, float* y) {
+    if (rows == 0 || n == 0) return FRQ_OK;
+    if (k > (size_t)0x7fffffff || n > (size_t)0x7fffffff || rows > 65535)
+        return fail(FRQ_UNSUPPORTED, "qmatmul: rows=%zu n=%zu k=%zu exceed the launch limits", rows,
+                    n, k);
+    ActView act;
+    int rc = quantize_rows(dev, vec_dot_type(t), x, rows, k, nullptr, &act);
+    if (rc) return rc;
+    HIP_TRY(launch_mmvq(t, w, act, y, (int)rows, (int)n, (int)k, (int)n, dev->stream, dev->num_cus));
+    return FRQ_OK;
+}
+
+bool aligned4(const void* p) { return ((uintptr_t)p & 3u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+const char* frq_last_error(void) { return g_err.c_str(); }
+
+size_t frq_type_size(int t) { return type_size(t); }
+size_t frq_block_size(int t) { return block_elems(t); }
+
+int frq_device_count(int* count) {
+    if (!count) return fail(FRQ_INVALID, "null count");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) n = 0;
+    *count = n;
+    return FRQ_OK;
+}
+
+int frq_device_open(int ordinal, frq_device** out) {
+    if (!out) return fail(FRQ_INVALID, "null out");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || ordinal < 0 || ordinal >= n)
+        return fail(FRQ_INVALID, "device ordinal %d not present (%d devices)", ordinal, n);
+    HIP_TRY(hipSetDevice(ordinal));
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, ordinal));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(FRQ_UNSUPPORTED, "device %d is %s; this library is built for gfx950", ordinal,
+                    prop.gcnArchName);
+    frq_device* d = new frq_device();
+    d->ordinal = ordinal;
+    d->num_cus = prop.multiProcessorCount;
+    hipError_t e = hipStreamCreateWithFlags(&d->own_stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete d;
+        return fail(FRQ_INTERNAL, "hipStreamCreate: %s", hipGetErrorString(e));
+    }
+    d->stream = d->own_stream;
+    *out = d;
+    return FRQ_OK;
+}
+
+int frq_device_close(frq_device* dev) {
+    if (!dev) return FRQ_OK;
+    (void)hipSetDevice(dev->ordinal);
+    (void)hipStreamSynchronize(dev->stream);
+    if (dev->ws) (void)hipFree(dev->ws);
+    if (dev->own_stream) (void)hipStreamDestroy(dev->own_stream);
+    delete dev;
+    return FRQ_OK;
+}
+
+int frq_device_set_stream(frq_device* dev, void* s) {
+    if (!dev) return fail(FRQ_INVALID, "null device");
+    dev->stream = s ? static_cast<hipStream_t>(s) : dev->own_stream;
+    return FRQ_OK;
+}
+
+int frq_sync(frq_device* dev) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    HIP_TRY(hipStreamSynchronize(dev->stream));
+    return FRQ_OK;
+}
+
+int frq_device_cu_count(const frq_device* dev, int* cus) {
+    if (!dev || !cus) return fail(FRQ_INVALID, "null argument");
+    *cus = dev->num_cus;
+    return FRQ_OK;
+}
+
+int frq_malloc(frq_device* dev, size_t bytes, void** dptr) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (!dptr) return fail(FRQ_INVALID, "null out");
+    *dptr = nullptr;
+    if (bytes == 0) return FRQ_OK;
+    hipError_t e = hipMalloc(dptr, bytes);
+    if (e != hipSuccess) return fail(FRQ_WORKSPACE, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    return FRQ_OK;
+}
+
+int frq_free(frq_device* dev, void* p) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (p) HIP_TRY(hipFree(p));
+    return FRQ_OK;
+}
+
+int frq_memcpy_htod(frq_device* dev, void* dst, const void* src, size_t bytes) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (!bytes) return FRQ_OK;
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, dev->stream));
+    HIP_TRY(hipStreamSynchronize(dev->stream));
+    return FRQ_OK;
+}
+
+int frq_memcpy_dtoh(frq_device* dev, void* dst, const void* src, size_t bytes) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (!bytes) return FRQ_OK;
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, dev->stream));
+    HIP_TRY(hipStreamSynchronize(dev->stream));
+    return FRQ_OK;
+}
+
+int frq_memcpy_dtod(frq_device* dev, void* dst, const void* src, size_t bytes) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (!bytes) return FRQ_OK;
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, dev->stream));
+    return FRQ_OK;
+}
+
+int frq_memset(frq_device* dev, void* dst, int value, size_t bytes) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (!bytes) return FRQ_OK;
+    HIP_TRY(hipMemsetAsync(dst, value, bytes, dev->stream));
+    return FRQ_OK;
+}
+
+// ---- QuantizedDeviceKernels ----
+
+static int new_storage(frq_device* dev, int t, size_t nbytes, frq_qstorage** out) {
+    frq_qstorage* q = new frq_qstorage();
+    q->dev = dev;
+    q->dtype = t;
+    q->nbytes = nbytes;
+    if (nbytes) {
+        hipError_t e = hipMalloc(&q->d_ptr, nbytes);
+        if (e != hipSuccess) {
+            delete q;
+            return fail(FRQ_WORKSPACE, "hipMalloc(%zu): %s", nbytes, hipGetErrorString(e));
+        }
+    }
+    *out = q;
+    return FRQ_OK;
+}
+
+int frq_qstorage_zeros(frq_device* dev, int t, size_t elem_count, frq_qstorage** out) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (!out) return fail(FRQ_INVALID, "null out");
+    if (!type_size(t)) return fail(FRQ_UNSUPPORTED, "qzeros: unsupported dtype %d", t);
+    if (elem_count % block_elems(t))
+        return fail(FRQ_INVALID, "qzeros: elem_count %zu is not a multiple of %zu", elem_count,
+                    block_elems(t));
+    const size_t nbytes = elem_count / block_elems(t) * type_size(t);
+    rc = new_storage(dev, t, nbytes, out);
+    if (rc) return rc;
+    if (nbytes) HIP_TRY(hipMemsetAsync((*out)->d_ptr, 0, nbytes, dev->stream));
+    HIP_TRY(hipStreamSynchronize(dev->stream));
+    return FRQ_OK;
+}
+
+int frq_qstorage_load(frq_device* dev, int t, const void* host, size_t nbytes, frq_qstorage** out) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (!out) return fail(FRQ_INVALID, "null out");
+    if (!type_size(t)) return fail(FRQ_UNSUPPORTED, "load_quantized: unsupported dtype %d", t);
+    if (nbytes % type_size(t))
+        return fail(FRQ_INVALID, "load_quantized: %zu bytes is not a multiple of the %zu-byte block",
+                    nbytes, type_size(t));
+    if (nbytes && !host) return fail(FRQ_INVALID, "load_quantized: null host data");
+    rc = new_storage(dev, t, nbytes, out);
+    if (rc) return rc;
+    if (nbytes) {
+        HIP_TRY(hipMemcpyAsync((*out)->d_ptr, host, nbytes, hipMemcpyHostToDevice, dev->stream));
+        HIP_TRY(hipStreamSynchronize(dev->stream));
+    }
+    return FRQ_OK;
+}
+
+int frq_qstorage_free(frq_qstorage* q) {
+    if (!q) return FRQ_OK;
+    if (q->d_ptr) {
+        (void)hipSetDevice(q->dev->ordinal);
+        (void)hipStreamSynchronize(q->dev->stream);
+        (void)hipFree(q->d_ptr);
+    }
+    delete q;
+    return FRQ_OK;
+}
+
+// ---- DynQuantizedStorage ----
+
+int frq_qstorage_dtype(const frq_qstorage* q) { return q ? q->dtype : -1; }
+size_t frq_qstorage_block_size(const frq_qstorage* q) { return q ? block_elems(q->dtype) : 0; }
+size_t frq_qstorage_size_in_bytes(const frq_qstorage* q) { return q ? q->nbytes : 0; }
+
+int frq_qstorage_data(const frq_qstorage* q, void* host, size_t nbytes) {
+    if (!q) return fail(FRQ_INVALID, "null storage");
+    if (nbytes != q->nbytes) return fail(FRQ_INVALID, "data: buffer %zu bytes, storage %zu", nbytes, q->nbytes);
+    return frq_memcpy_dtoh(q->dev, host, q->d_ptr, nbytes);
+}
+
+int frq_qstorage_device_ptr(const frq_qstorage* q, const void** out) {
+    if (!q || !out) return fail(FRQ_INVALID, "null argument");
+    *out = q->d_ptr;
+    return FRQ_OK;
+}
+
+static int dequant_common(const frq_qstorage* q, size_t elem_count, void* y, bool f16) {
+    if (!q) return fail(FRQ_INVALID, "null storage");
+    int rc = use_device(q->dev);
+    if (rc) return rc;
+    if (!is_weight_type(q->dtype)) return fail(FRQ_UNSUPPORTED, "dequantize: dtype %d", q->dtype);
+    const size_t blocks = q->nbytes / type_size(q->dtype);
+    if (elem_count != blocks * block_elems(q->dtype))
+        return fail(FRQ_INVALID, "dequantize: elem_count %zu but storage holds %zu", elem_count,
+                    blocks * block_elems(q->dtype));
+    if (!aligned4(y) && !f16) return fail(FRQ_MISALIGNED, "dequantize: output not 4-byte aligned");
+    HIP_TRY(launch_dequantize(q->dtype, q->d_ptr, blocks, (float*)y, f16, q->dev->stream));
+    return FRQ_OK;
+}
+
+int frq_qstorage_dequantize(const frq_qstorage* q, size_t elem_count, float* y) {
+    return dequant_common(q, elem_count, y, false);
+}
+
+int frq_qstorage_dequantize_f16(const frq_qstorage* q, size_t elem_count, uint16_t* y) {
+    return dequant_common(q, elem_count, y, true);
+}
+
+int frq_qstorage_fwd(const frq_qstorage* q, size_t n, size_t k, const float* x, size_t m, float* y) {
+    if (!q) return fail(FRQ_INVALID, "null storage");
+    int rc = use_device(q->dev);
+    if (rc) return rc;
+    if (!is_weight_type(q->dtype)) return fail(FRQ_UNSUPPORTED, "fwd: dtype %d", q->dtype);
+    if (k % block_elems(q->dtype))
+        return fail(FRQ_INVALID, "fwd: k=%zu is not a multiple of %zu", k, block_elems(q->dtype));
+    if (n * (k / block_elems(q->dtype)) * type_size(q->dtype) != q->nbytes)
+        return fail(FRQ_INVALID, "fwd: shape [%zu, %zu] does not match %zu storage bytes", n, k,
+                    q->nbytes);
+    if (!aligned4(x) || !aligned4(y)) return fail(FRQ_MISALIGNED, "fwd: f32 buffers must be 4-byte aligned");
+    return run_qmatmul(q->dev, q->dtype, q->d_ptr, x, m, n, k, y);
+}
+
+// ---- KernelRef seam ----
+
+int frq_qmatmul(frq_device* dev, int t, size_t batch, size_t m, size_t n, size_t k, const float* act,
+                size_t act_b, const uint32_t* w, size_t w_b, float* out, size_t out_b) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (!is_weight_type(t)) return fail(FRQ_UNSUPPORTED, "qmatmul: unsupported quant_type %d", t);
+    const size_t bs = block_elems(t);
+    if (k % bs) return fail(FRQ_INVALID, "qmatmul: k=%zu must be a multiple of block size %zu", k, bs);
+    const size_t need_w = n * (k / bs) * type_size(t);
+    const size_t need_a = batch * m * k * sizeof(float);
+    const size_t need_o = batch * m * n * sizeof(float);
+    if (act_b != need_a)
+        return fail(FRQ_INVALID, "qmatmul: activations bytes=%zu doesn't match batch=%zu x m=%zu x k=%zu x 4",
+                    act_b, batch, m, k);
+    if (w_b != need_w)
+        return fail(FRQ_INVALID, "qmatmul: weight bytes=%zu doesn't match n=%zu x k/block_size=%zu x %zu",
+                    w_b, n, k / bs, type_size(t));
+    if (out_b != need_o)
+        return fail(FRQ_INVALID, "qmatmul: out bytes=%zu doesn't match batch=%zu x m=%zu x n=%zu x 4",
+                    out_b, batch, m, n);
+    if (batch == 0 || m == 0 || n == 0) return FRQ_OK;
+    if (!aligned4(w) || !aligned4(act) || !aligned4(out))
+        return fail(FRQ_MISALIGNED, "qmatmul: buffers must be 4-byte aligned");
+    // The batch shares W, so all batch*m activation rows go through one launch.
+    return run_qmatmul(dev, t, reinterpret_cast<const uint8_t*>(w), act, batch * m, n, k, out);
+}
+
+// ---- taps ----
+
+int frq_quantize_q8k(frq_device* dev, const float* x, size_t rows, size_t k, void* blocks) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (k % QK_K) return fail(FRQ_INVALID, "quantize_q8k: k=%zu not a multiple of 256", k);
+    if (rows > 65535) return fail(FRQ_UNSUPPORTED, "quantize_q8k: rows=%zu", rows);
+    ActView v;
+    return quantize_rows(dev, GGML_Q8K, x, rows, k, blocks, &v);
+}
+
+int frq_quantize_q8_0(frq_device* dev, const float* x, size_t rows, size_t k, void* blocks) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (k % QK8_0) return fail(FRQ_INVALID, "quantize_q8_0: k=%zu not a multiple of 32", k);
+    if (rows > 65535) return fail(FRQ_UNSUPPORTED, "quantize_q8_0: rows=%zu", rows);
+    ActView v;
+    return quantize_rows(dev, GGML_Q8_0, x, rows, k, blocks, &v);
+}
+
+int frq_block_isums(frq_device* dev, int t, size_t m, size_t n, size_t k, const void* w,
+                    const float* x, int32_t* isum, int32_t* msum) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (!is_weight_type(t)) return fail(FRQ_UNSUPPORTED, "block_isums: dtype %d", t);
+    if (k % block_elems(t)) return fail(FRQ_INVALID, "block_isums: k=%zu", k);
+    if (m > 65535) return fail(FRQ_UNSUPPORTED, "block_isums: m=%zu", m);
+    if (m == 0 || n == 0) return FRQ_OK;
+    ActView act;
+    rc = quantize_rows(dev, vec_dot_type(t), x, m, k, nullptr, &act);
+    if (rc) return rc;
+    HIP_TRY(launch_block_isums(t, (const uint8_t*)w, act, isum, msum, (int)m, (int)n, (int)k, dev->stream));
+    return FRQ_OK;
+}
+
+}  // extern "C"

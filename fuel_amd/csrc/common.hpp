@@ -1,0 +1,128 @@
+// Shared device helpers for the gfx950 quantized-matmul kernels.
+//
+// Block formats are the GGUF ones fuel uses (fuel-quantized/src/k_quants.rs
+// :92-169): BlockQ8_0 34 B, BlockQ4K 144 B, BlockQ6K 210 B, BlockQ8K 292 B.
+// Weights stay in that byte layout in HBM (row-major [N, K/blk] blocks), so a
+// buffer produced by fuel's quantizer or read from a GGUF file is usable as is.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace frq {
+
+constexpr int QK_K = 256;
+constexpr int QK8_0 = 32;
+constexpr int Q8_0_BYTES = 34;
+constexpr int Q4K_BYTES = 144;
+constexpr int Q6K_BYTES = 210;
+constexpr int Q8K_BYTES = 292;
+
+// GgmlDType codes (fuel-ir/src/quantized.rs:36-76).
+enum : int { GGML_F32 = 0, GGML_F16 = 1, GGML_Q8_0 = 8, GGML_Q4K = 12, GGML_Q6K = 14, GGML_Q8K = 15 };
+
+__device__ __forceinline__ float f16_to_f32(uint32_t bits) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+
+// IEEE binary16 round-to-nearest-even, written on integers so the result does
+// not depend on the MODE register; same conversion as `half::f16::from_f32`.
+__device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
+    uint32_t x = __builtin_bit_cast(uint32_t, f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t exp = (x >> 23) & 0xffu;
+    uint32_t man = x & 0x7fffffu;
+    if (exp == 0xffu) return (uint16_t)(sign | 0x7c00u | (man ? (0x0200u | (man >> 13)) : 0u));
+    int e = (int)exp - 112;
+    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        uint32_t sig = man | 0x800000u;
+        uint32_t shift = (uint32_t)(14 - e);
+        uint32_t q = sig >> shift;
+        uint32_t rem = sig & ((1u << shift) - 1u);
+        uint32_t half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t q = ((uint32_t)e << 10) | (man >> 13);
+    uint32_t rem = man & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q++;
+    return (uint16_t)(sign | q);
+}
+
+// Rust `f as i8`: saturating, NaN -> 0.
+__device__ __forceinline__ int sat_i8(float v) {
+    if (v != v) return 0;
+    v = fminf(fmaxf(v, -128.0f), 127.0f);
+    return (int)v;
+}
+
+// Rust `v.round() as i32` (utils.rs:1-3): half away from zero, saturating.
+__device__ __forceinline__ int nearest_int(float v) {
+    float r = roundf(v);
+    if (r != r) return 0;
+    if (r >= 2147483647.0f) return 2147483647;
+    if (r <= -2147483648.0f) return (int)0x80000000;
+    return (int)r;
+}
+
+// 16 bytes from a 2-byte aligned address, using only dword-aligned loads.
+// A dword that holds at least one requested byte lies in the same page as
+// that byte, so this never touches a page the caller's range does not.
+__device__ __forceinline__ uint4 load16_a2(const uint8_t* p) {
+    const uintptr_t a = (uintptr_t)p;
+    const uint32_t* q = (const uint32_t*)(a & ~(uintptr_t)3);
+    const uint32_t sh = (uint32_t)(a & 3);
+    const uint32_t w0 = q[0], w1 = q[1], w2 = q[2], w3 = q[3];
+    const uint32_t w4 = sh ? q[4] : 0u;
+    return uint4{__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh),
+                 __builtin_amdgcn_alignbyte(w3, w2, sh), __builtin_amdgcn_alignbyte(w4, w3, sh)};
+}
+
+// 8 bytes from a 2-byte aligned address (same page rule as load16_a2).
+__device__ __forceinline__ uint2 load8_a2(const uint8_t* p) {
+    const uintptr_t a = (uintptr_t)p;
+    const uint32_t* q = (const uint32_t*)(a & ~(uintptr_t)3);
+    const uint32_t sh = (uint32_t)(a & 3);
+    const uint32_t w0 = q[0], w1 = q[1];
+    const uint32_t w2 = sh ? q[2] : 0u;
+    return uint2{__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh)};
+}
+
+__device__ __forceinline__ uint32_t load_u16(const uint8_t* p) {
+    return (uint32_t)*(const uint16_t*)p;
+}
+
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// Sum over the 64 lanes of a wavefront; every lane gets the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// Activation workspace.  The mat-vec kernels read activations as int8 quants
+// in a structure-of-arrays layout (16-byte aligned rows); the byte layout of
+// fuel's BlockQ8K / BlockQ8_0 is produced on request by the tap kernels.
+//   qs    : int8  [rows][K]
+//   d     : f32   [rows][K/blk]    (Q8K: the f32 d; Q8_0: f16 d widened)
+//   bsums : int16 [rows][K/256][16] (Q8K only: sums of 16 consecutive quants)
+// ---------------------------------------------------------------------------
+struct ActView {
+    int8_t* qs;
+    float* d;
+    int16_t* bsums;
+};
+
+}  // namespace frq

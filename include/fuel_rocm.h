@@ -1,0 +1,137 @@
+/*
+ * fuel_rocm.h -- C ABI of the MI355X (gfx950) quantized-matmul backend for
+ * fuel.  Plain pointers and sizes only; device pointers are HIP device
+ * addresses on the handle's device.  Every entry point returns a status:
+ *
+ *   FRQ_OK 0, FRQ_MISALIGNED 1, FRQ_INVALID 2, FRQ_UNSUPPORTED 3,
+ *   FRQ_WORKSPACE 4, FRQ_INTERNAL 5
+ *
+ * the integer convention of fuel's CUDA FFI status codes
+ * (fuel-cuda-backend/src/baracuda/status.rs:5-12).  frq_last_error() returns
+ * the message of the calling thread's last failure.  Entry points never abort.
+ *
+ * Two seams of the reference are mirrored:
+ *   (1) the trait-object seam QuantizedDeviceKernels + DynQuantizedStorage
+ *       (fuel-backend-contract/src/quantized.rs:29-119): frq_qstorage_*;
+ *   (2) the lazy-graph KernelRef registered at (OpKind::QMatMul,
+ *       [F32, U32, F32], BackendId) (fuel-dispatch/src/dispatch.rs:1638-1718,
+ *       5801; fuel-dispatch/src/kernel.rs:168-173, 482-488): frq_qmatmul.
+ *
+ * Work is enqueued on the device's stream and is asynchronous unless stated;
+ * frq_sync waits for it.  Calls on one device handle must not overlap from
+ * several threads (the handle owns one activation workspace).
+ */
+#ifndef FUEL_ROCM_H
+#define FUEL_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    FRQ_OK = 0,
+    FRQ_MISALIGNED = 1,
+    FRQ_INVALID = 2,
+    FRQ_UNSUPPORTED = 3,
+    FRQ_WORKSPACE = 4,
+    FRQ_INTERNAL = 5
+};
+
+/* GgmlDType codes (fuel-ir/src/quantized.rs:36-76, from_u32 / to_u32). */
+enum {
+    FRQ_F32 = 0,
+    FRQ_F16 = 1,
+    FRQ_Q8_0 = 8,
+    FRQ_Q4K = 12,
+    FRQ_Q6K = 14,
+    FRQ_Q8K = 15
+};
+
+typedef struct frq_device frq_device;
+typedef struct frq_qstorage frq_qstorage;
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char *frq_last_error(void);
+
+/* GgmlDType::type_size / block_size (fuel-ir/src/quantized.rs:78-104);
+ * 0 for a code this backend does not handle. */
+size_t frq_type_size(int ggml_dtype);
+size_t frq_block_size(int ggml_dtype);
+
+/* ---- device (the DynBackendDevice handle; fuel-backend-contract/src/dyn_backend.rs:292-398) ---- */
+int frq_device_count(int *count);
+/* Opens `ordinal` with its own HIP stream. */
+int frq_device_open(int ordinal, frq_device **out);
+int frq_device_close(frq_device *dev);
+/* Use a caller-owned hipStream_t (passed as void*) instead of the device's
+ * own stream; NULL restores the device's stream. */
+int frq_device_set_stream(frq_device *dev, void *hip_stream);
+int frq_sync(frq_device *dev);
+int frq_device_cu_count(const frq_device *dev, int *cus);
+
+/* Device memory helpers standing in for DynBackendStorage buffers. */
+int frq_malloc(frq_device *dev, size_t bytes, void **dptr);
+int frq_free(frq_device *dev, void *dptr);
+int frq_memcpy_htod(frq_device *dev, void *dst, const void *src, size_t bytes); /* synchronous */
+int frq_memcpy_dtoh(frq_device *dev, void *dst, const void *src, size_t bytes); /* synchronous */
+int frq_memcpy_dtod(frq_device *dev, void *dst, const void *src, size_t bytes); /* async */
+int frq_memset(frq_device *dev, void *dst, int value, size_t bytes);            /* async */
+
+/* ---- QuantizedDeviceKernels (fuel-backend-contract/src/quantized.rs:108-119) ---- */
+/* qzeros(elem_count, dtype): zero blocks; elem_count % block_size == 0. */
+int frq_qstorage_zeros(frq_device *dev, int ggml_dtype, size_t elem_count, frq_qstorage **out);
+/* load_quantized(dtype, data): copies `nbytes` of block bytes (a multiple of
+ * type_size) from host memory to the device, in fuel's block layout. */
+int frq_qstorage_load(frq_device *dev, int ggml_dtype, const void *host_bytes, size_t nbytes,
+                      frq_qstorage **out);
+int frq_qstorage_free(frq_qstorage *qs);
+
+/* ---- DynQuantizedStorage (fuel-backend-contract/src/quantized.rs:29-103) ---- */
+int frq_qstorage_dtype(const frq_qstorage *qs);
+size_t frq_qstorage_block_size(const frq_qstorage *qs);
+size_t frq_qstorage_size_in_bytes(const frq_qstorage *qs);
+/* data(): host copy of the block bytes (synchronous). */
+int frq_qstorage_data(const frq_qstorage *qs, void *host_dst, size_t nbytes);
+/* device_ptr(): raw device address of the block bytes. */
+int frq_qstorage_device_ptr(const frq_qstorage *qs, const void **out);
+/* dequantize(elem_count) / dequantize_f16(elem_count) into a caller device
+ * buffer of elem_count f32 / f16 values (to_float semantics). */
+int frq_qstorage_dequantize(const frq_qstorage *qs, size_t elem_count, float *y_dev);
+int frq_qstorage_dequantize_f16(const frq_qstorage *qs, size_t elem_count, uint16_t *y_dev);
+/* fwd(self_shape = [n, k], input [m, k] contiguous f32) -> y [m, n] f32.
+ * The trait method returns a fresh storage; here the caller passes the
+ * output buffer (the host-side mirror allocates it). */
+int frq_qstorage_fwd(const frq_qstorage *qs, size_t n, size_t k, const float *x_dev, size_t m,
+                     float *y_dev);
+
+/* ---- KernelRef seam: (QMatMul, [F32, U32, F32]) ----
+ * qmatmul_f32 wrapper semantics (fuel-dispatch/src/dispatch.rs:1638-1718 and
+ * fuel-cpu-backend/src/byte_kernels.rs:4757-4830): act [batch, m, k] f32,
+ * weight bytes = n * (k / block) blocks of `quant_type` (U32-typed storage,
+ * 4-byte aligned), out [batch, m, n] f32 pre-allocated and fully overwritten.
+ * Byte lengths are validated exactly as the CPU kernel does; a zero batch,
+ * m or n is a no-op.  quant_type is the GgmlDType code (Q8_0 = 8,
+ * Q4_K_M = Q4K = 12, Q6K = 14). */
+int frq_qmatmul(frq_device *dev, int quant_type, size_t batch, size_t m, size_t n, size_t k,
+                const float *act_dev, size_t act_bytes, const uint32_t *w_dev, size_t w_bytes,
+                float *out_dev, size_t out_bytes);
+
+/* ---- integer taps (build-internal parity probes; no reference counterpart) ----
+ * Quantize rows of f32 activations into fuel's activation blocks
+ * (BlockQ8K::from_float k_quants.rs:2230-2267, BlockQ8_0::from_float
+ * :629-658), written in the reference byte layout [rows, k/blk] blocks. */
+int frq_quantize_q8k(frq_device *dev, const float *x_dev, size_t rows, size_t k, void *blocks_dev);
+int frq_quantize_q8_0(frq_device *dev, const float *x_dev, size_t rows, size_t k, void *blocks_dev);
+/* Per-(row m, weight row n, block b) integer sums of the block dot product
+ * (vec_dot_unopt's integer stage): isum/msum [m, n, k/blk] int32.  The
+ * activations are quantized on the device from x_dev first. */
+int frq_block_isums(frq_device *dev, int ggml_dtype, size_t m, size_t n, size_t k,
+                    const void *w_dev, const float *x_dev, int32_t *isum_dev, int32_t *msum_dev);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
