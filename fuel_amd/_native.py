@@ -61,11 +61,14 @@ SIGNATURES = {
     "frq_qstorage_device_ptr": (_i32, [_vp, C.POINTER(_vp)]),
     "frq_qstorage_dequantize": (_i32, [_vp, _sz, _vp]),
     "frq_qstorage_dequantize_f16": (_i32, [_vp, _sz, _vp]),
+    "frq_qstorage_quantize": (_i32, [_vp, _vp, _sz]),
     "frq_qstorage_fwd": (_i32, [_vp, _sz, _sz, _vp, _sz, _vp]),
     "frq_qmatmul": (_i32, [_vp, _i32, _sz, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz]),
     "frq_quantize_q8k": (_i32, [_vp, _vp, _sz, _sz, _vp]),
     "frq_quantize_q8_0": (_i32, [_vp, _vp, _sz, _sz, _vp]),
     "frq_block_isums": (_i32, [_vp, _i32, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
+    "frq_fill_random_bits": (_i32, [_vp, _vp, _sz, C.c_uint64, C.c_uint64, C.c_uint32, C.c_uint32]),
+    "frq_fill_normal": (_i32, [_vp, _vp, _sz, C.c_uint64, C.c_uint32, C.c_float, C.c_float]),
 }
 
 _lib = None

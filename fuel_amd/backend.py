@@ -187,6 +187,12 @@ class RocmQStorage:
         check(lib().frq_qstorage_dequantize_f16(self._h, elem_count, C.c_void_p(y.ptr)))
         return y
 
+    def quantize(self, src: RocmStorage) -> None:
+        """from_float of a device f32 source onto this storage (on the device)."""
+        if src.dtype != np.float32:
+            raise FuelRocmError(N.FRQ_INVALID, f"quantize: expected f32 source, got {src.dtype}")
+        check(lib().frq_qstorage_quantize(self._h, C.c_void_p(src.ptr), src.nbytes // 4))
+
     def fwd(self, self_shape: Sequence[int], inp: RocmStorage):
         """QMatMul forward: input [..., k] -> fresh output [..., n]
         (fuel-cpu-backend/src/quantized.rs:85-142 semantics)."""
@@ -234,6 +240,20 @@ def qmatmul_f32_rocm_wrapper(inputs: Sequence[RocmStorage], outputs: Sequence[Ro
     check(lib().frq_qmatmul(act.dev.handle, p.quant_type, p.batch_count, p.m, p.n, p.k,
                             C.c_void_p(act.ptr), act.nbytes, C.c_void_p(w.ptr), w.nbytes,
                             C.c_void_p(out.ptr), out.nbytes))
+
+
+# ---- synthetic inputs ----
+
+def fill_normal(dev: RocmDevice, shape, seed: int, stream: int, mean: float = 0.0, std: float = 1.0) -> RocmStorage:
+    y = dev.alloc(shape, np.float32)
+    check(lib().frq_fill_normal(dev.handle, C.c_void_p(y.ptr), y.nbytes // 4, seed, stream, mean, std))
+    return y
+
+
+def fill_random_bits(dev: RocmDevice, n: int, start: int, seed: int, base: int, stream: int) -> RocmStorage:
+    y = dev.alloc((n,), np.uint32)
+    check(lib().frq_fill_random_bits(dev.handle, C.c_void_p(y.ptr), n, start, seed, base, stream))
+    return y
 
 
 # ---- parity taps ----

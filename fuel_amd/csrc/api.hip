@@ -144,10 +144,7 @@ int run_qmatmul(frq_device* dev, int t, const uint8_t* w, const float* x, size_t
     if (k > (size_t)0x7fffffff || n > (size_t)0x7fffffff || rows > 65535)
         return fail(FRQ_UNSUPPORTED, "qmatmul: rows=%zu n=%zu k=%zu exceed the launch limits", rows,
                     n, k);
-    ActView act;
-    int rc = quantize_rows(dev, vec_dot_type(t), x, rows, k, nullptr, &act);
-    if (rc) return rc;
-    HIP_TRY(launch_mmvq(t, w, act, y, (int)rows, (int)n, (int)k, (int)n, dev->stream, dev->num_cus));
+    HIP_TRY(launch_qmv(t, w, x, y, (int)rows, (int)n, (int)k, (int)n, dev->stream, dev->num_cus));
     return FRQ_OK;
 }
 
@@ -379,6 +376,20 @@ int frq_qstorage_dequantize_f16(const frq_qstorage* q, size_t elem_count, uint16
     return dequant_common(q, elem_count, y, true);
 }
 
+int frq_qstorage_quantize(frq_qstorage* q, const float* src, size_t elem_count) {
+    if (!q) return fail(FRQ_INVALID, "null storage");
+    int rc = use_device(q->dev);
+    if (rc) return rc;
+    if (!is_weight_type(q->dtype)) return fail(FRQ_UNSUPPORTED, "quantize: dtype %d", q->dtype);
+    const size_t blocks = q->nbytes / type_size(q->dtype);
+    if (elem_count != blocks * block_elems(q->dtype))
+        return fail(FRQ_INVALID, "quantize: %zu source elements for a storage of %zu", elem_count,
+                    blocks * block_elems(q->dtype));
+    if (((uintptr_t)src & 15u) != 0) return fail(FRQ_MISALIGNED, "quantize: source must be 16-byte aligned");
+    HIP_TRY(launch_quantize_weights(q->dtype, src, blocks, q->d_ptr, q->dev->stream));
+    return FRQ_OK;
+}
+
 int frq_qstorage_fwd(const frq_qstorage* q, size_t n, size_t k, const float* x, size_t m, float* y) {
     if (!q) return fail(FRQ_INVALID, "null storage");
     int rc = use_device(q->dev);
@@ -453,6 +464,24 @@ int frq_block_isums(frq_device* dev, int t, size_t m, size_t n, size_t k, const 
     rc = quantize_rows(dev, vec_dot_type(t), x, m, k, nullptr, &act);
     if (rc) return rc;
     HIP_TRY(launch_block_isums(t, (const uint8_t*)w, act, isum, msum, (int)m, (int)n, (int)k, dev->stream));
+    return FRQ_OK;
+}
+
+int frq_fill_random_bits(frq_device* dev, uint32_t* y, size_t n, uint64_t start, uint64_t seed, uint32_t base,
+                         uint32_t stream) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (n && !y) return fail(FRQ_INVALID, "null output");
+    HIP_TRY(launch_random_bits(y, n, start, seed, base, stream, dev->stream));
+    return FRQ_OK;
+}
+
+int frq_fill_normal(frq_device* dev, float* y, size_t n, uint64_t seed, uint32_t stream, float mean, float stdv) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (n && !y) return fail(FRQ_INVALID, "null output");
+    if (!aligned4(y)) return fail(FRQ_MISALIGNED, "fill_normal: output not 4-byte aligned");
+    HIP_TRY(launch_normal(y, n, seed, stream, mean, stdv, dev->stream));
     return FRQ_OK;
 }
 

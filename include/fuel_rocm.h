@@ -101,6 +101,11 @@ int frq_qstorage_device_ptr(const frq_qstorage *qs, const void **out);
  * buffer of elem_count f32 / f16 values (to_float semantics). */
 int frq_qstorage_dequantize(const frq_qstorage *qs, size_t elem_count, float *y_dev);
 int frq_qstorage_dequantize_f16(const frq_qstorage *qs, size_t elem_count, uint16_t *y_dev);
+/* quantize(src): from_float of elem_count f32 values on the device into this
+ * storage (BlockQ4K::from_float k_quants.rs:1470-1528, BlockQ6K::from_float
+ * :2005-2075, BlockQ8_0::from_float :629-658), bit-exact with the CPU
+ * quantizer; elem_count must equal the storage's element count. */
+int frq_qstorage_quantize(frq_qstorage *qs, const float *src_dev, size_t elem_count);
 /* fwd(self_shape = [n, k], input [m, k] contiguous f32) -> y [m, n] f32.
  * The trait method returns a fresh storage; here the caller passes the
  * output buffer (the host-side mirror allocates it). */
@@ -130,6 +135,16 @@ int frq_quantize_q8_0(frq_device *dev, const float *x_dev, size_t rows, size_t k
  * activations are quantized on the device from x_dev first. */
 int frq_block_isums(frq_device *dev, int ggml_dtype, size_t m, size_t n, size_t k,
                     const void *w_dev, const float *x_dev, int32_t *isum_dev, int32_t *msum_dev);
+
+/* ---- synthetic inputs (no reference counterpart: seeded test/bench data) ----
+ * Philox-4x32-10 words in fuel's RandomBits layout (fuel-cpu-kernels/src/
+ * philox.rs:91-133): element i = lane i%4 of the block at counter
+ * [(start+i)/4 lo, hi, base, stream], key = seed. */
+int frq_fill_random_bits(frq_device *dev, uint32_t *y_dev, size_t n, uint64_t start, uint64_t seed,
+                         uint32_t base, uint32_t stream);
+/* N(mean, std) by Box-Muller over the same words (counter base 0). */
+int frq_fill_normal(frq_device *dev, float *y_dev, size_t n, uint64_t seed, uint32_t stream, float mean,
+                    float std);
 
 #ifdef __cplusplus
 }

@@ -208,3 +208,42 @@ def test_kernelref_validation(dev):
     assert lib().frq_qmatmul(dev.handle, O.Q4K, 1, 0, 4, 512, C.c_void_p(empty.ptr), 0, C.c_void_p(w.ptr),
                              w.nbytes, C.c_void_p(empty.ptr), 0) == 0
     assert np.array_equal(out.numpy(), sentinel)
+
+
+# ---- device from_float (DynQuantizedStorage::quantize) and synthetic inputs ----
+
+def weight_rows(k):
+    rows = [np.zeros(k, np.float32), np.ones(k, np.float32), np.full(k, -0.75, np.float32),
+            (np.arange(k, dtype=np.float32) % 97 - 48) / 64]
+    spiky = np.zeros(k, np.float32)
+    spiky[::37] = 3.0
+    spiky[5::41] = -7.0
+    rows.append(spiky)
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("dt", [O.Q4K, O.Q6K, O.Q8_0])
+def test_device_quantize_bit_exact(dev, dt):
+    say("device from_float", dt)
+    k = 2048
+    w = np.concatenate([O.normal((64, k), seed=21, stream=5, std=0.02), weight_rows(k),
+                        O.normal((3, k), seed=22, stream=6, std=3.0)])
+    want = O.quantize(dt, w)
+    q = dev.qzeros(w.size, dt)
+    q.quantize(dev.from_numpy(w))
+    got = np.frombuffer(q.data(), O.BLOCK_DTYPE[dt]).reshape(want.shape)
+    bad = np.nonzero(got.view(np.uint8).reshape(got.size, -1) != want.view(np.uint8).reshape(want.size, -1))
+    assert got.tobytes() == want.tobytes(), f"first differing blocks {np.unique(bad[0])[:8]}"
+
+
+def test_random_bits_bit_exact(dev):
+    seed, base, stream = 0xDEADBEEF12345678, 3, 9
+    got = F.fill_random_bits(dev, 1001, 7, seed, base, stream).numpy()
+    assert np.array_equal(got, O.random_bits(1001, 7, seed, base, stream))
+
+
+def test_normal_matches_host_generator(dev):
+    got = F.fill_normal(dev, (3, 1000), 5, 2, 0.0, 0.02).numpy()
+    want = O.normal((3, 1000), seed=5, stream=2, std=0.02)
+    ulp = np.spacing(np.abs(want).astype(np.float32))
+    assert np.all(np.abs(got - want) <= ulp)
