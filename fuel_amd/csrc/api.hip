@@ -144,6 +144,10 @@ int run_qmatmul(frq_device* dev, int t, const uint8_t* w, const float* x, size_t
     if (k > (size_t)0x7fffffff || n > (size_t)0x7fffffff || rows > 65535)
         return fail(FRQ_UNSUPPORTED, "qmatmul: rows=%zu n=%zu k=%zu exceed the launch limits", rows,
                     n, k);
+    // each lane of the mat-vec holds at most 8 blocks of a row: K <= 8 * 16 * 256
+    // for the k-quants (4 lanes per superblock), K <= 8 * 32 * 32 for Q8_0
+    const size_t kmax = t == GGML_Q8_0 ? 8192 : 32768;
+    if (k > kmax) return fail(FRQ_UNSUPPORTED, "qmatmul: k=%zu exceeds %zu for dtype %d", k, kmax, t);
     HIP_TRY(launch_qmv(t, w, x, y, (int)rows, (int)n, (int)k, (int)n, dev->stream, dev->num_cus));
     return FRQ_OK;
 }

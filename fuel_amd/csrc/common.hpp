@@ -105,6 +105,21 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Wave64 sum through DPP row operations; the total is valid in lane 63 only.
+__device__ __forceinline__ float dpp_wave_sum(float v) {
+#define FRQ_DPP_ADD(ctrl, rmask)                                                                         \
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, rmask, \
+                                                               0xF, false))
+    FRQ_DPP_ADD(0xB1, 0xF);   // quad_perm [1,0,3,2]
+    FRQ_DPP_ADD(0x4E, 0xF);   // quad_perm [2,3,0,1]
+    FRQ_DPP_ADD(0x141, 0xF);  // row_half_mirror: each 8-lane half holds its sum
+    FRQ_DPP_ADD(0x140, 0xF);  // row_mirror: each 16-lane row holds its sum
+    FRQ_DPP_ADD(0x142, 0xA);  // row_bcast:15 -> rows 1, 3 add rows 0, 2
+    FRQ_DPP_ADD(0x143, 0xC);  // row_bcast:31 -> row 3 adds rows 0+1
+#undef FRQ_DPP_ADD
+    return v;
+}
+
 __device__ __forceinline__ int wave_sum_i(int v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
@@ -124,5 +139,36 @@ struct ActView {
     float* d;
     int16_t* bsums;
 };
+
+// LDS copy of one quantized activation row inside the mat-vec kernels.  Q8K
+// superblocks sit 272 bytes apart (256 + 16 of padding) so the 16 lane groups
+// of a wavefront, which read the same offset of 16 different superblocks, hit
+// different LDS banks; each section starts 16-byte aligned.
+struct ActLds {
+    int qstride;   // bytes between consecutive activation blocks
+    int off_d;     // f32 scales
+    int off_bs;    // int16 bsums (Q8K)
+    int bytes;     // total
+};
+
+__host__ __device__ constexpr int align16i(int x) { return (x + 15) & ~15; }
+
+__host__ __device__ inline ActLds act_lds_layout(int act_dtype, int K) {
+    ActLds l{};
+    if (act_dtype == GGML_Q8K) {
+        const int kb = K / QK_K;
+        l.qstride = QK_K + 16;
+        l.off_d = align16i(kb * l.qstride);
+        l.off_bs = align16i(l.off_d + 4 * kb);
+        l.bytes = l.off_bs + 32 * kb;
+    } else {
+        const int kb = K / QK8_0;
+        l.qstride = QK8_0;
+        l.off_d = align16i(K);
+        l.off_bs = align16i(l.off_d + 4 * kb);
+        l.bytes = l.off_bs;
+    }
+    return l;
+}
 
 }  // namespace frq

@@ -34,9 +34,11 @@ struct Q4K {
     struct Raw {
         uint4 hd, q0, q1;
     };
-    // Activation slice of block b of row `row` of an ActView (qs [rows][K], d [rows][KB], bsums [rows][KB][16]).
-    __device__ static void load_act(const int8_t* qs, const float* dv, const int16_t* bsums, int b, int c, Act& r) {
-        const uint4* q = reinterpret_cast<const uint4*>(qs + (size_t)b * QK_K + 64 * c);
+    // Activation slice of block b: quants `qstride` bytes apart per superblock,
+    // d [KB], bsums [KB][16].
+    __device__ static void load_act(const int8_t* qs, int qstride, const float* dv, const int16_t* bsums, int b,
+                                    int c, Act& r) {
+        const uint4* q = reinterpret_cast<const uint4*>(qs + (size_t)b * qstride + 64 * c);
         r.a[0] = q[0];
         r.a[1] = q[1];
         r.a[2] = q[2];
@@ -73,8 +75,9 @@ struct Q4K {
             lo = dot4(w[i] & 0x0f0f0f0fu, alo[i], lo);
             hi = dot4((w[i] >> 4) & 0x0f0f0f0fu, ahi[i], hi);
         }
-        isum = sc_lo * lo + sc_hi * hi;
-        msum = m_lo * x.bs_lo + m_hi * x.bs_hi;
+        // |lo|, |hi| < 2^16 and the 6-bit scales fit 24-bit multiplies exactly
+        isum = __mul24(sc_lo, lo) + __mul24(sc_hi, hi);
+        msum = __mul24(m_lo, x.bs_lo) + __mul24(m_hi, x.bs_hi);
         dw = f16_to_f32(r.hd.x & 0xffffu);
         dmw = f16_to_f32(r.hd.x >> 16);
     }
@@ -126,9 +129,10 @@ struct Q6K {
         uint32_t ssh;
         uint32_t dbits;
     };
-    __device__ static void load_act(const int8_t* qs, const float* dv, const int16_t* bsums, int b, int c, Act& r) {
+    __device__ static void load_act(const int8_t* qs, int qstride, const float* dv, const int16_t* bsums, int b,
+                                    int c, Act& r) {
         const int hh = c >> 1, l0 = 16 * (c & 1);
-        const int8_t* q = qs + (size_t)b * QK_K + 128 * hh + l0;
+        const int8_t* q = qs + (size_t)b * qstride + 128 * hh + l0;
         const int16_t* bs = bsums + (size_t)b * 16 + 8 * hh + (c & 1);
 #pragma unroll
         for (int qd = 0; qd < 4; qd++) {
@@ -184,7 +188,8 @@ struct Q6K {
         const int sc1 = (int)(int8_t)((scx >> (sel + 16)) & 0xffu);
         const int sc2 = (int)(int8_t)((scy >> sel) & 0xffu);
         const int sc3 = (int)(int8_t)((scy >> (sel + 16)) & 0xffu);
-        isum = sc0 * p0 + sc1 * p1 + sc2 * p2 + sc3 * p3;
+        // |p| <= 32*128*16 < 2^23: exact in 24-bit multiplies
+        isum = __mul24(sc0, p0) + __mul24(sc1, p1) + __mul24(sc2, p2) + __mul24(sc3, p3);
         msum = 0;
         dw = f16_to_f32(r.dbits);
         dmw = 0.0f;
@@ -207,8 +212,9 @@ struct Q80 {
         A2x16 q;
         uint32_t dbits;
     };
-    __device__ static void load_act(const int8_t* qs, const float* dv, const int16_t*, int b, int c, Act& r) {
-        r.a = *reinterpret_cast<const uint4*>(qs + (size_t)b * QK8_0 + 16 * c);
+    __device__ static void load_act(const int8_t* qs, int qstride, const float* dv, const int16_t*, int b, int c,
+                                    Act& r) {
+        r.a = *reinterpret_cast<const uint4*>(qs + (size_t)b * qstride + 16 * c);
         r.d = dv[b];
     }
     __device__ static void load(const uint8_t* blk, int c, Raw& r) {

@@ -3,13 +3,14 @@
 // step, in one kernel.
 //
 // Each workgroup first quantizes its activation row (f32 -> Q8K / Q8_0, the
-// bit-exact routine of q8.hpp) into LDS, while the first weight row's loads
-// are already in flight.  Then every wavefront walks weight rows with a grid
-// stride: LPB lanes per block, 64/LPB blocks of one row per step, the lane's
-// activation slices held in registers for the whole launch (activation-
-// stationary), the next row's 128-bit weight loads issued before the current
-// row is reduced.  Scales/mins are unpacked in registers, the integer block
-// sums use v_dot4_i32_i8 and each row ends in a wave64 reduction.
+// bit-exact routine of q8.hpp) into LDS: the activation loads are issued
+// first, then the first weight row's, so the quantize step overlaps the HBM
+// latency of the weights.  Then every wavefront walks weight rows with a grid
+// stride: LPB lanes per block, 64/LPB blocks of one row per step, the next
+// row's 128-bit weight loads in flight (a two-row register ring, no copies)
+// while the current row is reduced.  Activation slices are read from LDS,
+// scales/mins are unpacked in registers, the integer block sums use
+// v_dot4_i32_i8 and each row ends in a DPP wave64 reduction.
 //
 // The only rounding after the exact integer stage is the f32 combination
 // y += d_w*d_x*isum - dmin_w*d_x*msum.
@@ -20,101 +21,102 @@
 
 namespace frq {
 
+// Workgroup size: 512 threads while the two-row ring of raw weight registers
+// stays small (<= 40 dwords per row), else 256; both leave room for 2-3
+// resident workgroups per CU without spilling.
+template <class F, int SPL>
+constexpr int qmv_wg() {
+    return SPL * (int)(sizeof(typename F::Raw) / 4) <= 40 ? 512 : 256;
+}
+
+template <class F, int SPL>
+__device__ __forceinline__ void qmv_load_row(const uint8_t* __restrict__ W, size_t row_bytes, int row, int gi, int c,
+                                             int KB, typename F::Raw (&r)[SPL]) {
+    constexpr int BPW = 64 / F::LPB;
+#pragma unroll
+    for (int s = 0; s < SPL; s++) {
+        const int b = gi + BPW * s;
+        if (b < KB) F::load(W + (size_t)row * row_bytes + (size_t)b * F::BYTES, c, r[s]);
+    }
+}
+
+// Row dot product of one weight row (raw registers) with the LDS activation;
+// the f32 total is valid in lane 63.
+template <class F, int SPL>
+__device__ __forceinline__ float qmv_row(const typename F::Raw (&r)[SPL], const int8_t* s_qs, int qstride,
+                                         const float* s_d, const int16_t* s_bs, int gi, int c, int KB) {
+    constexpr int BPW = 64 / F::LPB;
+    float acc = 0.0f;
+#pragma unroll
+    for (int s = 0; s < SPL; s++) {
+        const int b = gi + BPW * s;
+        if (b < KB) {
+            typename F::Act xa;
+            F::load_act(s_qs, qstride, s_d, s_bs, b, c, xa);
+            int isum, msum;
+            float dw, dmw;
+            F::dot(r[s], xa, c, isum, msum, dw, dmw);
+            acc = fmaf(dw * xa.d, (float)isum, acc);
+            acc = fmaf(-(dmw * xa.d), (float)msum, acc);
+        }
+    }
+    return dpp_wave_sum(acc);
+}
+
 template <class F, int SPL, int WG>
 __global__ __launch_bounds__(WG) void qmv_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
                                                  float* __restrict__ y, int N, int K, int ldy) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int NW = WG / 64;
-    constexpr int BPW = 64 / F::LPB;  // blocks of one row per wavefront step
     const int m = blockIdx.y;
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int gi = lane / F::LPB, c = lane % F::LPB;
     const int KB = K / F::ELEMS;
-    const int KBa = F::ACT == GGML_Q8K ? K / QK_K : K / QK8_0;
     const size_t row_bytes = (size_t)KB * F::BYTES;
+    const ActLds lay = act_lds_layout(F::ACT, K);
     int8_t* s_qs = reinterpret_cast<int8_t*>(smem);
-    float* s_d = reinterpret_cast<float*>(smem + K);
-    int16_t* s_bs = reinterpret_cast<int16_t*>(smem + K + 4 * KBa);
+    float* s_d = reinterpret_cast<float*>(smem + lay.off_d);
+    int16_t* s_bs = reinterpret_cast<int16_t*>(smem + lay.off_bs);
     const int nw = gridDim.x * NW;
     int row = blockIdx.x * NW + w;
-
-    typename F::Raw cur[SPL > 0 ? SPL : 1];
-    if constexpr (SPL > 0) {
-        if (row < N) {
-#pragma unroll
-            for (int s = 0; s < SPL; s++) {
-                const int b = gi + BPW * s;
-                if (b < KB) F::load(W + (size_t)row * row_bytes + (size_t)b * F::BYTES, c, cur[s]);
-            }
-        }
-    }
-
     const float* xr = x + (size_t)m * K;
-    if constexpr (F::ACT == GGML_Q8K) q8k_quantize_row(xr, K, s_qs, s_d, s_bs, w, NW, lane);
-    else q8_0_quantize_row(xr, K, s_qs, s_d, w, NW, lane);
+
+    // 1. activation loads first (s_waitcnt vmcnt is in order: the quantize step
+    //    then waits for these only), 2. first weight row, 3. quantize to LDS.
+    // 256-element activation chunks of a row of SPL slots, per wavefront
+    constexpr int CHUNKS = SPL * (64 / F::LPB) * F::ELEMS / QK_K;
+    constexpr int MAXQ = (CHUNKS + NW - 1) / NW;
+    ActRowPre<MAXQ> pre;
+    act_row_load<F::ACT, NW, MAXQ>(xr, K, w, lane, pre);
+    typename F::Raw ra[SPL], rb[SPL];
+    if (row < N) qmv_load_row<F, SPL>(W, row_bytes, row, gi, c, KB, ra);
+    act_row_quantize<F::ACT, NW, MAXQ>(pre, K, s_qs, lay.qstride, s_d, s_bs, w, lane);
     __syncthreads();
 
-    if constexpr (SPL > 0) {
-        typename F::Act xa[SPL];
-#pragma unroll
-        for (int s = 0; s < SPL; s++) {
-            const int b = gi + BPW * s;
-            if (b < KB) F::load_act(s_qs, s_d, s_bs, b, c, xa[s]);
-        }
-        while (row < N) {
-            const int nrow = row + nw;
-            typename F::Raw nxt[SPL];
-            if (nrow < N) {
-#pragma unroll
-                for (int s = 0; s < SPL; s++) {
-                    const int b = gi + BPW * s;
-                    if (b < KB) F::load(W + (size_t)nrow * row_bytes + (size_t)b * F::BYTES, c, nxt[s]);
-                }
-            }
-            float acc = 0.0f;
-#pragma unroll
-            for (int s = 0; s < SPL; s++) {
-                const int b = gi + BPW * s;
-                if (b < KB) {
-                    int isum, msum;
-                    float dw, dmw;
-                    F::dot(cur[s], xa[s], c, isum, msum, dw, dmw);
-                    acc = fmaf(dw * xa[s].d, (float)isum, acc);
-                    acc = fmaf(-(dmw * xa[s].d), (float)msum, acc);
-                }
-            }
-            acc = wave_sum(acc);
-            if (lane == 0) y[(size_t)m * ldy + row] = acc;
-#pragma unroll
-            for (int s = 0; s < SPL; s++) cur[s] = nxt[s];
-            row = nrow;
-        }
-    } else {
-        for (; row < N; row += nw) {
-            const uint8_t* wr = W + (size_t)row * row_bytes;
-            float acc = 0.0f;
-            for (int b = gi; b < KB; b += BPW) {
-                typename F::Act xa;
-                typename F::Raw r;
-                F::load_act(s_qs, s_d, s_bs, b, c, xa);
-                F::load(wr + (size_t)b * F::BYTES, c, r);
-                int isum, msum;
-                float dw, dmw;
-                F::dot(r, xa, c, isum, msum, dw, dmw);
-                acc = fmaf(dw * xa.d, (float)isum, acc);
-                acc = fmaf(-(dmw * xa.d), (float)msum, acc);
-            }
-            acc = wave_sum(acc);
-            if (lane == 0) y[(size_t)m * ldy + row] = acc;
-        }
+    // Two-row ring: the next row's loads are in flight while a row is reduced.
+    // Past the last row a wave re-issues its current row (cache-resident)
+    // rather than branching around the loads.
+    while (row < N) {
+        int nrow = row + nw;
+        qmv_load_row<F, SPL>(W, row_bytes, nrow < N ? nrow : row, gi, c, KB, rb);
+        float t = qmv_row<F, SPL>(ra, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
+        if (lane == 63) y[(size_t)m * ldy + row] = t;
+        row = nrow;
+        if (row >= N) break;
+        nrow = row + nw;
+        qmv_load_row<F, SPL>(W, row_bytes, nrow < N ? nrow : row, gi, c, KB, ra);
+        t = qmv_row<F, SPL>(rb, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
+        if (lane == 63) y[(size_t)m * ldy + row] = t;
+        row = nrow;
     }
 }
 
 namespace {
 
-template <class F, int SPL, int WG>
+template <class F, int SPL>
 hipError_t launch_qmv(const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy, hipStream_t s,
                       int num_cus) {
+    constexpr int WG = qmv_wg<F, SPL>();
     constexpr int NW = WG / 64;
     static int occ = -1;  // resident workgroups per CU for this instantiation
     if (occ < 0) {
@@ -123,8 +125,7 @@ hipError_t launch_qmv(const uint8_t* w, const float* x, float* y, int M, int N, 
             o = 1;
         occ = o;
     }
-    const int kba = F::ACT == GGML_Q8K ? K / QK_K : K / QK8_0;
-    const size_t lds = (size_t)K + 4u * kba + (F::ACT == GGML_Q8K ? 32u * kba : 0u);
+    const size_t lds = (size_t)act_lds_layout(F::ACT, K).bytes;
     if (lds > 65536) return hipErrorInvalidValue;
     const int need = (N + NW - 1) / NW;
     int cap = num_cus * occ / (M > 0 ? M : 1);
@@ -140,16 +141,16 @@ hipError_t launch_fmt(const uint8_t* w, const float* x, float* y, int M, int N, 
     constexpr int BPW = 64 / F::LPB;
     const int KB = K / F::ELEMS;
     const int spl = (KB + BPW - 1) / BPW;
-    // Workgroup size by register footprint: the widest that needs no spills.
-    constexpr bool wide = sizeof(typename F::Raw) > 64;  // Q6K carries realignment dwords
     switch (spl) {
-        case 1: return launch_qmv<F, 1, 1024>(w, x, y, M, N, K, ldy, s, num_cus);
-        case 2: return launch_qmv<F, 2, wide ? 512 : 1024>(w, x, y, M, N, K, ldy, s, num_cus);
-        case 3: return launch_qmv<F, 3, 512>(w, x, y, M, N, K, ldy, s, num_cus);
-        case 4: return launch_qmv<F, 4, wide ? 256 : 512>(w, x, y, M, N, K, ldy, s, num_cus);
-        case 5: return launch_qmv<F, 5, 256>(w, x, y, M, N, K, ldy, s, num_cus);
-        case 6: return launch_qmv<F, 6, 256>(w, x, y, M, N, K, ldy, s, num_cus);
-        default: return launch_qmv<F, 0, 256>(w, x, y, M, N, K, ldy, s, num_cus);
+        case 1: return launch_qmv<F, 1>(w, x, y, M, N, K, ldy, s, num_cus);
+        case 2: return launch_qmv<F, 2>(w, x, y, M, N, K, ldy, s, num_cus);
+        case 3: return launch_qmv<F, 3>(w, x, y, M, N, K, ldy, s, num_cus);
+        case 4: return launch_qmv<F, 4>(w, x, y, M, N, K, ldy, s, num_cus);
+        case 5: return launch_qmv<F, 5>(w, x, y, M, N, K, ldy, s, num_cus);
+        case 6: return launch_qmv<F, 6>(w, x, y, M, N, K, ldy, s, num_cus);
+        case 7: return launch_qmv<F, 7>(w, x, y, M, N, K, ldy, s, num_cus);
+        case 8: return launch_qmv<F, 8>(w, x, y, M, N, K, ldy, s, num_cus);
+        default: return hipErrorInvalidValue;  // K beyond 8 slots: rejected by the host check
     }
 }
 
@@ -185,7 +186,7 @@ __global__ __launch_bounds__(64) void block_isums_kernel(const uint8_t* __restri
     if (live) {
         const int n = (int)(flat / KB), b = (int)(flat % KB);
         typename F::Act xa;
-        F::load_act(act.qs + (size_t)m * K, act.d + (size_t)m * KBa,
+        F::load_act(act.qs + (size_t)m * K, F::ACT == GGML_Q8K ? QK_K : QK8_0, act.d + (size_t)m * KBa,
                     act.bsums ? act.bsums + (size_t)m * KBa * 16 : nullptr, b, c, xa);
         typename F::Raw r;
         F::load(W + ((size_t)n * KB + b) * F::BYTES, c, r);

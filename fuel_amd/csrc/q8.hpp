@@ -18,52 +18,73 @@ struct Q8KWave {
     float d;
 };
 
-__device__ __forceinline__ Q8KWave q8k_quantize_wave(const float* __restrict__ x256, int lane) {
-    const float4 v = reinterpret_cast<const float4*>(x256)[lane];
+// Wave64 max of non-negative floats (NaN operands ignored, as fmaxf does):
+// DPP row steps leave each 16-lane row's max in its lanes, four readlanes
+// combine the rows into a wave-uniform value.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+#define FRQ_DPP_MAX(ctrl) \
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false)))
+    FRQ_DPP_MAX(0xB1);   // quad_perm [1,0,3,2]
+    FRQ_DPP_MAX(0x4E);   // quad_perm [2,3,0,1]
+    FRQ_DPP_MAX(0x141);  // row_half_mirror
+    FRQ_DPP_MAX(0x140);  // row_mirror
+#undef FRQ_DPP_MAX
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// Sum over each aligned group of 4 lanes (every lane of the group gets it).
+__device__ __forceinline__ int quad_sum(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+    return v;
+}
+
+// `v` = elements 4*lane..4*lane+3 of the superblock, already loaded.
+// The reference keeps the first element of largest |x| (strict '<' scan, so
+// NaN and 0 never win): amax = max |x| ignoring NaN, then the first lane (by
+// ballot) and first slot in it with |x| == amax supplies the signed value.
+__device__ __forceinline__ Q8KWave q8k_quantize_vals(const float4 v, int lane) {
     const float xv[4] = {v.x, v.y, v.z, v.w};
-    // First element of largest |x| (strict '<' scan: NaN and 0 never win).
-    float best = 0.0f, bval = 0.0f;
-    int bidx = 0x7fffffff;
+    float m = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float ax = fabsf(xv[i]);
-        if (best < ax) {
-            best = ax;
-            bval = xv[i];
-            bidx = 4 * lane + i;
-        }
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float ob = __shfl_xor(best, off, 64);
-        const float ov = __shfl_xor(bval, off, 64);
-        const int oi = __shfl_xor(bidx, off, 64);
-        if (ob > best || (ob == best && oi < bidx)) {
-            best = ob;
-            bval = ov;
-            bidx = oi;
-        }
-    }
+    for (int i = 0; i < 4; i++) m = fmaxf(m, fabsf(xv[i]));
+    const float amax = wave_max_nonneg(m);
     int q[4];
     float d;
-    if (best == 0.0f) {
+    if (amax == 0.0f) {
         q[0] = q[1] = q[2] = q[3] = 0;
         d = 0.0f;
     } else {
+        float mine = 0.0f;
+        bool has = false;
+#pragma unroll
+        for (int i = 3; i >= 0; i--)
+            if (fabsf(xv[i]) == amax) {
+                mine = xv[i];
+                has = true;
+            }
+        const unsigned long long ballot = __ballot(has);
+        const int first = __builtin_ctzll(ballot);
+        const float bval = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), first));
         const float iscale = -128.0f / bval;
 #pragma unroll
         for (int i = 0; i < 4; i++) q[i] = sat_i8(fminf(roundf(iscale * xv[i]), 127.0f));
         d = 1.0f / iscale;
     }
-    int s = q[0] + q[1] + q[2] + q[3];
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
     Q8KWave r;
+    r.bsum = quad_sum(q[0] + q[1] + q[2] + q[3]);
     r.packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) | ((uint32_t)(q[2] & 0xff) << 16) |
                ((uint32_t)(q[3] & 0xff) << 24);
-    r.bsum = s;
     r.d = d;
     return r;
+}
+
+__device__ __forceinline__ Q8KWave q8k_quantize_wave(const float* __restrict__ x256, int lane) {
+    return q8k_quantize_vals(reinterpret_cast<const float4*>(x256)[lane], lane);
 }
 
 // Eight 32-element blocks per wavefront: lane l owns elements 4(l%8).. of
@@ -73,15 +94,19 @@ struct Q80Wave {
     uint16_t dbits;
 };
 
-__device__ __forceinline__ Q80Wave q8_0_quantize_wave(const float* __restrict__ x32, bool live, int lane) {
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (live) v = reinterpret_cast<const float4*>(x32)[lane & 7];
+// `v` = elements 4*(lane%8).. of block lane/8 (zeros for lanes without a block).
+__device__ __forceinline__ Q80Wave q8_0_quantize_vals(const float4 v, int lane) {
     const float xv[4] = {v.x, v.y, v.z, v.w};
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) amax = fmaxf(amax, fabsf(xv[i]));
-#pragma unroll
-    for (int off = 4; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    // max over the block's 8 lanes (an aligned half of a DPP row)
+#define FRQ_DPP_MAX(ctrl) \
+    amax = fmaxf(amax, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, amax), ctrl, 0xF, 0xF, false)))
+    FRQ_DPP_MAX(0xB1);   // quad_perm [1,0,3,2]
+    FRQ_DPP_MAX(0x4E);   // quad_perm [2,3,0,1]
+    FRQ_DPP_MAX(0x141);  // row_half_mirror: lane i <-> 7-i within each 8-lane half
+#undef FRQ_DPP_MAX
     const float d = amax / 127.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
     int q[4];
@@ -94,29 +119,57 @@ __device__ __forceinline__ Q80Wave q8_0_quantize_wave(const float* __restrict__ 
     return r;
 }
 
-// Quantize one activation row x[K] into an ActView row (qs / d / bsums), with
-// the wavefronts w = 0..nw-1 of a workgroup sharing the blocks.
-__device__ __forceinline__ void q8k_quantize_row(const float* __restrict__ x, int K, int8_t* qs, float* dv,
-                                                 int16_t* bsums, int w, int nw, int lane) {
-    const int KB = K / QK_K;
-    for (int b = w; b < KB; b += nw) {
-        const Q8KWave r = q8k_quantize_wave(x + (size_t)b * QK_K, lane);
-        reinterpret_cast<uint32_t*>(qs + (size_t)b * QK_K)[lane] = r.packed;
-        if ((lane & 3) == 0) bsums[b * 16 + (lane >> 2)] = (int16_t)r.bsum;
-        if (lane == 0) dv[b] = r.d;
+__device__ __forceinline__ Q80Wave q8_0_quantize_wave(const float* __restrict__ x32, bool live, int lane) {
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live) v = reinterpret_cast<const float4*>(x32)[lane & 7];
+    return q8_0_quantize_vals(v, lane);
+}
+
+// Quantize one activation row x[K] into an ActView row (qs / d / bsums) with
+// the NW wavefronts of a workgroup.  The row is cut into 256-element chunks
+// (one Q8K superblock, or eight Q8_0 blocks); wavefront w owns chunks
+// w, w+NW, ..., at most MAXQ of them, and issues all their float4 loads
+// (act_row_load) before any arithmetic (act_row_quantize), so the whole row
+// costs one memory round trip.  The caller sizes MAXQ >= ceil(chunks / NW).
+template <int MAXQ>
+struct ActRowPre {
+    float4 v[MAXQ];
+};
+
+template <int ACT, int NW, int MAXQ>
+__device__ __forceinline__ void act_row_load(const float* __restrict__ x, int K, int w, int lane,
+                                             ActRowPre<MAXQ>& p) {
+    const int nchunks = (K + QK_K - 1) / QK_K;
+#pragma unroll
+    for (int i = 0; i < MAXQ; i++) {
+        const int ch = w + NW * i;
+        p.v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        // Q8_0 rows end on a 32-element block that may leave the last chunk short
+        const bool live = ch < nchunks && (ACT == GGML_Q8K || ch * QK_K + 4 * lane < K);
+        if (live) p.v[i] = reinterpret_cast<const float4*>(x + (size_t)ch * QK_K)[lane];
     }
 }
 
-__device__ __forceinline__ void q8_0_quantize_row(const float* __restrict__ x, int K, int8_t* qs, float* dv,
-                                                  int w, int nw, int lane) {
-    const int KB = K / QK8_0;
-    for (int c = w; c * 8 < KB; c += nw) {
-        const int blk = c * 8 + (lane >> 3);
-        const bool live = blk < KB;
-        const Q80Wave r = q8_0_quantize_wave(x + (size_t)blk * QK8_0, live, lane);
-        if (live) {
-            reinterpret_cast<uint32_t*>(qs + (size_t)blk * QK8_0)[lane & 7] = r.packed;
-            if ((lane & 7) == 0) dv[blk] = f16_to_f32(r.dbits);
+template <int ACT, int NW, int MAXQ>
+__device__ __forceinline__ void act_row_quantize(const ActRowPre<MAXQ>& p, int K, int8_t* qs, int qstride,
+                                                 float* dv, int16_t* bsums, int w, int lane) {
+    const int nchunks = (K + QK_K - 1) / QK_K;
+#pragma unroll
+    for (int i = 0; i < MAXQ; i++) {
+        const int ch = w + NW * i;
+        if (ch >= nchunks) break;
+        if constexpr (ACT == GGML_Q8K) {
+            const Q8KWave r = q8k_quantize_vals(p.v[i], lane);
+            reinterpret_cast<uint32_t*>(qs + (size_t)ch * qstride)[lane] = r.packed;
+            if ((lane & 3) == 0) bsums[ch * 16 + (lane >> 2)] = (int16_t)r.bsum;
+            if (lane == 0) dv[ch] = r.d;
+        } else {
+            const Q80Wave r = q8_0_quantize_vals(p.v[i], lane);
+            const int blk = ch * 8 + (lane >> 3);
+            if (blk < K / QK8_0) {
+                reinterpret_cast<uint32_t*>(qs + (size_t)blk * qstride)[lane & 7] = r.packed;
+                if ((lane & 7) == 0) dv[blk] = f16_to_f32(r.dbits);
+            }
         }
     }
 }
