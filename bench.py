@@ -34,6 +34,7 @@ METRIC = "Q4_K matvec GB/s (% of HBM peak) + decode tokens/s, 7B-shape, 1 MI355X
 SHAPES = [(4096, 4096), (4096, 11008), (11008, 4096), (4096, 32000)]  # (K, N)
 HBM_PEAK_GBS = 8000.0
 ROTATE_BYTES = 1.2e9
+CPU_COPIES = 4
 SEED = 20261201
 
 
@@ -44,6 +45,22 @@ def say(*a):
 def algo_bytes(k: int, n: int, type_size: int = 144, block: int = 256) -> int:
     """Algorithmic bytes of one QMatMul at M = 1: weights + f32 x + f32 y."""
     return n * (k // block) * type_size + 4 * k + 4 * n
+
+
+def copy_calibration(nbytes: int, reps: int = 3) -> None:
+    """Device-to-device copies of a known size: the reference point that
+    scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    import ctypes as C
+
+    import fuel_amd as F
+
+    dev = F.RocmDevice(0)
+    a = dev.alloc((nbytes,), np.uint8)
+    b = dev.alloc((nbytes,), np.uint8)
+    for _ in range(reps):
+        F._native.check(F.lib().frq_memcpy_dtod(dev.handle, C.c_void_p(b.ptr), C.c_void_p(a.ptr), nbytes))
+    dev.synchronize()
+    dev.close()
 
 
 def gpu_leg(steps: int, warmup: int):
@@ -140,16 +157,19 @@ def cpu_leg(target_s: float):
     mats = []
     for si, (k, n) in enumerate(SHAPES):
         w = O.quantize(O.Q4K, O.normal((n, k), SEED, 100 + si, std=0.02))
-        mats.append((O.normal((1, k), SEED, 200 + si), w))
-    for x, w in mats:
-        O.matmul(O.Q4K, x, w, avx2=True, threads=threads)
+        # rotated copies, as on the GPU: the sweep's weights exceed the host's last-level cache
+        mats.append((O.normal((1, k), SEED, 200 + si), [w] + [w.copy() for _ in range(CPU_COPIES - 1)]))
+    for x, ws in mats:
+        O.matmul(O.Q4K, x, ws[0], avx2=True, threads=threads)
     times = []
     t_end = time.time() + target_s
+    i = 0
     while time.time() < t_end or len(times) < 3:
         t = time.perf_counter()
-        for x, w in mats:
-            O.matmul(O.Q4K, x, w, avx2=True, threads=threads)
+        for x, ws in mats:
+            O.matmul(O.Q4K, x, ws[i % CPU_COPIES], avx2=True, threads=threads)
         times.append(time.perf_counter() - t)
+        i += 1
     med = float(np.median(times))
     step_bytes = sum(algo_bytes(k, n) for k, n in SHAPES)
     return {
@@ -157,7 +177,8 @@ def cpu_leg(target_s: float):
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{len(times)} sweeps of the 4-shape Q4_K M=1 QMatMul ({step_bytes / 1e6:.1f} MB each), "
+        "sample": f"{len(times)} sweeps of the 4-shape Q4_K M=1 QMatMul ({step_bytes / 1e6:.1f} MB each, "
+                  f"weights rotated over {CPU_COPIES} copies), "
                   f"median {med * 1e3:.2f} ms; oracle matmul<BlockQ4K> with the AVX2 vec_dot, "
                   f"{threads} OpenMP threads; avx2={'yes' if O.have_avx2() else 'no (scalar)'}",
     }
@@ -170,16 +191,31 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--shape", action="append", default=None,
+                    help="restrict the sweep to KxN (profiling runs); repeatable")
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="first run device copies of this size (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported "
               "(this build has no multi-GPU path; the sharding design is documented only)", file=sys.stderr)
         return 2
 
+    global SHAPES
+    if args.shape:
+        SHAPES = [tuple(int(v) for v in sh.split("x")) for sh in args.shape]
+    if args.copy_bytes:
+        copy_calibration(args.copy_bytes)
     ms_per_step, step_bytes, per_shape, rot = gpu_leg(args.steps, args.warmup)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    dom = per_shape["4096x32000"]
-    dom_bytes = algo_bytes(4096, 32000)
+    dom_key = "4096x32000" if "4096x32000" in per_shape else next(iter(per_shape))
+    dom = per_shape[dom_key]
+    dk, dn = (int(v) for v in dom_key.split("x"))
+    dom_bytes = algo_bytes(dk, dn)
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "qmv_q4k_%s_traffic.json" % dom_key)
+    if os.path.exists(tpath):  # HBM bytes per launch from the committed FETCH/WRITE_SIZE runs
+        traffic = json.load(open(tpath)).get("traffic_bytes_per_launch")
     out = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -206,14 +242,14 @@ def main() -> int:
         "decode_tokens_per_s": None,
         "roofline": {
             "bound": "hbm",
-            "kernel": "qmv_kernel<Q4K> (fused Q8K quantize + mat-vec), K=4096 N=32000, M=1",
+            "kernel": f"qmv_kernel<Q4K> (fused Q8K quantize + mat-vec), K={dk} N={dn}, M=1",
             "achieved": dom["GB_s"],
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dom["GB_s"] / HBM_PEAK_GBS, 4),
             "bytes_per_launch": dom_bytes,
             "avg_launch_us": dom["us"],
-            "traffic": None,
+            "traffic": traffic,
         },
     }
     if not args.no_cpu:
