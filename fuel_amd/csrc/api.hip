@@ -79,6 +79,10 @@ int vec_dot_type(int t) { return t == GGML_Q8_0 ? GGML_Q8_0 : GGML_Q8K; }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// From this many activation rows on, QMatMul runs as an int8-MFMA GEMM instead
+// of the fused mat-vec (which streams the weights once per row group).
+constexpr size_t MMQ_MIN_ROWS = 16;
+
 // Byte size of the quantized-activation workspace for rows x k.
 size_t act_bytes(int vt, size_t rows, size_t k) {
     const size_t kb = k / block_elems(vt);
@@ -148,6 +152,20 @@ int run_qmatmul(frq_device* dev, int t, const uint8_t* w, const float* x, size_t
     // for the k-quants (4 lanes per superblock), K <= 8 * 32 * 32 for Q8_0
     const size_t kmax = t == GGML_Q8_0 ? 8192 : 32768;
     if (k > kmax) return fail(FRQ_UNSUPPORTED, "qmatmul: k=%zu exceeds %zu for dtype %d", k, kmax, t);
+    if (rows >= MMQ_MIN_ROWS && mmq_supported(t)) {
+        // many activation rows: quantize them once, then the int8-MFMA GEMM
+        // workspace: quantized rows, then the split-K partial sums
+        const size_t abytes = align256(act_bytes(vec_dot_type(t), rows, k));
+        const size_t pelems = mmq_partial_elems((int)rows, (int)n, dev->num_cus);
+        int rc = ensure_ws(dev, abytes + pelems * sizeof(float));
+        if (rc) return rc;
+        ActView act;
+        rc = quantize_rows(dev, vec_dot_type(t), x, rows, k, nullptr, &act);
+        if (rc) return rc;
+        float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(dev->ws) + abytes);
+        HIP_TRY(launch_mmq(t, w, act, y, part, pelems, (int)rows, (int)n, (int)k, (int)n, dev->num_cus, dev->stream));
+        return FRQ_OK;
+    }
     HIP_TRY(launch_qmv(t, w, x, y, (int)rows, (int)n, (int)k, (int)n, dev->stream, dev->num_cus));
     return FRQ_OK;
 }

@@ -18,6 +18,13 @@ hipError_t launch_quantize_q8_0(const float* x, int rows, int K, ActView act, ui
 // activation quantization fused into the kernel.
 hipError_t launch_qmv(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K,
                       int ldy, hipStream_t s, int num_cus);
+// mmq.hip: int8-MFMA matmul for M >= 16 over activations already quantized
+// into the workspace (quantize_q8k), y [M, N] with row stride ldy.
+// `part` (part_elems floats, may be null) holds split-K partial sums.
+bool mmq_supported(int dtype);
+size_t mmq_partial_elems(int M, int N, int num_cus);
+hipError_t launch_mmq(int dtype, const uint8_t* w, ActView act, float* y, float* part, size_t part_elems, int M,
+                      int N, int K, int ldy, int num_cus, hipStream_t s);
 // Per-(m, n, block) integer sums, the bit-exact stage of the dot products.
 hipError_t launch_block_isums(int dtype, const uint8_t* w, ActView act, int32_t* isum,
                               int32_t* msum, int M, int N, int K, hipStream_t s);

@@ -247,3 +247,48 @@ def test_normal_matches_host_generator(dev):
     want = O.normal((3, 1000), seed=5, stream=2, std=0.02)
     ulp = np.spacing(np.abs(want).astype(np.float32))
     assert np.all(np.abs(got - want) <= ulp)
+
+
+# ---- batched / prefill: int8 MFMA path (M >= 16) ----
+
+@pytest.mark.parametrize("m", [16, 32, 128, 512])
+def test_qmatmul_q4k_mfma_rows(dev, m):
+    say("mfma q4k m", m)
+    k, n = 4096, 4096
+    wq = weights(O.Q4K, n, k)
+    x = acts(m, k)
+    want = O.matmul(O.Q4K, x, wq)
+    out = dev.alloc((m, n), np.float32)
+    F.qmatmul_f32_rocm_wrapper([dev.from_numpy(x), dev.from_numpy(as_u32(wq))], [out],
+                               F.QMatMulParams(O.Q4K, 1, m, n, k))
+    err = rel_err(out.numpy(), want)
+    say("  rel_err", err)
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("k,n", SHAPES_7B)
+def test_qmatmul_q4k_mfma_m32_7b_shapes(dev, k, n):
+    say("mfma q4k m=32", k, n)
+    wq = weights(O.Q4K, n, k)
+    x = acts(32, k)
+    want = O.matmul(O.Q4K, x, wq)
+    out = dev.alloc((32, n), np.float32)
+    F.qmatmul_f32_rocm_wrapper([dev.from_numpy(x), dev.from_numpy(as_u32(wq))], [out],
+                               F.QMatMulParams(O.Q4K, 1, 32, n, k))
+    assert rel_err(out.numpy(), want) <= TOL
+
+
+@pytest.mark.parametrize("batch,m,n,k", [(1, 40, 100, 512), (3, 17, 130, 768), (1, 200, 70, 256)])
+def test_qmatmul_q4k_mfma_ragged(dev, batch, m, n, k):
+    # row and column tails that do not fill a tile
+    wq = weights(O.Q4K, n, k)
+    x = acts(batch * m, k)
+    want = O.matmul(O.Q4K, x, wq)
+    w = dev.from_numpy(np.frombuffer(wq.tobytes() + bytes((-wq.nbytes) % 4), np.uint32))
+    # fuel's U32 weight storage needs a 4-byte multiple; pad only when n*kb*144 is not one
+    out = dev.alloc((batch, m, n), np.float32)
+    if wq.nbytes % 4:
+        pytest.skip("Q4K blocks are always a 4-byte multiple")
+    F.qmatmul_f32_rocm_wrapper([dev.from_numpy(x.reshape(batch, m, k)), w], [out],
+                               F.QMatMulParams(O.Q4K, batch, m, n, k))
+    assert rel_err(out.numpy().reshape(batch * m, n), want) <= TOL
