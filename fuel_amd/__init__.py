@@ -15,6 +15,8 @@ from .backend import (
     device_count,
     fill_normal,
     fill_random_bits,
+    moe_ffn,
+    moe_route,
     qmatmul_f32_rocm_wrapper,
     quantize_q8_0,
     quantize_q8k,
@@ -24,5 +26,6 @@ from .backend import (
 __all__ = [
     "F16", "F32", "Q4K", "Q6K", "Q8K", "Q8_0", "FuelRocmError", "LIB_PATH", "SIGNATURES", "lib",
     "QMatMulParams", "RocmDevice", "RocmQStorage", "RocmStorage", "block_isums", "block_size",
-    "device_count", "fill_normal", "fill_random_bits", "qmatmul_f32_rocm_wrapper", "quantize_q8_0", "quantize_q8k", "type_size",
+    "device_count", "fill_normal", "fill_random_bits", "moe_ffn", "moe_route",
+    "qmatmul_f32_rocm_wrapper", "quantize_q8_0", "quantize_q8k", "type_size",
 ]

@@ -209,6 +209,33 @@ class RocmQStorage:
         check(lib().frq_qstorage_fwd(self._h, n, k, C.c_void_p(inp.ptr), m, C.c_void_p(y.ptr)))
         return y, out_shape
 
+    def indexed_moe_forward(self, self_shape: Sequence[int], inp: RocmStorage, ids: RocmStorage):
+        """mul_mat_id: self = experts [e, n, k]; input [t, 1 | topk, k] (or
+        [t, k]); ids [t, topk] int32 -> fresh output [t, topk, n] with
+        y[t, s] = W[ids[t, s]] @ x[t, s or 0]
+        (fuel-backend-contract/src/quantized.rs:82-95)."""
+        e, n, k = (int(d) for d in self_shape)
+        if inp.dtype != np.float32:
+            raise FuelRocmError(N.FRQ_UNSUPPORTED, f"indexed_moe_forward: expected f32 input, got {inp.dtype}")
+        if ids.dtype != np.int32 or len(ids.shape) != 2:
+            raise FuelRocmError(N.FRQ_INVALID, f"indexed_moe_forward: ids must be int32 [t, topk], got "
+                                               f"{ids.dtype} {ids.shape}")
+        t, topk = ids.shape
+        if len(inp.shape) == 2:
+            slots = 1
+        elif len(inp.shape) == 3:
+            slots = inp.shape[1]
+        else:
+            raise FuelRocmError(N.FRQ_INVALID, f"indexed_moe_forward: input {inp.shape} is not [t, slots, k]")
+        if inp.shape[0] != t or inp.shape[-1] != k:
+            raise FuelRocmError(N.FRQ_INVALID, f"indexed_moe_forward: input {inp.shape} incompatible with "
+                                               f"experts {tuple(self_shape)} and ids {ids.shape}")
+        out_shape = (t, topk, n)
+        y = self.dev.alloc(out_shape, np.float32)
+        check(lib().frq_indexed_moe_forward(self._h, e, n, k, C.c_void_p(inp.ptr), t, slots,
+                                            C.c_void_p(ids.ptr), topk, C.c_void_p(y.ptr)))
+        return y, out_shape
+
 
 @dataclass
 class QMatMulParams:
@@ -278,3 +305,37 @@ def block_isums(dev: RocmDevice, ggml_dtype: int, w: RocmStorage, x: RocmStorage
     check(lib().frq_block_isums(dev.handle, ggml_dtype, m, n, k, C.c_void_p(w.ptr), C.c_void_p(x.ptr),
                                 C.c_void_p(isum.ptr), C.c_void_p(msum.ptr)))
     return isum.numpy(), msum.numpy()
+
+
+def moe_route(dev: RocmDevice, logits: RocmStorage, topk: int):
+    """Top-k softmax routing and expert batches of logits [t, e] on the device
+    (lazy_nn/moe.rs:90-127, moe_routing.rs:252-275, 334-360).  Returns numpy
+    (ids [t, topk], w [t, topk], expert_offsets [e + 1], sorted_token_ids
+    [t * topk], sorted_slot [t * topk])."""
+    t, e = logits.shape
+    ids = dev.alloc((t, topk), np.int32)
+    w = dev.alloc((t, topk), np.float32)
+    offsets = dev.alloc((e + 1,), np.int32)
+    sorted_tok = dev.alloc((t * topk,), np.int32)
+    sorted_slot = dev.alloc((t * topk,), np.int32)
+    check(lib().frq_moe_route(dev.handle, C.c_void_p(logits.ptr), t, e, topk, C.c_void_p(ids.ptr),
+                              C.c_void_p(w.ptr), C.c_void_p(offsets.ptr), C.c_void_p(sorted_tok.ptr),
+                              C.c_void_p(sorted_slot.ptr)))
+    return ids.numpy(), w.numpy(), offsets.numpy(), sorted_tok.numpy(), sorted_slot.numpy()
+
+
+def moe_ffn(dev: RocmDevice, ggml_dtype: int, x: RocmStorage, logits: RocmStorage, w_gate, w_up, w_down,
+            ffn: int, topk: int, out: RocmStorage | None = None) -> RocmStorage:
+    """The quantized expert layer: route logits [t, e], SwiGLU experts over the
+    routed rows, weighted combine -> out [t, d] (lazy_nn/moe.rs:296-348).
+    w_gate / w_up / w_down: device addresses (int) or RocmQStorage of the
+    expert-major block bytes."""
+    t, d = x.shape
+    e = logits.shape[1]
+    if out is None:
+        out = dev.alloc((t, d), np.float32)
+    ptr = lambda w: w.device_ptr() if isinstance(w, RocmQStorage) else int(w)
+    check(lib().frq_moe_ffn(dev.handle, ggml_dtype, t, d, ffn, e, topk, C.c_void_p(x.ptr), C.c_void_p(logits.ptr),
+                            C.c_void_p(ptr(w_gate)), C.c_void_p(ptr(w_up)), C.c_void_p(ptr(w_down)),
+                            C.c_void_p(out.ptr)))
+    return out

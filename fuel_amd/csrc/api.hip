@@ -172,6 +172,50 @@ int run_qmatmul(frq_device* dev, int t, const uint8_t* w, const float* x, size_t
 
 bool aligned4(const void* p) { return ((uintptr_t)p & 3u) == 0; }
 
+// Largest K a mat-vec lane group covers (8 register slots per lane).
+size_t qmv_kmax(int t) { return t == GGML_Q8_0 ? 8192 : 32768; }
+
+// Indexed mat-vec over M launch rows, in launches of at most 65535 rows (the
+// grid's y limit).  With a null x_row the activation row is m / x_div, so the
+// chunks hold whole multiples of x_div rows.
+int run_indexed(frq_device* dev, int t, const uint8_t* w, const float* x, size_t M, int N, int K, float* y, int ldy,
+                QmvIndex ix) {
+    const size_t step = ix.x_row ? 65535 : (size_t)(65535 / ix.x_div) * ix.x_div;
+    for (size_t m0 = 0; m0 < M; m0 += step) {
+        const size_t rows = M - m0 < step ? M - m0 : step;
+        QmvIndex c = ix;
+        const float* xc = x;
+        c.w_sel = ix.w_sel + m0;
+        if (ix.x_row) {
+            c.x_row = ix.x_row + m0;
+        } else {
+            const size_t xo = m0 / ix.x_div * (size_t)ix.ldx;
+            xc = x + xo;
+            if (ix.x2) c.x2 = ix.x2 + xo;
+        }
+        HIP_TRY(launch_qmv_indexed(t, w, xc, y + m0 * (size_t)ldy, (int)rows, N, K, ldy, c, dev->stream, dev->num_cus));
+    }
+    return FRQ_OK;
+}
+
+int check_moe_dims(const char* who, size_t e, size_t topk) {
+    if (e == 0 || e > (size_t)MOE_MAX_EXPERTS)
+        return fail(FRQ_UNSUPPORTED, "%s: %zu experts (supported 1..%d)", who, e, MOE_MAX_EXPERTS);
+    if (topk == 0 || topk > e || topk > (size_t)MOE_MAX_TOPK)
+        return fail(FRQ_INVALID, "%s: topk=%zu must be in 1..min(experts=%zu, %d)", who, topk, e, MOE_MAX_TOPK);
+    return FRQ_OK;
+}
+
+// Routing + expert batches into caller buffers; entry_expert / entry_pos are
+// device scratch of t * topk ints.
+int route_and_batch(frq_device* dev, const float* logits, size_t t, size_t e, size_t topk, int* ids, float* w,
+                    int* offsets, int* sorted_token, int* sorted_slot, int* entry_expert, int* entry_pos) {
+    HIP_TRY(launch_moe_route(logits, (int)t, (int)e, (int)topk, ids, w, dev->stream));
+    HIP_TRY(launch_moe_batches(ids, (int)(t * topk), (int)e, (int)topk, offsets, sorted_token, sorted_slot,
+                               entry_expert, entry_pos, dev->stream));
+    return FRQ_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -486,6 +530,127 @@ int frq_block_isums(frq_device* dev, int t, size_t m, size_t n, size_t k, const 
     rc = quantize_rows(dev, vec_dot_type(t), x, m, k, nullptr, &act);
     if (rc) return rc;
     HIP_TRY(launch_block_isums(t, (const uint8_t*)w, act, isum, msum, (int)m, (int)n, (int)k, dev->stream));
+    return FRQ_OK;
+}
+
+// ---- MoE ----
+
+int frq_moe_route(frq_device* dev, const float* logits, size_t t, size_t e, size_t topk, int32_t* ids, float* w,
+                  int32_t* offsets, int32_t* sorted_token, int32_t* sorted_slot) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if ((rc = check_moe_dims("moe_route", e, topk))) return rc;
+    if (t * topk > (size_t)0x7fffffff) return fail(FRQ_UNSUPPORTED, "moe_route: t=%zu too large", t);
+    if (!logits || !ids || !w || !offsets || !sorted_token) return fail(FRQ_INVALID, "moe_route: null buffer");
+    if (t == 0) {
+        HIP_TRY(hipMemsetAsync(offsets, 0, (e + 1) * sizeof(int32_t), dev->stream));
+        return FRQ_OK;
+    }
+    const size_t p = t * topk;
+    if ((rc = ensure_ws(dev, 2 * align256(p * sizeof(int))))) return rc;
+    int* entry_expert = static_cast<int*>(dev->ws);
+    int* entry_pos = reinterpret_cast<int*>(static_cast<uint8_t*>(dev->ws) + align256(p * sizeof(int)));
+    return route_and_batch(dev, logits, t, e, topk, ids, w, offsets, sorted_token, sorted_slot, entry_expert,
+                           entry_pos);
+}
+
+int frq_indexed_moe_forward(const frq_qstorage* q, size_t e, size_t n, size_t k, const float* x, size_t t,
+                            size_t x_slots, const int32_t* ids, size_t topk, float* y) {
+    if (!q) return fail(FRQ_INVALID, "null storage");
+    int rc = use_device(q->dev);
+    if (rc) return rc;
+    const int dt = q->dtype;
+    if (!is_weight_type(dt)) return fail(FRQ_UNSUPPORTED, "indexed_moe_forward: dtype %d", dt);
+    if (k % block_elems(dt))
+        return fail(FRQ_INVALID, "indexed_moe_forward: k=%zu is not a multiple of %zu", k, block_elems(dt));
+    const size_t expert_bytes = n * (k / block_elems(dt)) * type_size(dt);
+    if (e * expert_bytes != q->nbytes)
+        return fail(FRQ_INVALID, "indexed_moe_forward: shape [%zu, %zu, %zu] does not match %zu storage bytes", e, n,
+                    k, q->nbytes);
+    if (topk == 0 || topk > 65535) return fail(FRQ_INVALID, "indexed_moe_forward: topk=%zu", topk);
+    if (x_slots != 1 && x_slots != topk)
+        return fail(FRQ_INVALID, "indexed_moe_forward: input has %zu rows per token, expected 1 or topk=%zu", x_slots,
+                    topk);
+    if (k > qmv_kmax(dt)) return fail(FRQ_UNSUPPORTED, "indexed_moe_forward: k=%zu exceeds %zu", k, qmv_kmax(dt));
+    if (n > (size_t)0x7fffffff || t * topk > (size_t)0x7fffffff || e > (size_t)0x7fffffff)
+        return fail(FRQ_UNSUPPORTED, "indexed_moe_forward: sizes exceed the launch limits");
+    if (t == 0 || n == 0) return FRQ_OK;
+    if (!x || !ids || !y) return fail(FRQ_INVALID, "indexed_moe_forward: null buffer");
+    if (!aligned4(x) || !aligned4(y)) return fail(FRQ_MISALIGNED, "indexed_moe_forward: f32 buffers not 4-byte aligned");
+    QmvIndex ix{};
+    ix.x_row = nullptr;
+    ix.x_div = x_slots == 1 ? (int)topk : 1;
+    ix.ldx = (int)k;
+    ix.w_sel = ids;
+    ix.n_experts = (int)e;
+    ix.expert_bytes = expert_bytes;
+    return run_indexed(q->dev, dt, q->d_ptr, x, t * topk, (int)n, (int)k, y, (int)n, ix);
+}
+
+int frq_moe_ffn(frq_device* dev, int dt, size_t t, size_t d, size_t ffn, size_t e, size_t topk, const float* x,
+                const float* logits, const void* w_gate, const void* w_up, const void* w_down, float* out) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (!is_weight_type(dt)) return fail(FRQ_UNSUPPORTED, "moe_ffn: dtype %d", dt);
+    if ((rc = check_moe_dims("moe_ffn", e, topk))) return rc;
+    const size_t bs = block_elems(dt);
+    if (d % bs || ffn % bs || d == 0 || ffn == 0)
+        return fail(FRQ_INVALID, "moe_ffn: d=%zu and ffn=%zu must be positive multiples of %zu", d, ffn, bs);
+    if (d > qmv_kmax(dt) || ffn > qmv_kmax(dt))
+        return fail(FRQ_UNSUPPORTED, "moe_ffn: d=%zu / ffn=%zu exceed %zu", d, ffn, qmv_kmax(dt));
+    if (t * topk > (size_t)0x7fffffff / (2 * ffn > d ? 2 * ffn : d))
+        return fail(FRQ_UNSUPPORTED, "moe_ffn: t=%zu too large", t);
+    if (t == 0) return FRQ_OK;
+    if (!x || !logits || !w_gate || !w_up || !w_down || !out) return fail(FRQ_INVALID, "moe_ffn: null buffer");
+    if (!aligned4(x) || !aligned4(out) || !aligned4(logits))
+        return fail(FRQ_MISALIGNED, "moe_ffn: f32 buffers not 4-byte aligned");
+    const size_t p = t * topk;
+    // workspace: ids, w, offsets, sorted token, entry expert, entry position,
+    // gate|up outputs [p, 2 ffn], down outputs [p, d]
+    const size_t ib = align256(p * sizeof(int));
+    const size_t ob = align256((e + 1) * sizeof(int));
+    const size_t gub = align256(p * 2 * ffn * sizeof(float));
+    const size_t ydb = align256(p * d * sizeof(float));
+    if ((rc = ensure_ws(dev, 5 * ib + ob + gub + ydb))) return rc;
+    uint8_t* b = static_cast<uint8_t*>(dev->ws);
+    int* ids = reinterpret_cast<int*>(b);
+    float* wts = reinterpret_cast<float*>(b + ib);
+    int* sorted_token = reinterpret_cast<int*>(b + 2 * ib);
+    int* entry_expert = reinterpret_cast<int*>(b + 3 * ib);
+    int* entry_pos = reinterpret_cast<int*>(b + 4 * ib);
+    int* offsets = reinterpret_cast<int*>(b + 5 * ib);
+    float* gu = reinterpret_cast<float*>(b + 5 * ib + ob);
+    float* yd = reinterpret_cast<float*>(b + 5 * ib + ob + gub);
+    if ((rc = route_and_batch(dev, logits, t, e, topk, ids, wts, offsets, sorted_token, nullptr, entry_expert,
+                              entry_pos)))
+        return rc;
+    const size_t gate_bytes = ffn * (d / bs) * type_size(dt);
+    const size_t down_bytes = d * (ffn / bs) * type_size(dt);
+    // gate | up in one launch over the sorted entries: gu[p] = [gate(x) | up(x)]
+    QmvIndex gi{};
+    gi.x_row = sorted_token;
+    gi.x_div = 1;
+    gi.ldx = (int)d;
+    gi.w_sel = entry_expert;
+    gi.n_experts = (int)e;
+    gi.expert_bytes = gate_bytes;
+    gi.w2 = static_cast<const uint8_t*>(w_up);
+    gi.n_split = (int)ffn;
+    if ((rc = run_indexed(dev, dt, static_cast<const uint8_t*>(w_gate), x, p, (int)(2 * ffn), (int)d, gu,
+                          (int)(2 * ffn), gi)))
+        return rc;
+    // down over silu(gate) * up, quantized inside the mat-vec
+    QmvIndex di{};
+    di.x_row = nullptr;
+    di.x_div = 1;
+    di.ldx = (int)(2 * ffn);
+    di.w_sel = entry_expert;
+    di.n_experts = (int)e;
+    di.expert_bytes = down_bytes;
+    di.x2 = gu + ffn;
+    if ((rc = run_indexed(dev, dt, static_cast<const uint8_t*>(w_down), gu, p, (int)d, (int)ffn, yd, (int)d, di)))
+        return rc;
+    HIP_TRY(launch_moe_combine(yd, ids, wts, entry_pos, (int)t, (int)topk, (int)d, out, dev->stream));
     return FRQ_OK;
 }
 

@@ -18,6 +18,40 @@ hipError_t launch_quantize_q8_0(const float* x, int rows, int K, ActView act, ui
 // activation quantization fused into the kernel.
 hipError_t launch_qmv(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K,
                       int ldy, hipStream_t s, int num_cus);
+
+// Indexed mat-vec (MoE mul_mat_id): launch row m reads activation row
+// x_row[m] (or m / x_div when x_row is null; stride ldx floats) and the
+// weights of expert w_sel[m] (expert_bytes apart; an id outside
+// [0, n_experts) yields a NaN output row and reads no weights).  Output rows
+// n >= n_split come from W2 instead of W (gate|up in one launch); with x2 set
+// the activation is silu(x) * x2, the SwiGLU input of the down projection
+// (x2 indexed like x).
+struct QmvIndex {
+    const int* x_row;
+    int x_div;
+    int ldx;
+    const int* w_sel;
+    int n_experts;
+    size_t expert_bytes;
+    const uint8_t* w2;
+    int n_split;
+    const float* x2;
+};
+hipError_t launch_qmv_indexed(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
+                              const QmvIndex& ix, hipStream_t s, int num_cus);
+
+// moe.hip: top-k softmax routing of logits [T, E] (ids/w [T, topk]), the
+// expert batches of the routed entries (counting sort: expert_offsets [E+1],
+// per sorted position the token, the flat (token, slot) entry and the expert,
+// per entry its sorted position), and the combine of the per-position expert
+// outputs yd [P, d] back onto the tokens in ascending expert order.
+constexpr int MOE_MAX_EXPERTS = 1024;
+constexpr int MOE_MAX_TOPK = 64;
+hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int* ids, float* w, hipStream_t s);
+hipError_t launch_moe_batches(const int* ids, int P, int E, int topk, int* offsets, int* sorted_token,
+                              int* sorted_slot, int* entry_expert, int* entry_pos, hipStream_t s);
+hipError_t launch_moe_combine(const float* yd, const int* ids, const float* w, const int* entry_pos, int T, int topk,
+                              int d, float* out, hipStream_t s);
 // mmq.hip: int8-MFMA matmul for M >= 16 over activations already quantized
 // into the workspace (quantize_q8k), y [M, N] with row stride ldy.
 // `part` (part_elems floats, may be null) holds split-K partial sums.

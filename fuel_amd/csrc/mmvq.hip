@@ -30,13 +30,13 @@ constexpr int qmv_wg() {
 }
 
 template <class F, int SPL>
-__device__ __forceinline__ void qmv_load_row(const uint8_t* __restrict__ W, size_t row_bytes, int row, int gi, int c,
-                                             int KB, typename F::Raw (&r)[SPL]) {
+__device__ __forceinline__ void qmv_load_row(const uint8_t* __restrict__ wr, int gi, int c, int KB,
+                                             typename F::Raw (&r)[SPL]) {
     constexpr int BPW = 64 / F::LPB;
 #pragma unroll
     for (int s = 0; s < SPL; s++) {
         const int b = gi + BPW * s;
-        if (b < KB) F::load(W + (size_t)row * row_bytes + (size_t)b * F::BYTES, c, r[s]);
+        if (b < KB) F::load(wr + (size_t)b * F::BYTES, c, r[s]);
     }
 }
 
@@ -63,9 +63,9 @@ __device__ __forceinline__ float qmv_row(const typename F::Raw (&r)[SPL], const 
     return dpp_wave_sum(acc);
 }
 
-template <class F, int SPL, int WG>
+template <class F, int SPL, int WG, bool IDX>
 __global__ __launch_bounds__(WG) void qmv_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
-                                                 float* __restrict__ y, int N, int K, int ldy) {
+                                                 float* __restrict__ y, int N, int K, int ldy, QmvIndex ix) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int NW = WG / 64;
     const int m = blockIdx.y;
@@ -80,6 +80,26 @@ __global__ __launch_bounds__(WG) void qmv_kernel(const uint8_t* __restrict__ W, 
     const int nw = gridDim.x * NW;
     int row = blockIdx.x * NW + w;
     const float* xr = x + (size_t)m * K;
+    const uint8_t* W2 = W;
+    int n_split = N;
+    const float* xr2 = nullptr;
+    if constexpr (IDX) {  // MoE: gathered activation row, per-row expert, optional second matrix
+        const int sel = ix.w_sel[m];
+        if ((unsigned)sel >= (unsigned)ix.n_experts) {  // uniform over the workgroup
+            for (int r = blockIdx.x * WG + threadIdx.x; r < N; r += gridDim.x * WG)
+                y[(size_t)m * ldy + r] = __builtin_nanf("");
+            return;
+        }
+        const size_t xo = (size_t)(ix.x_row ? ix.x_row[m] : m / ix.x_div) * ix.ldx;
+        xr = x + xo;
+        if (ix.x2) xr2 = ix.x2 + xo;
+        const size_t eoff = (size_t)sel * ix.expert_bytes;
+        W += eoff;
+        if (ix.w2) {
+            W2 = ix.w2 + eoff;
+            n_split = ix.n_split;
+        }
+    }
 
     // 1. activation loads first (s_waitcnt vmcnt is in order: the quantize step
     //    then waits for these only), 2. first weight row, 3. quantize to LDS.
@@ -87,9 +107,12 @@ __global__ __launch_bounds__(WG) void qmv_kernel(const uint8_t* __restrict__ W, 
     constexpr int CHUNKS = SPL * (64 / F::LPB) * F::ELEMS / QK_K;
     constexpr int MAXQ = (CHUNKS + NW - 1) / NW;
     ActRowPre<MAXQ> pre;
-    act_row_load<F::ACT, NW, MAXQ>(xr, K, w, lane, pre);
+    if (IDX && xr2) act_row_load_swiglu<F::ACT, NW, MAXQ>(xr, xr2, K, w, lane, pre);
+    else act_row_load<F::ACT, NW, MAXQ>(xr, K, w, lane, pre);
+    // rows >= n_split live in the second matrix (row - n_split)
+    auto wrow = [&](int r) { return r < n_split ? W + (size_t)r * row_bytes : W2 + (size_t)(r - n_split) * row_bytes; };
     typename F::Raw ra[SPL], rb[SPL];
-    if (row < N) qmv_load_row<F, SPL>(W, row_bytes, row, gi, c, KB, ra);
+    if (row < N) qmv_load_row<F, SPL>(wrow(row), gi, c, KB, ra);
     act_row_quantize<F::ACT, NW, MAXQ>(pre, K, s_qs, lay.qstride, s_d, s_bs, w, lane);
     __syncthreads();
 
@@ -98,13 +121,13 @@ __global__ __launch_bounds__(WG) void qmv_kernel(const uint8_t* __restrict__ W, 
     // rather than branching around the loads.
     while (row < N) {
         int nrow = row + nw;
-        qmv_load_row<F, SPL>(W, row_bytes, nrow < N ? nrow : row, gi, c, KB, rb);
+        qmv_load_row<F, SPL>(wrow(nrow < N ? nrow : row), gi, c, KB, rb);
         float t = qmv_row<F, SPL>(ra, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
         if (lane == 63) y[(size_t)m * ldy + row] = t;
         row = nrow;
         if (row >= N) break;
         nrow = row + nw;
-        qmv_load_row<F, SPL>(W, row_bytes, nrow < N ? nrow : row, gi, c, KB, ra);
+        qmv_load_row<F, SPL>(wrow(nrow < N ? nrow : row), gi, c, KB, ra);
         t = qmv_row<F, SPL>(rb, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
         if (lane == 63) y[(size_t)m * ldy + row] = t;
         row = nrow;
@@ -113,15 +136,16 @@ __global__ __launch_bounds__(WG) void qmv_kernel(const uint8_t* __restrict__ W, 
 
 namespace {
 
-template <class F, int SPL>
-hipError_t launch_qmv(const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy, hipStream_t s,
-                      int num_cus) {
+template <class F, int SPL, bool IDX>
+hipError_t launch_qmv(const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy, const QmvIndex& ix,
+                      hipStream_t s, int num_cus) {
     constexpr int WG = qmv_wg<F, SPL>();
     constexpr int NW = WG / 64;
     static int occ = -1;  // resident workgroups per CU for this instantiation
     if (occ < 0) {
         int o = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, qmv_kernel<F, SPL, WG>, WG, 16384) != hipSuccess || o < 1)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, qmv_kernel<F, SPL, WG, IDX>, WG, 16384) != hipSuccess ||
+            o < 1)
             o = 1;
         occ = o;
     }
@@ -131,26 +155,37 @@ hipError_t launch_qmv(const uint8_t* w, const float* x, float* y, int M, int N, 
     int cap = num_cus * occ / (M > 0 ? M : 1);
     if (cap < 1) cap = 1;
     const int gx = need < cap ? need : cap;
-    hipLaunchKernelGGL((qmv_kernel<F, SPL, WG>), dim3(gx, M), dim3(WG), lds, s, w, x, y, N, K, ldy);
+    hipLaunchKernelGGL((qmv_kernel<F, SPL, WG, IDX>), dim3(gx, M), dim3(WG), lds, s, w, x, y, N, K, ldy, ix);
     return hipGetLastError();
 }
 
-template <class F>
-hipError_t launch_fmt(const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy, hipStream_t s,
-                      int num_cus) {
+template <class F, bool IDX>
+hipError_t launch_fmt(const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy, const QmvIndex& ix,
+                      hipStream_t s, int num_cus) {
     constexpr int BPW = 64 / F::LPB;
     const int KB = K / F::ELEMS;
     const int spl = (KB + BPW - 1) / BPW;
     switch (spl) {
-        case 1: return launch_qmv<F, 1>(w, x, y, M, N, K, ldy, s, num_cus);
-        case 2: return launch_qmv<F, 2>(w, x, y, M, N, K, ldy, s, num_cus);
-        case 3: return launch_qmv<F, 3>(w, x, y, M, N, K, ldy, s, num_cus);
-        case 4: return launch_qmv<F, 4>(w, x, y, M, N, K, ldy, s, num_cus);
-        case 5: return launch_qmv<F, 5>(w, x, y, M, N, K, ldy, s, num_cus);
-        case 6: return launch_qmv<F, 6>(w, x, y, M, N, K, ldy, s, num_cus);
-        case 7: return launch_qmv<F, 7>(w, x, y, M, N, K, ldy, s, num_cus);
-        case 8: return launch_qmv<F, 8>(w, x, y, M, N, K, ldy, s, num_cus);
+        case 1: return launch_qmv<F, 1, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        case 2: return launch_qmv<F, 2, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        case 3: return launch_qmv<F, 3, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        case 4: return launch_qmv<F, 4, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        case 5: return launch_qmv<F, 5, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        case 6: return launch_qmv<F, 6, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        case 7: return launch_qmv<F, 7, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        case 8: return launch_qmv<F, 8, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
         default: return hipErrorInvalidValue;  // K beyond 8 slots: rejected by the host check
+    }
+}
+
+template <bool IDX>
+hipError_t launch_dtype(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
+                        const QmvIndex& ix, hipStream_t s, int num_cus) {
+    switch (dtype) {
+        case GGML_Q4K: return launch_fmt<Q4K, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        case GGML_Q6K: return launch_fmt<Q6K, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        case GGML_Q8_0: return launch_fmt<Q80, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        default: return hipErrorInvalidValue;
     }
 }
 
@@ -158,12 +193,12 @@ hipError_t launch_fmt(const uint8_t* w, const float* x, float* y, int M, int N, 
 
 hipError_t launch_qmv(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
                       hipStream_t s, int num_cus) {
-    switch (dtype) {
-        case GGML_Q4K: return launch_fmt<Q4K>(w, x, y, M, N, K, ldy, s, num_cus);
-        case GGML_Q6K: return launch_fmt<Q6K>(w, x, y, M, N, K, ldy, s, num_cus);
-        case GGML_Q8_0: return launch_fmt<Q80>(w, x, y, M, N, K, ldy, s, num_cus);
-        default: return hipErrorInvalidValue;
-    }
+    return launch_dtype<false>(dtype, w, x, y, M, N, K, ldy, QmvIndex{}, s, num_cus);
+}
+
+hipError_t launch_qmv_indexed(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
+                              const QmvIndex& ix, hipStream_t s, int num_cus) {
+    return launch_dtype<true>(dtype, w, x, y, M, N, K, ldy, ix, s, num_cus);
 }
 
 // ------------------------------------------------------------------------

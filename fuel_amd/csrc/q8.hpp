@@ -150,6 +150,25 @@ __device__ __forceinline__ void act_row_load(const float* __restrict__ x, int K,
     }
 }
 
+// SwiGLU input: silu(g) * u = g / (1 + exp(-g)) * u, element by element in the
+// order of fuel's SiLU (byte_kernels.rs silu: x / (1 + (-x).exp())).
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
+template <int ACT, int NW, int MAXQ>
+__device__ __forceinline__ void act_row_load_swiglu(const float* __restrict__ g, const float* __restrict__ u, int K,
+                                                    int w, int lane, ActRowPre<MAXQ>& p) {
+    ActRowPre<MAXQ> pu;
+    act_row_load<ACT, NW, MAXQ>(g, K, w, lane, p);
+    act_row_load<ACT, NW, MAXQ>(u, K, w, lane, pu);
+#pragma unroll
+    for (int i = 0; i < MAXQ; i++) {
+        p.v[i].x = silu_mul(p.v[i].x, pu.v[i].x);
+        p.v[i].y = silu_mul(p.v[i].y, pu.v[i].y);
+        p.v[i].z = silu_mul(p.v[i].z, pu.v[i].z);
+        p.v[i].w = silu_mul(p.v[i].w, pu.v[i].w);
+    }
+}
+
 template <int ACT, int NW, int MAXQ>
 __device__ __forceinline__ void act_row_quantize(const ActRowPre<MAXQ>& p, int K, int8_t* qs, int qstride,
                                                  float* dv, int16_t* bsums, int w, int lane) {

@@ -124,6 +124,39 @@ int frq_qmatmul(frq_device *dev, int quant_type, size_t batch, size_t m, size_t 
                 const float *act_dev, size_t act_bytes, const uint32_t *w_dev, size_t w_bytes,
                 float *out_dev, size_t out_bytes);
 
+/* ---- MoE mul_mat_id ----
+ * Routing (LazyMoeRouter::route, fuel-core/src/lazy_nn/moe.rs:90-127;
+ * MoeRouter::top_k_softmax and build_expert_batches, fuel-inference/src/
+ * moe_routing.rs:252-275, 334-360): logits [t, e] f32 -> ids [t, topk] int32
+ * (descending logit, ties to the lower expert id), w [t, topk] f32 softmax of
+ * the picked logits, expert_offsets [e + 1], sorted_token_ids [t * topk]
+ * (experts ascending, tokens ascending within an expert; the layout of the
+ * CUDA routed-MMVQ FFI, fuel-cuda-backend/src/quantized.rs:138-144) and
+ * sorted_slot [t * topk] (the flat entry token * topk + slot of each sorted
+ * position; NULL to skip).  e <= 1024, 1 <= topk <= min(e, 64).  Device
+ * pointers; asynchronous on the device stream. */
+int frq_moe_route(frq_device *dev, const float *logits_dev, size_t t, size_t e, size_t topk,
+                  int32_t *ids_dev, float *w_dev, int32_t *expert_offsets_dev,
+                  int32_t *sorted_token_ids_dev, int32_t *sorted_slot_dev);
+/* DynQuantizedStorage::indexed_moe_forward (fuel-backend-contract/src/
+ * quantized.rs:82-95; the CUDA override was retired, fuel-cuda-backend/src/
+ * quantized.rs:292-304): self = e experts of [n, k] blocks, expert-major;
+ * x [t, x_slots, k] f32 with x_slots 1 (one row per token) or topk; ids
+ * [t, topk] int32; y [t, topk, n] f32 with y[t][s] = W_{ids[t][s]} x[t][s or 0].
+ * An id outside [0, e) gives a NaN row. */
+int frq_indexed_moe_forward(const frq_qstorage *experts, size_t e, size_t n, size_t k,
+                            const float *x_dev, size_t t, size_t x_slots, const int32_t *ids_dev,
+                            size_t topk, float *y_dev);
+/* The quantized expert layer (LazyMoeLayer::forward, lazy_nn/moe.rs:296-348):
+ * route logits [t, e] as frq_moe_route, then for every expert
+ * y_e = down(silu(gate(x_sel)) * up(x_sel)) over its routed rows and
+ * out[t] = sum of w_{t,e} * y_e[t] in ascending expert order.  w_gate and
+ * w_up hold e experts of [ffn, d] blocks, w_down e experts of [d, ffn] blocks
+ * (ggml_dtype, expert-major); x [t, d] f32, out [t, d] f32. */
+int frq_moe_ffn(frq_device *dev, int ggml_dtype, size_t t, size_t d, size_t ffn, size_t e, size_t topk,
+                const float *x_dev, const float *logits_dev, const void *w_gate_dev, const void *w_up_dev,
+                const void *w_down_dev, float *out_dev);
+
 /* ---- integer taps (build-internal parity probes; no reference counterpart) ----
  * Quantize rows of f32 activations into fuel's activation blocks
  * (BlockQ8K::from_float k_quants.rs:2230-2267, BlockQ8_0::from_float
