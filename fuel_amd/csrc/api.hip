@@ -209,12 +209,18 @@ int check_moe_dims(const char* who, size_t e, size_t topk) {
 // Routing + expert batches into caller buffers; entry_expert / entry_pos are
 // device scratch of t * topk ints.
 int route_and_batch(frq_device* dev, const float* logits, size_t t, size_t e, size_t topk, int* ids, float* w,
-                    int* offsets, int* sorted_token, int* sorted_slot, int* entry_expert, int* entry_pos) {
+                    int* offsets, int* sorted_token, int* sorted_slot, int* entry_expert, int* entry_pos,
+                    const MoeTiles& tiles = MoeTiles{}) {
     HIP_TRY(launch_moe_route(logits, (int)t, (int)e, (int)topk, ids, w, dev->stream));
     HIP_TRY(launch_moe_batches(ids, (int)(t * topk), (int)e, (int)topk, offsets, sorted_token, sorted_slot,
-                               entry_expert, entry_pos, dev->stream));
+                               entry_expert, entry_pos, tiles, dev->stream));
     return FRQ_OK;
 }
+
+// From this many routed entries per expert on average, the expert projections
+// run as grouped int8-MFMA matmuls (one weight pass per expert tile) instead
+// of one mat-vec per routed row.
+constexpr double MOE_MMQ_MIN_ROWS_PER_EXPERT = 1.0;
 
 }  // namespace
 
@@ -605,27 +611,73 @@ int frq_moe_ffn(frq_device* dev, int dt, size_t t, size_t d, size_t ffn, size_t 
     if (!aligned4(x) || !aligned4(out) || !aligned4(logits))
         return fail(FRQ_MISALIGNED, "moe_ffn: f32 buffers not 4-byte aligned");
     const size_t p = t * topk;
-    // workspace: ids, w, offsets, sorted token, entry expert, entry position,
-    // gate|up outputs [p, 2 ffn], down outputs [p, d]
+    const bool grouped = mmq_supported(dt) && (double)p >= MOE_MMQ_MIN_ROWS_PER_EXPERT * (double)e;
+    const int bm = mmq_group_rows((int)(p / e));
+    const size_t max_tiles = grouped ? (p + bm - 1) / bm + e : 0;
+    // workspace: ids, w, sorted token, entry expert, entry position, offsets,
+    // tile table, gate|up outputs [p, 2 ffn], down outputs [p, d], and for the
+    // grouped path the quantized x [t, d] and silu(gate) * up [p, ffn] rows
     const size_t ib = align256(p * sizeof(int));
     const size_t ob = align256((e + 1) * sizeof(int));
+    const size_t tb = align256((max_tiles + 1) * sizeof(int));
     const size_t gub = align256(p * 2 * ffn * sizeof(float));
     const size_t ydb = align256(p * d * sizeof(float));
-    if ((rc = ensure_ws(dev, 5 * ib + ob + gub + ydb))) return rc;
+    const size_t axb = grouped ? align256(act_bytes(GGML_Q8K, t, d)) : 0;
+    const size_t ahb = grouped ? align256(act_bytes(GGML_Q8K, p, ffn)) : 0;
+    if ((rc = ensure_ws(dev, 5 * ib + ob + 3 * tb + gub + ydb + axb + ahb))) return rc;
     uint8_t* b = static_cast<uint8_t*>(dev->ws);
-    int* ids = reinterpret_cast<int*>(b);
-    float* wts = reinterpret_cast<float*>(b + ib);
-    int* sorted_token = reinterpret_cast<int*>(b + 2 * ib);
-    int* entry_expert = reinterpret_cast<int*>(b + 3 * ib);
-    int* entry_pos = reinterpret_cast<int*>(b + 4 * ib);
-    int* offsets = reinterpret_cast<int*>(b + 5 * ib);
-    float* gu = reinterpret_cast<float*>(b + 5 * ib + ob);
-    float* yd = reinterpret_cast<float*>(b + 5 * ib + ob + gub);
+    auto carve = [&b](size_t n) {
+        uint8_t* r = b;
+        b += n;
+        return r;
+    };
+    int* ids = reinterpret_cast<int*>(carve(ib));
+    float* wts = reinterpret_cast<float*>(carve(ib));
+    int* sorted_token = reinterpret_cast<int*>(carve(ib));
+    int* entry_expert = reinterpret_cast<int*>(carve(ib));
+    int* entry_pos = reinterpret_cast<int*>(carve(ib));
+    int* offsets = reinterpret_cast<int*>(carve(ob));
+    MoeTiles tiles{};
+    tiles.bm = grouped ? bm : 0;
+    tiles.tile_expert = reinterpret_cast<int*>(carve(tb));
+    tiles.tile_row0 = reinterpret_cast<int*>(carve(tb));
+    tiles.ntiles = reinterpret_cast<int*>(carve(tb));
+    float* gu = reinterpret_cast<float*>(carve(gub));
+    float* yd = reinterpret_cast<float*>(carve(ydb));
+    void* ax = carve(axb);
+    void* ah = carve(ahb);
     if ((rc = route_and_batch(dev, logits, t, e, topk, ids, wts, offsets, sorted_token, nullptr, entry_expert,
-                              entry_pos)))
+                              entry_pos, tiles)))
         return rc;
     const size_t gate_bytes = ffn * (d / bs) * type_size(dt);
     const size_t down_bytes = d * (ffn / bs) * type_size(dt);
+    if (grouped) {
+        // x rows quantized once; the gate|up tiles gather them by token
+        const ActView xv = act_view(ax, GGML_Q8K, t, d);
+        HIP_TRY(launch_quantize_q8k(x, (int)t, (int)d, xv, nullptr, dev->stream));
+        MmqGroup g{};
+        g.tile_expert = tiles.tile_expert;
+        g.tile_row0 = tiles.tile_row0;
+        g.ntiles = tiles.ntiles;
+        g.expert_offsets = offsets;
+        g.x_row = sorted_token;
+        g.expert_bytes = gate_bytes;
+        g.w2 = static_cast<const uint8_t*>(w_up);
+        g.n_split = (int)ffn;
+        HIP_TRY(launch_mmq_grouped(dt, static_cast<const uint8_t*>(w_gate), xv, gu, bm, (int)max_tiles,
+                                   (int)(2 * ffn), (int)d, (int)(2 * ffn), g, dev->stream));
+        // silu(gate) * up quantized per sorted row, then the down tiles
+        const ActView hv = act_view(ah, GGML_Q8K, p, ffn);
+        HIP_TRY(launch_quantize_q8k_swiglu(gu, (int)(2 * ffn), (int)p, (int)ffn, hv, dev->stream));
+        g.x_row = nullptr;
+        g.expert_bytes = down_bytes;
+        g.w2 = nullptr;
+        g.n_split = 0;
+        HIP_TRY(launch_mmq_grouped(dt, static_cast<const uint8_t*>(w_down), hv, yd, bm, (int)max_tiles, (int)d,
+                                   (int)ffn, (int)d, g, dev->stream));
+        HIP_TRY(launch_moe_combine(yd, ids, wts, entry_pos, (int)t, (int)topk, (int)d, out, dev->stream));
+        return FRQ_OK;
+    }
     // gate | up in one launch over the sorted entries: gu[p] = [gate(x) | up(x)]
     QmvIndex gi{};
     gi.x_row = sorted_token;

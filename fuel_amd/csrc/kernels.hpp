@@ -11,6 +11,8 @@ namespace frq {
 // quantize.hip
 hipError_t launch_quantize_q8k(const float* x, int rows, int K, ActView act, uint8_t* aos,
                                hipStream_t s);
+// Q8K rows of silu(g) * u with g = x[m][0, K) and u = x[m][K, 2K) (row stride ldx).
+hipError_t launch_quantize_q8k_swiglu(const float* x, int ldx, int rows, int K, ActView act, hipStream_t s);
 hipError_t launch_quantize_q8_0(const float* x, int rows, int K, ActView act, uint8_t* aos,
                                 hipStream_t s);
 
@@ -48,8 +50,18 @@ hipError_t launch_qmv_indexed(int dtype, const uint8_t* w, const float* x, float
 constexpr int MOE_MAX_EXPERTS = 1024;
 constexpr int MOE_MAX_TOPK = 64;
 hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int* ids, float* w, hipStream_t s);
+// With tile_bm > 0 the batches kernel also writes the tile table of a grouped
+// matmul: tiles of tile_bm sorted rows, expert by expert (tile_expert,
+// tile_row0, ntiles[0] = count; at most P / tile_bm + E tiles).
+struct MoeTiles {
+    int bm;
+    int* tile_expert;
+    int* tile_row0;
+    int* ntiles;
+};
 hipError_t launch_moe_batches(const int* ids, int P, int E, int topk, int* offsets, int* sorted_token,
-                              int* sorted_slot, int* entry_expert, int* entry_pos, hipStream_t s);
+                              int* sorted_slot, int* entry_expert, int* entry_pos, const MoeTiles& tiles,
+                              hipStream_t s);
 hipError_t launch_moe_combine(const float* yd, const int* ids, const float* w, const int* entry_pos, int T, int topk,
                               int d, float* out, hipStream_t s);
 // mmq.hip: int8-MFMA matmul for M >= 16 over activations already quantized
@@ -59,6 +71,24 @@ bool mmq_supported(int dtype);
 size_t mmq_partial_elems(int M, int N, int num_cus);
 hipError_t launch_mmq(int dtype, const uint8_t* w, ActView act, float* y, float* part, size_t part_elems, int M,
                       int N, int K, int ldy, int num_cus, hipStream_t s);
+
+// Grouped (MoE) int8-MFMA matmul: workgroup x takes tile x of the tile table
+// (rows [tile_row0, expert end) of one expert, up to bm of them); its weights
+// are expert e's (expert_bytes apart), columns n >= n_split read w2 instead
+// (gate|up in one launch), activation row m is x_row[m] (null: m).
+struct MmqGroup {
+    const int* tile_expert;
+    const int* tile_row0;
+    const int* ntiles;
+    const int* expert_offsets;
+    const int* x_row;
+    size_t expert_bytes;
+    const uint8_t* w2;
+    int n_split;
+};
+int mmq_group_rows(int rows_per_expert);  // tile height for an average rows-per-expert
+hipError_t launch_mmq_grouped(int dtype, const uint8_t* w, ActView act, float* y, int bm, int max_tiles, int N, int K,
+                              int ldy, const MmqGroup& g, hipStream_t s);
 // Per-(m, n, block) integer sums, the bit-exact stage of the dot products.
 hipError_t launch_block_isums(int dtype, const uint8_t* w, ActView act, int32_t* isum,
                               int32_t* msum, int M, int N, int K, hipStream_t s);

@@ -37,33 +37,32 @@ struct MmqTile {
     static constexpr int W_PT = (W_CH + NT - 1) / NT;
 };
 
-// Global -> register prefetch of one superblock's activation rows and raw weight blocks.
+// Global -> register prefetch of one superblock's activation rows and raw
+// weight blocks.  arow: this thread's activation row per chunk (-1: padding
+// row, staged as zeros); wrow: its weight row base per chunk; dxrow: the row
+// whose scale it stages (-1: none).
 template <int RT, int CT, int WM, int WN>
-__device__ __forceinline__ void mmq_fetch(const uint8_t* __restrict__ W, const ActView& act, int M, int N, int K,
-                                          int m0, int n0, int b, int tid, uint4 (&ra)[MmqTile<RT, CT, WM, WN>::A_PT],
+__device__ __forceinline__ void mmq_fetch(const ActView& act, int K, int b, int tid,
+                                          const int (&arow)[MmqTile<RT, CT, WM, WN>::A_PT],
+                                          const uint8_t* const (&wrow)[MmqTile<RT, CT, WM, WN>::W_PT], int dxrow,
+                                          uint4 (&ra)[MmqTile<RT, CT, WM, WN>::A_PT],
                                           uint4 (&rw)[MmqTile<RT, CT, WM, WN>::W_PT], float& rdx) {
     using T = MmqTile<RT, CT, WM, WN>;
     const int KB = K / QK_K;
 #pragma unroll
     for (int i = 0; i < T::A_PT; i++) {
-        const int idx = tid + i * T::NT;
-        const int r = idx >> 4, ch = idx & 15;
+        const int ch = (tid + i * T::NT) & 15;
         ra[i] = uint4{0u, 0u, 0u, 0u};
-        if (idx < T::A_CH && m0 + r < M)
-            ra[i] = *reinterpret_cast<const uint4*>(act.qs + (size_t)(m0 + r) * K + (size_t)b * QK_K + 16 * ch);
+        if (arow[i] >= 0)
+            ra[i] = *reinterpret_cast<const uint4*>(act.qs + (size_t)arow[i] * K + (size_t)b * QK_K + 16 * ch);
     }
 #pragma unroll
     for (int i = 0; i < T::W_PT; i++) {
         const int idx = tid + i * T::NT;
-        if (idx < T::W_CH) {
-            const int cidx = idx / 9, ch = idx % 9;
-            int n = n0 + cidx;
-            n = n < N ? n : N - 1;  // tail columns re-read a valid block; their outputs are dropped
-            rw[i] = *reinterpret_cast<const uint4*>(W + ((size_t)n * KB + b) * Q4K_BYTES + 16 * ch);
-        }
+        rw[i] = uint4{0u, 0u, 0u, 0u};  // (a conditionally-set array would live in scratch)
+        if (idx < T::W_CH) rw[i] = *reinterpret_cast<const uint4*>(wrow[i] + (size_t)b * Q4K_BYTES + 16 * (idx % 9));
     }
-    rdx = 0.0f;
-    if (tid < T::BM && m0 + tid < M) rdx = act.d[(size_t)(m0 + tid) * KB + b];
+    rdx = dxrow >= 0 ? act.d[(size_t)dxrow * KB + b] : 0.0f;
 }
 
 template <int RT, int CT, int WM, int WN>
@@ -87,10 +86,13 @@ __device__ __forceinline__ void mmq_stage(int8_t* s_a, uint8_t* s_w, float* s_dx
 // grid = (M tiles, N tiles, K splits).  With ksplit > 1 each workgroup sums a
 // contiguous range of superblocks into part[split][M][N]; mmq_reduce_kernel
 // adds the splits in order afterwards (deterministic).
-template <int RT, int CT, int WM, int WN>
+// GROUPED (MoE): workgroup x is tile x of the expert-sorted rows (g.tile_*);
+// its rows end at its expert's end offset, its weights are that expert's, and
+// activation row m is g.x_row[m] (gathered token rows) when x_row is set.
+template <int RT, int CT, int WM, int WN, bool GROUPED>
 __global__ __launch_bounds__(64 * WM * WN) void mmq_q4k_kernel(const uint8_t* __restrict__ W, ActView act,
                                                                float* __restrict__ y, int M, int N, int K,
-                                                               int ldy) {
+                                                               int ldy, MmqGroup g) {
     using T = MmqTile<RT, CT, WM, WN>;
     constexpr int BM = T::BM, BN = T::BN;
     __shared__ __align__(16) int8_t s_a[BM * A_STRIDE];
@@ -99,11 +101,43 @@ __global__ __launch_bounds__(64 * WM * WN) void mmq_q4k_kernel(const uint8_t* __
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
-    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+    const int n0 = blockIdx.y * BN;
     const int KB = K / QK_K;
+    const size_t row_bytes = (size_t)KB * Q4K_BYTES;
     const int nsplit = gridDim.z;
     const int b0 = (int)((long long)KB * blockIdx.z / nsplit), b1 = (int)((long long)KB * (blockIdx.z + 1) / nsplit);
     const int l16 = lane & 15, kb = lane >> 4;
+
+    int m0 = blockIdx.x * BM, mend = M, n_split = N;
+    const uint8_t* W1 = W;
+    const uint8_t* W2 = W;
+    const int* x_row = nullptr;
+    if constexpr (GROUPED) {
+        const int tile = blockIdx.x;
+        if (tile >= *g.ntiles) return;  // uniform: the tile table is shorter than the grid bound
+        const int e = g.tile_expert[tile];
+        m0 = g.tile_row0[tile];
+        mend = g.expert_offsets[e + 1];
+        W1 = W + (size_t)e * g.expert_bytes;
+        W2 = g.w2 ? g.w2 + (size_t)e * g.expert_bytes : W1;
+        if (g.w2) n_split = g.n_split;
+        x_row = g.x_row;
+    }
+    int arow[T::A_PT];
+#pragma unroll
+    for (int i = 0; i < T::A_PT; i++) {
+        const int idx = tid + i * T::NT;
+        const int m = m0 + (idx >> 4);
+        arow[i] = idx < T::A_CH && m < mend ? (x_row ? x_row[m] : m) : -1;
+    }
+    const int dxrow = tid < BM && m0 + tid < mend ? (x_row ? x_row[m0 + tid] : m0 + tid) : -1;
+    const uint8_t* wrow[T::W_PT];
+#pragma unroll
+    for (int i = 0; i < T::W_PT; i++) {
+        int n = n0 + (tid + i * T::NT) / 9;
+        n = n < N ? n : N - 1;  // tail columns re-read a valid block; their outputs are dropped
+        wrow[i] = n < n_split ? W1 + (size_t)n * row_bytes : W2 + (size_t)(n - n_split) * row_bytes;
+    }
 
     float facc[RT][CT][4];
 #pragma unroll
@@ -115,13 +149,13 @@ __global__ __launch_bounds__(64 * WM * WN) void mmq_q4k_kernel(const uint8_t* __
 
     uint4 ra[T::A_PT], rw[T::W_PT];
     float rdx;
-    if (b0 < b1) mmq_fetch<RT, CT, WM, WN>(W, act, M, N, K, m0, n0, b0, tid, ra, rw, rdx);
+    if (b0 < b1) mmq_fetch<RT, CT, WM, WN>(act, K, b0, tid, arow, wrow, dxrow, ra, rw, rdx);
 
     for (int b = b0; b < b1; b++) {
         __syncthreads();  // the previous superblock's LDS reads are done
         mmq_stage<RT, CT, WM, WN>(s_a, s_w, s_dx, tid, ra, rw, rdx);
         __syncthreads();
-        if (b + 1 < b1) mmq_fetch<RT, CT, WM, WN>(W, act, M, N, K, m0, n0, b + 1, tid, ra, rw, rdx);
+        if (b + 1 < b1) mmq_fetch<RT, CT, WM, WN>(act, K, b + 1, tid, arow, wrow, dxrow, ra, rw, rdx);
 
         v4i ia[RT][CT], ib[RT][CT], im[RT][CT];
 #pragma unroll
@@ -208,7 +242,7 @@ __global__ __launch_bounds__(64 * WM * WN) void mmq_q4k_kernel(const uint8_t* __
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int m = m0 + wm * RT * 16 + r * 16 + 4 * kb + i;
-                if (m < M && n < N) out[(size_t)m * ld + n] = facc[r][c][i];
+                if (m < mend && n < N) out[(size_t)m * ld + n] = facc[r][c][i];
             }
         }
 }
@@ -239,8 +273,8 @@ hipError_t launch_cfg(const uint8_t* w, ActView act, float* y, float* part, size
         while (ks > 1 && (size_t)ks * M * N > part_elems) ks--;
     }
     dim3 grid(mt, nt, ks);
-    hipLaunchKernelGGL((mmq_q4k_kernel<RT, CT, WM, WN>), grid, dim3(T::NT), 0, s, w, act, ks > 1 ? part : y, M, N,
-                       K, ldy);
+    hipLaunchKernelGGL((mmq_q4k_kernel<RT, CT, WM, WN, false>), grid, dim3(T::NT), 0, s, w, act, ks > 1 ? part : y,
+                       M, N, K, ldy, MmqGroup{});
     if (ks > 1) {
         const size_t total = (size_t)M * N;
         hipLaunchKernelGGL(mmq_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, y, M, N,
@@ -249,7 +283,26 @@ hipError_t launch_cfg(const uint8_t* w, ActView act, float* y, float* part, size
     return hipGetLastError();
 }
 
+template <int RT, int CT, int WM, int WN>
+hipError_t launch_grouped_cfg(const uint8_t* w, ActView act, float* y, int max_tiles, int N, int K, int ldy,
+                              const MmqGroup& g, hipStream_t s) {
+    using T = MmqTile<RT, CT, WM, WN>;
+    dim3 grid(max_tiles, (N + T::BN - 1) / T::BN, 1);
+    hipLaunchKernelGGL((mmq_q4k_kernel<RT, CT, WM, WN, true>), grid, dim3(T::NT), 0, s, w, act, y, 0, N, K, ldy, g);
+    return hipGetLastError();
+}
+
 }  // namespace
+
+int mmq_group_rows(int rows_per_expert) { return rows_per_expert >= 24 ? 32 : 16; }
+
+hipError_t launch_mmq_grouped(int dtype, const uint8_t* w, ActView act, float* y, int bm, int max_tiles, int N, int K,
+                              int ldy, const MmqGroup& g, hipStream_t s) {
+    if (dtype != GGML_Q4K || max_tiles <= 0) return max_tiles == 0 ? hipSuccess : hipErrorInvalidValue;
+    if (bm == 32) return launch_grouped_cfg<2, 1, 1, 4>(w, act, y, max_tiles, N, K, ldy, g, s);  // 32 x 64
+    if (bm == 16) return launch_grouped_cfg<1, 1, 1, 4>(w, act, y, max_tiles, N, K, ldy, g, s);  // 16 x 64
+    return hipErrorInvalidValue;
+}
 
 bool mmq_supported(int dtype) { return dtype == GGML_Q4K; }
 

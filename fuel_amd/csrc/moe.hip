@@ -112,7 +112,7 @@ __global__ __launch_bounds__(BATCH_WG) void moe_batches_kernel(const int* __rest
                                                               int* __restrict__ sorted_token,
                                                               int* __restrict__ sorted_slot,
                                                               int* __restrict__ entry_expert,
-                                                              int* __restrict__ entry_pos) {
+                                                              int* __restrict__ entry_pos, MoeTiles tiles) {
     __shared__ int off[MOE_MAX_EXPERTS];
     __shared__ int fill[MOE_MAX_EXPERTS];
     __shared__ int tot[MOE_MAX_EXPERTS];
@@ -144,6 +144,21 @@ __global__ __launch_bounds__(BATCH_WG) void moe_batches_kernel(const int* __rest
         offsets[tid] = excl;
     }
     if (tid == E - 1) offsets[E] = excl + c;
+    if (tiles.bm > 0) {  // tile table of the grouped matmul: ceil(count / bm) tiles per expert
+        const int nt = (c + tiles.bm - 1) / tiles.bm;
+        const int tincl = wave_incl_scan(nt, lane);
+        __syncthreads();  // wsum of the count scan has been read
+        if (lane == 63) wsum[wave] = tincl;
+        __syncthreads();
+        int tbase = 0;
+        for (int w = 0; w < wave; w++) tbase += wsum[w];
+        const int t0 = tbase + tincl - nt;
+        for (int j = 0; j < nt; j++) {
+            tiles.tile_expert[t0 + j] = tid;
+            tiles.tile_row0[t0 + j] = excl + j * tiles.bm;
+        }
+        if (tid == E - 1) tiles.ntiles[0] = t0 + nt;
+    }
     __syncthreads();
 
     const int chunk = 32 * wpe;
@@ -242,14 +257,15 @@ hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int* id
 }
 
 hipError_t launch_moe_batches(const int* ids, int P, int E, int topk, int* offsets, int* sorted_token,
-                              int* sorted_slot, int* entry_expert, int* entry_pos, hipStream_t s) {
+                              int* sorted_slot, int* entry_expert, int* entry_pos, const MoeTiles& tiles,
+                              hipStream_t s) {
     if (E <= 0 || E > MOE_MAX_EXPERTS || topk <= 0) return hipErrorInvalidValue;
     // words per expert per chunk: enough for all P entries when they fit
     const int need = (P + 31) / 32;
     int wpe = BATCH_WORDS / E;
     if (need < wpe) wpe = need > 0 ? need : 1;
     hipLaunchKernelGGL(moe_batches_kernel, dim3(1), dim3(BATCH_WG), 0, s, ids, P, E, topk, wpe, offsets,
-                       sorted_token, sorted_slot, entry_expert, entry_pos);
+                       sorted_token, sorted_slot, entry_expert, entry_pos, tiles);
     return hipGetLastError();
 }
 

@@ -24,6 +24,23 @@ __global__ __launch_bounds__(64) void quantize_q8k_kernel(const float* __restric
     }
 }
 
+// SwiGLU input of the down projection: rows of silu(g) * u, g and u side by
+// side in one row of stride ldx; grid = (K/256, rows).
+__global__ __launch_bounds__(64) void quantize_q8k_swiglu_kernel(const float* __restrict__ x, int ldx, int K,
+                                                                 ActView act) {
+    const int b = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
+    const int KB = K / QK_K;
+    const float* g = x + (size_t)m * ldx + (size_t)b * QK_K;
+    const float4 gv = reinterpret_cast<const float4*>(g)[lane];
+    const float4 uv = reinterpret_cast<const float4*>(g + K)[lane];
+    const float4 h = make_float4(silu_mul(gv.x, uv.x), silu_mul(gv.y, uv.y), silu_mul(gv.z, uv.z),
+                                 silu_mul(gv.w, uv.w));
+    const Q8KWave r = q8k_quantize_vals(h, lane);
+    reinterpret_cast<uint32_t*>(act.qs + (size_t)m * K + (size_t)b * QK_K)[lane] = r.packed;
+    if ((lane & 3) == 0) act.bsums[((size_t)m * KB + b) * 16 + (lane >> 2)] = (int16_t)r.bsum;
+    if (lane == 0) act.d[(size_t)m * KB + b] = r.d;
+}
+
 // Eight 32-element blocks per wavefront; grid = (ceil(K/256), rows).
 __global__ __launch_bounds__(64) void quantize_q8_0_kernel(const float* __restrict__ x, int K,
                                                            ActView act, uint8_t* __restrict__ aos) {
@@ -48,6 +65,12 @@ hipError_t launch_quantize_q8k(const float* x, int rows, int K, ActView act, uin
                                hipStream_t s) {
     dim3 grid(K / QK_K, rows);
     hipLaunchKernelGGL(quantize_q8k_kernel, grid, dim3(64), 0, s, x, K, act, aos);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_q8k_swiglu(const float* x, int ldx, int rows, int K, ActView act, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(quantize_q8k_swiglu_kernel, dim3(K / QK_K, rows), dim3(64), 0, s, x, ldx, K, act);
     return hipGetLastError();
 }
 
