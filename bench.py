@@ -14,7 +14,12 @@ kernel (the 4096x32000 Q4_K mat-vec) timed alone the same way.  `cpu_baseline`
 is the oracle's restatement of fuel's CPU path (matmul<BlockQ4K> with the AVX2
 vec_dot) on the host cores, on the same four shapes.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+The same run measures BASELINE config 4 (`decode`): greedy decode of a
+random-init LLaMA-2-7B-shaped Q4_K_M-mix decoder after a 512-token prompt,
+256 generated tokens timed, with fuel's CPU path (the oracle's restatement)
+timed on the same weights and KV state beside it (`decode.cpu_baseline`).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-decode] [--decode-only]
 """
 from __future__ import annotations
 
@@ -146,6 +151,131 @@ def gpu_leg(steps: int, warmup: int):
     return ms_per_step, step_bytes, per_shape, R
 
 
+DECODE_PROMPT = 512
+DECODE_NEW = 256
+
+
+def decode_leg(new_tokens: int = DECODE_NEW, prompt_len: int = DECODE_PROMPT):
+    """random-init LLaMA-2-7B-shaped decoder (Q4_K_M-style
+    mix), a 512-token uniform random prompt, greedy decode of `new_tokens`.
+    Every step is one replay of a captured HIP graph (194 launches); the
+    prompt is run through the same step with its tokens forced.  Timed: the
+    `new_tokens` steps that each emit a generated token."""
+    import fuel_amd as F
+    from fuel_amd.hiprt import HipRuntime
+    from fuel_amd.llama import LlamaConfig, LlamaDecoder
+
+    cfg = LlamaConfig(max_ctx=prompt_len + new_tokens)
+    hip = HipRuntime()
+    dev = F.RocmDevice(0)
+    stream = hip.stream_create()
+    dev.set_stream(stream)
+    t0 = time.time()
+    dec = LlamaDecoder(dev, cfg, seed=SEED)
+    t_build = time.time() - t0
+    bits = F.fill_random_bits(dev, prompt_len, 0, SEED, 0, 77).numpy()
+    prompt = (bits % cfg.vocab).astype(np.int32)   # uniform ids in [0, vocab)
+    dec.start(prompt)
+    hip.stream_sync(stream)
+    g = hip.capture(stream, dec.enqueue_step)
+    e0, e1 = hip.event_create(), hip.event_create()
+    dec.start(prompt)
+    hip.event_record(e0, stream)
+    for _ in range(prompt_len - 1):              # forced steps: cache rows 0 .. prompt_len-2
+        hip.graph_launch(g, stream)
+    hip.event_record(e1, stream)
+    hip.event_sync(e1)
+    prefill_ms = hip.elapsed_ms(e0, e1)
+    hip.event_record(e0, stream)
+    for _ in range(new_tokens):                  # each step emits one generated token
+        hip.graph_launch(g, stream)
+    hip.event_record(e1, stream)
+    hip.event_sync(e1)
+    decode_ms = hip.elapsed_ms(e0, e1)
+    tokens = dec.tokens_host()
+    # logits of the first generated position, recomputed eagerly for the CPU check
+    p0 = prompt_len - 1
+    dec.pos.copy_from(np.array([p0], np.int32))
+    import ctypes as C
+    F._native.check(F.lib().frq_memcpy_dtod(dev.handle, C.c_void_p(dec.x.ptr),
+                                            C.c_void_p(dec.embed.ptr + int(tokens[p0]) * cfg.dim * 4), cfg.dim * 4))
+    hip.graph_launch(g, stream)
+    hip.stream_sync(stream)
+    logits0 = dec.logits.numpy()
+    hip.graph_destroy(g)
+    wbytes = cfg.weight_bytes_per_token()
+    mean_ctx = prompt_len + (new_tokens + 1) / 2.0
+    kv_bytes = 2 * cfg.n_layers * cfg.dim * 2 * mean_ctx       # f16 K and V rows read per token
+    ms_tok = decode_ms / new_tokens
+    res = {
+        "tokens_per_s": round(new_tokens / (decode_ms * 1e-3), 1),
+        "ms_per_token": round(ms_tok, 4),
+        "prefill_ms_by_decode_steps": round(prefill_ms, 2),
+        "weight_bytes_per_token": wbytes,
+        "kv_bytes_per_token_mean": int(kv_bytes),
+        "hbm_GB_s": round((wbytes + kv_bytes) / (ms_tok * 1e-3) / 1e9, 1),
+        "launches_per_token": dec.launches_per_step(),
+        "build_s": round(t_build, 1),
+        "generated_head": tokens[prompt_len:prompt_len + 8].tolist(),
+    }
+    return res, dec, dev, tokens, logits0
+
+
+def cpu_decode_leg(dec, tokens, logits0, target_s: float, prompt_len: int = DECODE_PROMPT):
+    """fuel's CPU quantized path (oracle restatement of the decode step, AVX2
+    vec_dot) on the same weights and KV state: decode tokens/s on the host
+    cores, and the logits of the first generated position against the GPU's."""
+    import oracle as O
+    from oracle.llama import LlamaConfig as OConfig, OracleLlama
+
+    threads = int(os.environ.get("RAYON_NUM_THREADS") or os.environ.get("OMP_NUM_THREADS") or 0)
+    if threads <= 0:
+        threads = len(os.sched_getaffinity(0))
+    cfg = dec.cfg
+    wh = dec.weights_host()
+
+    def blocks(t):
+        raw, shape, dt = t
+        return np.frombuffer(raw, dtype=O.BLOCK_DTYPE[dt]).reshape(shape)
+
+    w = {"embed": wh["embed"], "final_gain": wh["final_gain"], "out": blocks(wh["out"]), "layers": []}
+    for lw in wh["layers"]:
+        w["layers"].append({k: (blocks(v) if isinstance(v, tuple) else v) for k, v in lw.items()})
+    del wh
+    ocfg = OConfig(dim=cfg.dim, n_layers=cfg.n_layers, n_heads=cfg.n_heads, head_dim=cfg.head_dim, ffn=cfg.ffn,
+                   vocab=cfg.vocab, eps=cfg.eps, rope_theta=cfg.rope_theta, max_ctx=cfg.max_ctx)
+    m = OracleLlama(ocfg, w, threads=threads)
+    p0 = prompt_len - 1
+    for li in range(cfg.n_layers):               # the GPU's cache rows 0 .. p0-1
+        kc, vc = dec.kv_host(li)
+        m.kc[li, :, :p0] = kc[:, :p0]
+        m.vc[li, :, :p0] = vc[:, :p0]
+    times = []
+    t_end = time.time() + target_s
+    pos = p0
+    logits_cpu0 = None
+    while (time.time() < t_end or len(times) < 2) and pos < cfg.max_ctx - 1:
+        t = time.perf_counter()
+        lg = m.step(int(tokens[pos]), pos)       # teacher-forced on the GPU's tokens
+        times.append(time.perf_counter() - t)
+        if logits_cpu0 is None:
+            logits_cpu0 = lg
+        pos += 1
+    med = float(np.median(times))
+    err = float(np.abs(logits0 - logits_cpu0).max() / np.linalg.norm(logits_cpu0))
+    return {
+        "value": round(1.0 / med, 3),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{len(times)} decode steps of the same 7B-shaped model at positions {p0}..{pos - 1} "
+                  f"(KV rows 0..{p0 - 1} copied from the GPU run), median {med * 1e3:.1f} ms/token; "
+                  f"oracle restatement of the decode step with matmul<T> AVX2 vec_dot, {threads} OpenMP threads",
+        "logits_rel_err_vs_gpu_first_step": err,
+        "greedy_agrees_first_step": int(np.argmax(logits_cpu0)) == int(tokens[p0 + 1]),
+    }
+
+
 def cpu_leg(target_s: float):
     """fuel's CPU quantized path (oracle restatement, AVX2 vec_dot) on the host
     cores: median time of repeated 4-shape sweeps."""
@@ -195,6 +325,8 @@ def main() -> int:
                     help="restrict the sweep to KxN (profiling runs); repeatable")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="first run device copies of this size (counter calibration)")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--decode-only", action="store_true", help="run only the config-4 decode legs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported "
@@ -206,6 +338,14 @@ def main() -> int:
         SHAPES = [tuple(int(v) for v in sh.split("x")) for sh in args.shape]
     if args.copy_bytes:
         copy_calibration(args.copy_bytes)
+    if args.decode_only:
+        dres, dec, dev, tokens, logits0 = decode_leg()
+        say(f"[bench] decode {dres}")
+        if not args.no_cpu:
+            dres["cpu_baseline"] = cpu_decode_leg(dec, tokens, logits0, args.cpu_seconds)
+        print(json.dumps({"metric": "decode tokens/s, LLaMA-2-7B-shaped Q4_K_M mix (BASELINE config 4)",
+                          "value": dres["tokens_per_s"], "unit": "tokens/s", "decode": dres}), flush=True)
+        return 0
     ms_per_step, step_bytes, per_shape, rot = gpu_leg(args.steps, args.warmup)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     dom_key = "4096x32000" if "4096x32000" in per_shape else next(iter(per_shape))
@@ -252,6 +392,15 @@ def main() -> int:
             "traffic": traffic,
         },
     }
+    if not args.no_decode:
+        dres, dec, dev, tokens, logits0 = decode_leg()
+        say(f"[bench] decode {dres}")
+        out["decode_tokens_per_s"] = dres["tokens_per_s"]
+        out["decode"] = dres
+        if not args.no_cpu:
+            dres["cpu_baseline"] = cpu_decode_leg(dec, tokens, logits0, args.cpu_seconds)
+            out["decode_cpu_tokens_per_s"] = dres["cpu_baseline"]["value"]
+        del dec, dev
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_leg(args.cpu_seconds)
     print(json.dumps(out), flush=True)

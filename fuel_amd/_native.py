@@ -69,6 +69,11 @@ SIGNATURES = {
     "frq_moe_route": (_i32, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp]),
     "frq_indexed_moe_forward": (_i32, [_vp, _sz, _sz, _sz, _vp, _sz, _sz, _vp, _sz, _vp]),
     "frq_moe_ffn": (_i32, [_vp, _i32, _sz, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "frq_qmatmul_fused": (_i32, [_vp, _i32, _sz, _sz, _sz, _vp, _vp, _sz, _vp, _vp, C.c_float, _i32, _vp, _sz]),
+    "frq_attention_decode_workspace": (_sz, [_sz, _sz]),
+    "frq_attention_decode": (_i32, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _sz,
+                                    _vp]),
+    "frq_argmax_embed": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _vp, _vp]),
     "frq_block_isums": (_i32, [_vp, _i32, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
     "frq_fill_random_bits": (_i32, [_vp, _vp, _sz, C.c_uint64, C.c_uint64, C.c_uint32, C.c_uint32]),
     "frq_fill_normal": (_i32, [_vp, _vp, _sz, C.c_uint64, C.c_uint32, C.c_float, C.c_float]),

@@ -179,11 +179,11 @@ size_t qmv_kmax(int t) { return t == GGML_Q8_0 ? 8192 : 32768; }
 // grid's y limit).  With a null x_row the activation row is m / x_div, so the
 // chunks hold whole multiples of x_div rows.
 int run_indexed(frq_device* dev, int t, const uint8_t* w, const float* x, size_t M, int N, int K, float* y, int ldy,
-                QmvIndex ix) {
+                QmvOpts ix) {
     const size_t step = ix.x_row ? 65535 : (size_t)(65535 / ix.x_div) * ix.x_div;
     for (size_t m0 = 0; m0 < M; m0 += step) {
         const size_t rows = M - m0 < step ? M - m0 : step;
-        QmvIndex c = ix;
+        QmvOpts c = ix;
         const float* xc = x;
         c.w_sel = ix.w_sel + m0;
         if (ix.x_row) {
@@ -583,7 +583,7 @@ int frq_indexed_moe_forward(const frq_qstorage* q, size_t e, size_t n, size_t k,
     if (t == 0 || n == 0) return FRQ_OK;
     if (!x || !ids || !y) return fail(FRQ_INVALID, "indexed_moe_forward: null buffer");
     if (!aligned4(x) || !aligned4(y)) return fail(FRQ_MISALIGNED, "indexed_moe_forward: f32 buffers not 4-byte aligned");
-    QmvIndex ix{};
+    QmvOpts ix{};
     ix.x_row = nullptr;
     ix.x_div = x_slots == 1 ? (int)topk : 1;
     ix.ldx = (int)k;
@@ -679,7 +679,7 @@ int frq_moe_ffn(frq_device* dev, int dt, size_t t, size_t d, size_t ffn, size_t 
         return FRQ_OK;
     }
     // gate | up in one launch over the sorted entries: gu[p] = [gate(x) | up(x)]
-    QmvIndex gi{};
+    QmvOpts gi{};
     gi.x_row = sorted_token;
     gi.x_div = 1;
     gi.ldx = (int)d;
@@ -692,7 +692,7 @@ int frq_moe_ffn(frq_device* dev, int dt, size_t t, size_t d, size_t ffn, size_t 
                           (int)(2 * ffn), gi)))
         return rc;
     // down over silu(gate) * up, quantized inside the mat-vec
-    QmvIndex di{};
+    QmvOpts di{};
     di.x_row = nullptr;
     di.x_div = 1;
     di.ldx = (int)(2 * ffn);
@@ -703,6 +703,76 @@ int frq_moe_ffn(frq_device* dev, int dt, size_t t, size_t d, size_t ffn, size_t 
     if ((rc = run_indexed(dev, dt, static_cast<const uint8_t*>(w_down), gu, p, (int)d, (int)ffn, yd, (int)d, di)))
         return rc;
     HIP_TRY(launch_moe_combine(yd, ids, wts, entry_pos, (int)t, (int)topk, (int)d, out, dev->stream));
+    return FRQ_OK;
+}
+
+// ---- decode-step fusions ----
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int frq_qmatmul_fused(frq_device* dev, int dt, size_t m, size_t n, size_t k, const void* w, const float* x, size_t ldx,
+                      const float* x2, const float* gain, float eps, int accumulate, float* y, size_t ldy) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (!is_weight_type(dt)) return fail(FRQ_UNSUPPORTED, "qmatmul_fused: dtype %d", dt);
+    if (k == 0 || k % block_elems(dt))
+        return fail(FRQ_INVALID, "qmatmul_fused: k=%zu must be a positive multiple of %zu", k, block_elems(dt));
+    if (k > qmv_kmax(dt)) return fail(FRQ_UNSUPPORTED, "qmatmul_fused: k=%zu exceeds %zu", k, qmv_kmax(dt));
+    if (m > 65535 || n > (size_t)0x7fffffff) return fail(FRQ_UNSUPPORTED, "qmatmul_fused: m=%zu n=%zu", m, n);
+    if (m == 0 || n == 0) return FRQ_OK;
+    if (!w || !x || !y) return fail(FRQ_INVALID, "qmatmul_fused: null buffer");
+    if (m > 1 && (ldx < k || ldy < n)) return fail(FRQ_INVALID, "qmatmul_fused: ldx=%zu < k or ldy=%zu < n", ldx, ldy);
+    if (ldx > (size_t)0x7fffffff || ldy > (size_t)0x7fffffff) return fail(FRQ_UNSUPPORTED, "qmatmul_fused: strides");
+    if (x2 && gain) return fail(FRQ_INVALID, "qmatmul_fused: rms_gain and x2 are exclusive");
+    if (!aligned16(x) || (x2 && !aligned16(x2)) || (gain && !aligned16(gain)) || ldx % 4)
+        return fail(FRQ_MISALIGNED, "qmatmul_fused: x, x2, gain must be 16-byte aligned and ldx %% 4 == 0");
+    if (!aligned4(y) || !aligned4(w)) return fail(FRQ_MISALIGNED, "qmatmul_fused: w / y not 4-byte aligned");
+    QmvOpts o{};
+    o.ldx = (int)ldx;
+    o.x2 = x2;
+    o.rms_gain = gain;
+    o.rms_eps = eps;
+    o.accumulate = accumulate ? 1 : 0;
+    HIP_TRY(launch_qmv_fused(dt, static_cast<const uint8_t*>(w), x, y, (int)m, (int)n, (int)k, (int)ldy, o,
+                             dev->stream, dev->num_cus));
+    return FRQ_OK;
+}
+
+size_t frq_attention_decode_workspace(size_t n_heads, size_t max_ctx) {
+    if (n_heads == 0 || n_heads > 65535 || max_ctx == 0 || max_ctx > (size_t)0x7fffffff / (n_heads * ATTN_HEAD_DIM))
+        return 0;
+    return attn_decode_work_bytes((int)n_heads, (int)max_ctx);
+}
+
+int frq_attention_decode(frq_device* dev, size_t n_heads, size_t head_dim, size_t max_ctx, const float* qk,
+                         const float* v, const float* rcos, const float* rsin, uint16_t* kc, uint16_t* vc,
+                         const int32_t* pos, float scale, void* work, size_t work_bytes, float* out) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (head_dim != (size_t)ATTN_HEAD_DIM)
+        return fail(FRQ_UNSUPPORTED, "attention_decode: head_dim=%zu (supported: %d)", head_dim, ATTN_HEAD_DIM);
+    const size_t need = frq_attention_decode_workspace(n_heads, max_ctx);
+    if (need == 0) return fail(FRQ_INVALID, "attention_decode: n_heads=%zu max_ctx=%zu", n_heads, max_ctx);
+    if (!qk || !v || !rcos || !rsin || !kc || !vc || !pos || !work || !out)
+        return fail(FRQ_INVALID, "attention_decode: null buffer");
+    if (work_bytes < need) return fail(FRQ_WORKSPACE, "attention_decode: workspace %zu < %zu bytes", work_bytes, need);
+    if (!aligned16(kc) || !aligned16(vc) || !aligned4(work))
+        return fail(FRQ_MISALIGNED, "attention_decode: caches must be 16-byte aligned, work 4-byte aligned");
+    HIP_TRY(launch_attn_decode(qk, v, rcos, rsin, kc, vc, (int)n_heads, (int)max_ctx, pos, scale,
+                               static_cast<float*>(work), out, dev->stream));
+    return FRQ_OK;
+}
+
+int frq_argmax_embed(frq_device* dev, const float* logits, size_t vocab, const float* table, size_t dim, int32_t* tokens,
+                     size_t tokens_cap, size_t prompt_len, int32_t* pos, float* x) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (vocab == 0 || vocab > (size_t)0x7fffffff || dim == 0 || dim % 4 || tokens_cap > (size_t)0x7fffffff)
+        return fail(FRQ_INVALID, "argmax_embed: vocab=%zu dim=%zu", vocab, dim);
+    if (!logits || !table || !tokens || !pos || !x) return fail(FRQ_INVALID, "argmax_embed: null buffer");
+    if (!aligned16(table) || !aligned16(x)) return fail(FRQ_MISALIGNED, "argmax_embed: table / x not 16-byte aligned");
+    const int pl = prompt_len > tokens_cap ? (int)tokens_cap : (int)prompt_len;
+    HIP_TRY(launch_argmax_embed(logits, (int)vocab, table, (int)dim, tokens, (int)tokens_cap, pl, pos, x, dev->stream));
     return FRQ_OK;
 }
 

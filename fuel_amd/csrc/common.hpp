@@ -171,4 +171,21 @@ __host__ __device__ inline ActLds act_lds_layout(int act_dtype, int K) {
     return l;
 }
 
+// First-index argmax of fuel's scans (argextremum_dim_f32, fuel-cpu-backend/
+// src/byte_kernels.rs:8178-8241: element 0 is taken unconditionally, then
+// element d replaces the best when v > best) as a max under a total order, so
+// that any reduction tree gives the scan's answer: larger key wins, equal keys
+// go to the lower index, and scan_key maps a NaN at index 0 to +inf (never
+// displaced) and any other NaN to -inf (never taken).
+__device__ __forceinline__ float scan_key(float v, int j) {
+    return v != v ? (j == 0 ? __builtin_inff() : -__builtin_inff()) : v;
+}
+
+__device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
+    if (ov > v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
+    }
+}
+
 }  // namespace frq

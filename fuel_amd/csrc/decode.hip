@@ -1,0 +1,284 @@
+// Decode-step kernels around the quantized mat-vecs of a LLaMA-shaped
+// decoder (fuel-core/src/lazy.rs:7363-7440, one token at position pos):
+//
+//   attention: RoPE of q and k (rotate-half with the f32 tables of
+//   build_rope_tables, fuel-graph/src/lib.rs:10808-10868; rope_f32,
+//   fuel-cpu-backend/src/byte_kernels.rs:1885-1964), append of k and v to an
+//   f16 KV cache, scores (q . k_j) * scale, softmax over j <= pos and the
+//   weighted sum of the values, per head.  The context is split over
+//   workgroups (flash-decoding) and a second kernel merges the splits.
+//
+//   argmax + embedding: the next token (the prompt's while it lasts, else the
+//   first-index argmax of the logits, argmax_dim_f32 byte_kernels.rs:8246),
+//   its embedding row into the residual stream, pos += 1.  Both read pos from
+//   device memory so that a captured step replays for every token.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace frq {
+
+namespace {
+
+constexpr int HD = ATTN_HEAD_DIM;
+constexpr int ATT_WG = 256;
+constexpr int GROUPS = ATT_WG / 16;  // positions in flight per workgroup (16 lanes each)
+
+// Sum over 16-lane groups (lanes l and l^8, l^4, l^2, l^1).
+__device__ __forceinline__ float group16_sum(float v) {
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+// Raw f16 x 8 chunk (one 16-byte load) to floats.
+__device__ __forceinline__ void h8_to_f(const uint4& u, float (&f)[8]) {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        f[2 * i] = __half2float(__ushort_as_half((unsigned short)(w[i] & 0xffffu)));
+        f[2 * i + 1] = __half2float(__ushort_as_half((unsigned short)(w[i] >> 16)));
+    }
+}
+
+// grid = (heads, nsplit), 256 threads.  qk = [q | k] unrotated (heads * HD
+// each), vn = v; caches are [heads][max_ctx][HD] f16.  Split sp of a head
+// takes a contiguous range of at most 16 * ATTN_NIT positions: 16 lanes per
+// position (8 dims per lane), every K and V load of the range issued before
+// any arithmetic (one memory round trip).  It writes its unnormalized output,
+// max and sum to part[head][sp]; attn_combine_kernel merges the splits (a
+// kernel boundary, not a device-scope fence, orders the two).
+__global__ __launch_bounds__(ATT_WG) void attn_split_kernel(const float* __restrict__ qk, const float* __restrict__ vn,
+                                                           const float* __restrict__ rcos,
+                                                           const float* __restrict__ rsin, __half* kc, __half* vc,
+                                                           int max_ctx, const int* __restrict__ pos_p, float scale,
+                                                           float* __restrict__ part) {
+    __shared__ float s_q[HD], s_kn[HD], s_vn[HD];
+    __shared__ float s_acc[ATT_WG / 64][HD];
+    __shared__ float s_red[ATT_WG / 64];
+    const int h = blockIdx.x, sp = blockIdx.y, H = gridDim.x, nsplit = gridDim.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = tid >> 4, l16 = tid & 15;
+    const int pos = *pos_p;
+    if (pos < 0 || pos >= max_ctx) return;  // the combine writes NaN
+    const int n = pos + 1;
+    const int chunk = (n + nsplit - 1) / nsplit;
+    const int p0 = min(n, sp * chunk), p1 = min(n, p0 + chunk);
+    const bool owner = p0 < p1 && p1 == n;  // this split holds the new position
+    const size_t cbase = (size_t)h * max_ctx * HD;
+
+    // 1. all K / V loads of the range (row pos is stale in memory; replaced below)
+    uint4 kr[ATTN_NIT], vr[ATTN_NIT];
+#pragma unroll
+    for (int it = 0; it < ATTN_NIT; it++) {
+        const int j = p0 + g + GROUPS * it;
+        kr[it] = uint4{0u, 0u, 0u, 0u};
+        vr[it] = uint4{0u, 0u, 0u, 0u};
+        if (j < p1) {
+            kr[it] = *reinterpret_cast<const uint4*>(kc + cbase + (size_t)j * HD + 8 * l16);
+            vr[it] = *reinterpret_cast<const uint4*>(vc + cbase + (size_t)j * HD + 8 * l16);
+        }
+    }
+    // 2. rope(q); in the owner split rope(k) and v, rounded to f16 and appended
+    const float* cs = rcos + (size_t)pos * HD;
+    const float* sn = rsin + (size_t)pos * HD;
+    if (tid < HD / 2) {  // out[i] = x[i] cos[i] - x[i+h] sin[i], out[i+h] = x[i+h] cos[i+h] + x[i] sin[i+h]
+        const float* q = qk + (size_t)h * HD;
+        const float lo = q[tid], hi = q[tid + HD / 2];
+        s_q[tid] = lo * cs[tid] - hi * sn[tid];
+        s_q[tid + HD / 2] = hi * cs[tid + HD / 2] + lo * sn[tid + HD / 2];
+    } else if (tid < HD && owner) {
+        const int i = tid - HD / 2;
+        const float* k = qk + (size_t)(H + h) * HD;
+        const float lo = k[i], hi = k[i + HD / 2];
+        const __half a = __float2half(lo * cs[i] - hi * sn[i]);
+        const __half b = __float2half(hi * cs[i + HD / 2] + lo * sn[i + HD / 2]);
+        kc[cbase + (size_t)pos * HD + i] = a;
+        kc[cbase + (size_t)pos * HD + i + HD / 2] = b;
+        s_kn[i] = __half2float(a);
+        s_kn[i + HD / 2] = __half2float(b);
+    } else if (tid >= HD && owner) {
+        const int i = tid - HD;
+        const __half a = __float2half(vn[(size_t)h * HD + i]);
+        vc[cbase + (size_t)pos * HD + i] = a;
+        s_vn[i] = __half2float(a);
+    }
+    __syncthreads();
+
+    // 3. scores (all 16 lanes of a group end with their position's score)
+    float q8[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) q8[e] = s_q[8 * l16 + e];
+    float sc[ATTN_NIT];
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int it = 0; it < ATTN_NIT; it++) {
+        const int j = p0 + g + GROUPS * it;
+        float kv[8];
+        h8_to_f(kr[it], kv);
+        if (owner && j == pos) {  // (s_kn / s_vn hold data only in the owner split)
+#pragma unroll
+            for (int e = 0; e < 8; e++) kv[e] = s_kn[8 * l16 + e];
+        }
+        float d = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) d = fmaf(q8[e], kv[e], d);
+        d = group16_sum(d) * scale;
+        sc[it] = j < p1 ? d : -__builtin_inff();
+        mx = fmaxf(mx, sc[it]);
+    }
+    // 4. softmax statistics of the range, weighted values
+#pragma unroll
+    for (int off = 32; off >= 16; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if (lane == 0) s_red[wave] = mx;
+    __syncthreads();
+    mx = s_red[0];
+#pragma unroll
+    for (int w = 1; w < ATT_WG / 64; w++) mx = fmaxf(mx, s_red[w]);
+    __syncthreads();
+    float l = 0.0f;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int it = 0; it < ATTN_NIT; it++) {
+        const int j = p0 + g + GROUPS * it;
+        const float p = j < p1 ? expf(sc[it] - mx) : 0.0f;
+        l += p;
+        float vv[8];
+        h8_to_f(vr[it], vv);
+        if (owner && j == pos) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) vv[e] = s_vn[8 * l16 + e];
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[e] = fmaf(p, vv[e], acc[e]);
+    }
+    // 5. sum over the 16 groups: in-wave across the 4 groups, then over waves
+#pragma unroll
+    for (int off = 32; off >= 16; off >>= 1) {
+        l += __shfl_xor(l, off);
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[e] += __shfl_xor(acc[e], off);
+    }
+    if (lane < 16) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) s_acc[wave][8 * l16 + e] = acc[e];
+    }
+    if (lane == 0) s_red[wave] = l;
+    __syncthreads();
+    float* pp = part + ((size_t)h * nsplit + sp) * (HD + 2);
+    if (tid < HD) {
+        float o = 0.0f;
+#pragma unroll
+        for (int w = 0; w < ATT_WG / 64; w++) o += s_acc[w][tid];
+        pp[tid] = o;
+    }
+    if (tid == 0) {
+        float lt = 0.0f;
+#pragma unroll
+        for (int w = 0; w < ATT_WG / 64; w++) lt += s_red[w];
+        pp[HD] = mx;  // -inf for an empty range
+        pp[HD + 1] = lt;
+    }
+}
+
+// out[h] = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M) over the splits.
+__global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restrict__ part, int nsplit, int max_ctx,
+                                                         const int* __restrict__ pos_p, float* __restrict__ out) {
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int pos = *pos_p;
+    if (pos < 0 || pos >= max_ctx) {
+        out[(size_t)h * HD + tid] = __builtin_nanf("");
+        return;
+    }
+    const float* ph = part + (size_t)h * nsplit * (HD + 2);
+    float M = -__builtin_inff();
+    for (int s = 0; s < nsplit; s++) M = fmaxf(M, ph[s * (HD + 2) + HD]);
+    float L = 0.0f, O = 0.0f;
+    for (int s = 0; s < nsplit; s++) {
+        const float f = expf(ph[s * (HD + 2) + HD] - M);  // an empty range has max -inf: factor 0
+        L = fmaf(ph[s * (HD + 2) + HD + 1], f, L);
+        O = fmaf(ph[s * (HD + 2) + tid], f, O);
+    }
+    out[(size_t)h * HD + tid] = O / L;
+}
+
+constexpr int AM_WG = 1024;
+
+__global__ __launch_bounds__(AM_WG) void argmax_embed_kernel(const float* __restrict__ logits, int vocab,
+                                                            const float* __restrict__ table, int dim, int* tokens,
+                                                            int tokens_cap, int prompt_len, int* pos_p,
+                                                            float* __restrict__ x) {
+    __shared__ float s_v[AM_WG / 64];
+    __shared__ int s_i[AM_WG / 64];
+    __shared__ int s_tok;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos = *pos_p;
+    const int nxt = pos + 1;
+    const bool forced = nxt < prompt_len && nxt < tokens_cap;
+    int tok;
+    if (forced) {
+        tok = tokens[nxt];
+    } else {
+        float bv = -__builtin_inff();
+        int bi = 0x7fffffff;
+        for (int i = tid; i < vocab; i += AM_WG) argmax_merge(bv, bi, scan_key(logits[i], i), i);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float ov = __shfl_xor(bv, off);
+            const int oi = __shfl_xor(bi, off);
+            argmax_merge(bv, bi, ov, oi);
+        }
+        if (lane == 0) {
+            s_v[wave] = bv;
+            s_i[wave] = bi;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            for (int w = 1; w < AM_WG / 64; w++) argmax_merge(bv, bi, s_v[w], s_i[w]);
+            s_tok = bi;
+        }
+        __syncthreads();
+        tok = s_tok;
+    }
+    if ((unsigned)tok >= (unsigned)vocab) tok = 0;  // an out-of-range prompt id reads row 0
+    const float4* src = reinterpret_cast<const float4*>(table + (size_t)tok * dim);
+    for (int i = tid; i < dim / 4; i += AM_WG) reinterpret_cast<float4*>(x)[i] = src[i];
+    __syncthreads();  // every thread has read pos
+    if (tid == 0) {
+        if (!forced && nxt < tokens_cap) tokens[nxt] = tok;
+        *pos_p = nxt;
+    }
+}
+
+}  // namespace
+
+int attn_decode_splits(int n_heads, int max_ctx) {
+    int s = (256 + n_heads - 1) / n_heads;  // about one workgroup per CU in all
+    const int need = (max_ctx + ATTN_MAX_CHUNK - 1) / ATTN_MAX_CHUNK;  // at most ATTN_MAX_CHUNK positions a split
+    return s < need ? need : s;
+}
+
+size_t attn_decode_work_bytes(int n_heads, int max_ctx) {
+    return (size_t)n_heads * attn_decode_splits(n_heads, max_ctx) * (HD + 2) * sizeof(float);
+}
+
+hipError_t launch_attn_decode(const float* qk, const float* v, const float* rcos, const float* rsin, uint16_t* kc,
+                              uint16_t* vc, int n_heads, int max_ctx, const int* pos, float scale, float* part,
+                              float* out, hipStream_t s) {
+    const int ns = attn_decode_splits(n_heads, max_ctx);
+    hipLaunchKernelGGL(attn_split_kernel, dim3(n_heads, ns), dim3(ATT_WG), 0, s, qk, v, rcos, rsin,
+                       reinterpret_cast<__half*>(kc), reinterpret_cast<__half*>(vc), max_ctx, pos, scale, part);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(HD), 0, s, part, ns, max_ctx, pos, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax_embed(const float* logits, int vocab, const float* table, int dim, int* tokens,
+                               int tokens_cap, int prompt_len, int* pos, float* x, hipStream_t s) {
+    hipLaunchKernelGGL(argmax_embed_kernel, dim3(1), dim3(AM_WG), 0, s, logits, vocab, table, dim, tokens, tokens_cap,
+                       prompt_len, pos, x);
+    return hipGetLastError();
+}
+
+}  // namespace frq

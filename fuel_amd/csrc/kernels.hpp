@@ -21,14 +21,18 @@ hipError_t launch_quantize_q8_0(const float* x, int rows, int K, ActView act, ui
 hipError_t launch_qmv(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K,
                       int ldy, hipStream_t s, int num_cus);
 
-// Indexed mat-vec (MoE mul_mat_id): launch row m reads activation row
-// x_row[m] (or m / x_div when x_row is null; stride ldx floats) and the
-// weights of expert w_sel[m] (expert_bytes apart; an id outside
-// [0, n_experts) yields a NaN output row and reads no weights).  Output rows
-// n >= n_split come from W2 instead of W (gate|up in one launch); with x2 set
-// the activation is silu(x) * x2, the SwiGLU input of the down projection
-// (x2 indexed like x).
-struct QmvIndex {
+// Options of the generalized mat-vec.
+// Indexed (MoE mul_mat_id): launch row m reads activation row x_row[m] (or
+// m / x_div when x_row is null; stride ldx floats) and the weights of expert
+// w_sel[m] (expert_bytes apart; an id outside [0, n_experts) yields a NaN
+// output row and reads no weights).  Output rows n >= n_split come from W2
+// instead of W (gate|up in one launch).
+// Both modes: with x2 set the activation is silu(x) * x2, the SwiGLU input of
+// the down projection (x2 indexed like x).
+// Fused (decode step): activation row m at x + m * ldx; with rms_gain set it
+// is first RMS-normalized with the affine gain, (x * rsqrt(mean(x^2) + eps)) *
+// gain; with accumulate set the output is added to y (residual stream).
+struct QmvOpts {
     const int* x_row;
     int x_div;
     int ldx;
@@ -38,9 +42,14 @@ struct QmvIndex {
     const uint8_t* w2;
     int n_split;
     const float* x2;
+    const float* rms_gain;
+    float rms_eps;
+    int accumulate;
 };
 hipError_t launch_qmv_indexed(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
-                              const QmvIndex& ix, hipStream_t s, int num_cus);
+                              const QmvOpts& ix, hipStream_t s, int num_cus);
+hipError_t launch_qmv_fused(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
+                            const QmvOpts& o, hipStream_t s, int num_cus);
 
 // moe.hip: top-k softmax routing of logits [T, E] (ids/w [T, topk]), the
 // expert batches of the routed entries (counting sort: expert_offsets [E+1],
@@ -104,5 +113,21 @@ hipError_t launch_random_bits(uint32_t* y, size_t n, unsigned long long start, u
                               uint32_t base, uint32_t stream, hipStream_t s);
 hipError_t launch_normal(float* y, size_t n, unsigned long long seed, uint32_t stream, float mean, float stdv,
                          hipStream_t s);
+
+// decode.hip: attention of one new token per head over an f16 KV cache with
+// RoPE and the cache append fused (head_dim ATTN_HEAD_DIM): a split kernel
+// over context ranges writing (output, max, sum) partials to `part`
+// (attn_decode_work_bytes), then a combine kernel; and the greedy next-token
+// + embedding step.
+constexpr int ATTN_HEAD_DIM = 128;
+constexpr int ATTN_NIT = 8;                     // positions per 16-lane group and split
+constexpr int ATTN_MAX_CHUNK = 16 * ATTN_NIT;   // positions per split (256-thread workgroups)
+int attn_decode_splits(int n_heads, int max_ctx);
+size_t attn_decode_work_bytes(int n_heads, int max_ctx);
+hipError_t launch_attn_decode(const float* qk, const float* v, const float* rcos, const float* rsin, uint16_t* kc,
+                              uint16_t* vc, int n_heads, int max_ctx, const int* pos, float scale, float* part,
+                              float* out, hipStream_t s);
+hipError_t launch_argmax_embed(const float* logits, int vocab, const float* table, int dim, int* tokens,
+                               int tokens_cap, int prompt_len, int* pos, float* x, hipStream_t s);
 
 }  // namespace frq

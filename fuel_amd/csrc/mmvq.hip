@@ -63,10 +63,25 @@ __device__ __forceinline__ float qmv_row(const typename F::Raw (&r)[SPL], const 
     return dpp_wave_sum(acc);
 }
 
-template <class F, int SPL, int WG, bool IDX>
+enum QmvMode { QMV_PLAIN = 0, QMV_INDEXED = 1, QMV_FUSED = 2 };
+
+// Sum over the workgroup of one float per wavefront (valid in lane 63 of each
+// wavefront), broadcast to every thread.
+template <int NW>
+__device__ __forceinline__ float block_sum_waves(float v, float* s_red, int w, int lane) {
+    if (lane == 63) s_red[w] = v;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NW; i++) t += s_red[i];
+    return t;
+}
+
+template <class F, int SPL, int WG, int MODE>
 __global__ __launch_bounds__(WG) void qmv_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
-                                                 float* __restrict__ y, int N, int K, int ldy, QmvIndex ix) {
+                                                 float* __restrict__ y, int N, int K, int ldy, QmvOpts ix) {
     extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ float s_red[WG / 64];
     constexpr int NW = WG / 64;
     const int m = blockIdx.y;
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -83,7 +98,7 @@ __global__ __launch_bounds__(WG) void qmv_kernel(const uint8_t* __restrict__ W, 
     const uint8_t* W2 = W;
     int n_split = N;
     const float* xr2 = nullptr;
-    if constexpr (IDX) {  // MoE: gathered activation row, per-row expert, optional second matrix
+    if constexpr (MODE == QMV_INDEXED) {  // MoE: gathered activation row, per-row expert, optional second matrix
         const int sel = ix.w_sel[m];
         if ((unsigned)sel >= (unsigned)ix.n_experts) {  // uniform over the workgroup
             for (int r = blockIdx.x * WG + threadIdx.x; r < N; r += gridDim.x * WG)
@@ -100,6 +115,13 @@ __global__ __launch_bounds__(WG) void qmv_kernel(const uint8_t* __restrict__ W, 
             n_split = ix.n_split;
         }
     }
+    if constexpr (MODE == QMV_FUSED) {
+        const size_t xo = (size_t)m * ix.ldx;
+        xr = x + xo;
+        if (ix.x2) xr2 = ix.x2 + xo;
+    }
+    float* yr = y + (size_t)m * ldy;
+    const bool acc_out = MODE == QMV_FUSED && ix.accumulate;
 
     // 1. activation loads first (s_waitcnt vmcnt is in order: the quantize step
     //    then waits for these only), 2. first weight row, 3. quantize to LDS.
@@ -107,12 +129,22 @@ __global__ __launch_bounds__(WG) void qmv_kernel(const uint8_t* __restrict__ W, 
     constexpr int CHUNKS = SPL * (64 / F::LPB) * F::ELEMS / QK_K;
     constexpr int MAXQ = (CHUNKS + NW - 1) / NW;
     ActRowPre<MAXQ> pre;
-    if (IDX && xr2) act_row_load_swiglu<F::ACT, NW, MAXQ>(xr, xr2, K, w, lane, pre);
+    if (MODE != QMV_PLAIN && xr2) act_row_load_swiglu<F::ACT, NW, MAXQ>(xr, xr2, K, w, lane, pre);
     else act_row_load<F::ACT, NW, MAXQ>(xr, K, w, lane, pre);
     // rows >= n_split live in the second matrix (row - n_split)
     auto wrow = [&](int r) { return r < n_split ? W + (size_t)r * row_bytes : W2 + (size_t)(r - n_split) * row_bytes; };
     typename F::Raw ra[SPL], rb[SPL];
-    if (row < N) qmv_load_row<F, SPL>(wrow(row), gi, c, KB, ra);
+    float resa = 0.0f, resb = 0.0f;  // residual values, loaded ahead of their row's weights
+    if (row < N) {
+        if (acc_out && lane == 63) resa = yr[row];
+        qmv_load_row<F, SPL>(wrow(row), gi, c, KB, ra);
+    }
+    if (MODE == QMV_FUSED && ix.rms_gain) {
+        // rms_norm_last_dim (sum of squares over the whole row, spread over the
+        // wavefronts) and the affine gain, before quantization
+        act_row_rms_norm<F::ACT, NW, MAXQ>(pre, ix.rms_gain, ix.rms_eps, K, w, lane,
+                                           [&](float v) { return block_sum_waves<NW>(v, s_red, w, lane); });
+    }
     act_row_quantize<F::ACT, NW, MAXQ>(pre, K, s_qs, lay.qstride, s_d, s_bs, w, lane);
     __syncthreads();
 
@@ -121,30 +153,34 @@ __global__ __launch_bounds__(WG) void qmv_kernel(const uint8_t* __restrict__ W, 
     // rather than branching around the loads.
     while (row < N) {
         int nrow = row + nw;
-        qmv_load_row<F, SPL>(wrow(nrow < N ? nrow : row), gi, c, KB, rb);
+        int lrow = nrow < N ? nrow : row;
+        if (acc_out && lane == 63) resb = yr[lrow];
+        qmv_load_row<F, SPL>(wrow(lrow), gi, c, KB, rb);
         float t = qmv_row<F, SPL>(ra, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
-        if (lane == 63) y[(size_t)m * ldy + row] = t;
+        if (lane == 63) yr[row] = acc_out ? resa + t : t;
         row = nrow;
         if (row >= N) break;
         nrow = row + nw;
-        qmv_load_row<F, SPL>(wrow(nrow < N ? nrow : row), gi, c, KB, ra);
+        lrow = nrow < N ? nrow : row;
+        if (acc_out && lane == 63) resa = yr[lrow];
+        qmv_load_row<F, SPL>(wrow(lrow), gi, c, KB, ra);
         t = qmv_row<F, SPL>(rb, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
-        if (lane == 63) y[(size_t)m * ldy + row] = t;
+        if (lane == 63) yr[row] = acc_out ? resb + t : t;
         row = nrow;
     }
 }
 
 namespace {
 
-template <class F, int SPL, bool IDX>
-hipError_t launch_qmv(const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy, const QmvIndex& ix,
+template <class F, int SPL, int MODE>
+hipError_t launch_qmv(const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy, const QmvOpts& ix,
                       hipStream_t s, int num_cus) {
     constexpr int WG = qmv_wg<F, SPL>();
     constexpr int NW = WG / 64;
     static int occ = -1;  // resident workgroups per CU for this instantiation
     if (occ < 0) {
         int o = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, qmv_kernel<F, SPL, WG, IDX>, WG, 16384) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, qmv_kernel<F, SPL, WG, MODE>, WG, 16384) != hipSuccess ||
             o < 1)
             o = 1;
         occ = o;
@@ -155,36 +191,36 @@ hipError_t launch_qmv(const uint8_t* w, const float* x, float* y, int M, int N, 
     int cap = num_cus * occ / (M > 0 ? M : 1);
     if (cap < 1) cap = 1;
     const int gx = need < cap ? need : cap;
-    hipLaunchKernelGGL((qmv_kernel<F, SPL, WG, IDX>), dim3(gx, M), dim3(WG), lds, s, w, x, y, N, K, ldy, ix);
+    hipLaunchKernelGGL((qmv_kernel<F, SPL, WG, MODE>), dim3(gx, M), dim3(WG), lds, s, w, x, y, N, K, ldy, ix);
     return hipGetLastError();
 }
 
-template <class F, bool IDX>
-hipError_t launch_fmt(const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy, const QmvIndex& ix,
+template <class F, int MODE>
+hipError_t launch_fmt(const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy, const QmvOpts& ix,
                       hipStream_t s, int num_cus) {
     constexpr int BPW = 64 / F::LPB;
     const int KB = K / F::ELEMS;
     const int spl = (KB + BPW - 1) / BPW;
     switch (spl) {
-        case 1: return launch_qmv<F, 1, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
-        case 2: return launch_qmv<F, 2, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
-        case 3: return launch_qmv<F, 3, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
-        case 4: return launch_qmv<F, 4, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
-        case 5: return launch_qmv<F, 5, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
-        case 6: return launch_qmv<F, 6, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
-        case 7: return launch_qmv<F, 7, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
-        case 8: return launch_qmv<F, 8, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        case 1: return launch_qmv<F, 1, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        case 2: return launch_qmv<F, 2, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        case 3: return launch_qmv<F, 3, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        case 4: return launch_qmv<F, 4, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        case 5: return launch_qmv<F, 5, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        case 6: return launch_qmv<F, 6, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        case 7: return launch_qmv<F, 7, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        case 8: return launch_qmv<F, 8, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
         default: return hipErrorInvalidValue;  // K beyond 8 slots: rejected by the host check
     }
 }
 
-template <bool IDX>
+template <int MODE>
 hipError_t launch_dtype(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
-                        const QmvIndex& ix, hipStream_t s, int num_cus) {
+                        const QmvOpts& ix, hipStream_t s, int num_cus) {
     switch (dtype) {
-        case GGML_Q4K: return launch_fmt<Q4K, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
-        case GGML_Q6K: return launch_fmt<Q6K, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
-        case GGML_Q8_0: return launch_fmt<Q80, IDX>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        case GGML_Q4K: return launch_fmt<Q4K, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        case GGML_Q6K: return launch_fmt<Q6K, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        case GGML_Q8_0: return launch_fmt<Q80, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
         default: return hipErrorInvalidValue;
     }
 }
@@ -193,12 +229,12 @@ hipError_t launch_dtype(int dtype, const uint8_t* w, const float* x, float* y, i
 
 hipError_t launch_qmv(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
                       hipStream_t s, int num_cus) {
-    return launch_dtype<false>(dtype, w, x, y, M, N, K, ldy, QmvIndex{}, s, num_cus);
+    return launch_dtype<QMV_PLAIN>(dtype, w, x, y, M, N, K, ldy, QmvOpts{}, s, num_cus);
 }
 
 hipError_t launch_qmv_indexed(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
-                              const QmvIndex& ix, hipStream_t s, int num_cus) {
-    return launch_dtype<true>(dtype, w, x, y, M, N, K, ldy, ix, s, num_cus);
+                              const QmvOpts& ix, hipStream_t s, int num_cus) {
+    return launch_dtype<QMV_INDEXED>(dtype, w, x, y, M, N, K, ldy, ix, s, num_cus);
 }
 
 // ------------------------------------------------------------------------
@@ -256,6 +292,11 @@ hipError_t launch_block_isums(int dtype, const uint8_t* w, ActView act, int32_t*
         case GGML_Q8_0: return go(Q80{});
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_qmv_fused(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
+                            const QmvOpts& o, hipStream_t s, int num_cus) {
+    return launch_dtype<QMV_FUSED>(dtype, w, x, y, M, N, K, ldy, o, s, num_cus);
 }
 
 }  // namespace frq

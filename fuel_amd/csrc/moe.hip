@@ -23,22 +23,6 @@ namespace {
 
 constexpr int ROUTE_WG = 256;  // one wavefront per token
 
-// Larger key wins; equal keys go to the lower index.  This is a max under a
-// total order, so a butterfly leaves every lane with the same winner.
-__device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
-    if (ov > v || (ov == v && oi < i)) {
-        v = ov;
-        i = oi;
-    }
-}
-
-// Key of element j for the sequential scan "best = 0; take j if work[j] >
-// work[best]": a NaN at j = 0 is never displaced, a NaN elsewhere is never
-// taken.  With these keys the total-order argmax equals that scan.
-__device__ __forceinline__ float scan_key(float v, int j) {
-    return v != v ? (j == 0 ? INFINITY : -INFINITY) : v;
-}
-
 template <int EPL>
 __global__ __launch_bounds__(ROUTE_WG) void moe_route_kernel(const float* __restrict__ logits, int T, int E, int topk,
                                                             int* __restrict__ ids, float* __restrict__ wts) {

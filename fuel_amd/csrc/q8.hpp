@@ -169,6 +169,39 @@ __device__ __forceinline__ void act_row_load_swiglu(const float* __restrict__ g,
     }
 }
 
+// rms_norm_last_dim_f32 (fuel-cpu-backend/src/byte_kernels.rs:2339-2368) and
+// the affine gain of apply_affine_rms_norm (fuel-core/src/lazy.rs:10330-10346)
+// on a row held by the workgroup: y = (x * (1 / sqrt(sum(x^2) * (1/K) + eps)))
+// * gain.  block_sum(v) sums one value per wavefront (lane 63) over the
+// workgroup; the sum of squares is a tree here, sequential in the reference.
+template <int ACT, int NW, int MAXQ, class BlockSum>
+__device__ __forceinline__ void act_row_rms_norm(ActRowPre<MAXQ>& p, const float* __restrict__ gain, float eps, int K,
+                                                 int w, int lane, BlockSum block_sum) {
+    const int nchunks = (K + QK_K - 1) / QK_K;
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MAXQ; i++) {  // dead lanes / chunks hold zeros
+        ss = fmaf(p.v[i].x, p.v[i].x, ss);
+        ss = fmaf(p.v[i].y, p.v[i].y, ss);
+        ss = fmaf(p.v[i].z, p.v[i].z, ss);
+        ss = fmaf(p.v[i].w, p.v[i].w, ss);
+    }
+    const float total = block_sum(dpp_wave_sum(ss));
+    const float rinv = 1.0f / sqrtf(total * (1.0f / (float)K) + eps);
+#pragma unroll
+    for (int i = 0; i < MAXQ; i++) {
+        const int ch = w + NW * i;
+        const bool live = ch < nchunks && (ACT == GGML_Q8K || ch * QK_K + 4 * lane < K);
+        if (live) {
+            const float4 g = reinterpret_cast<const float4*>(gain + (size_t)ch * QK_K)[lane];
+            p.v[i].x = (p.v[i].x * rinv) * g.x;
+            p.v[i].y = (p.v[i].y * rinv) * g.y;
+            p.v[i].z = (p.v[i].z * rinv) * g.z;
+            p.v[i].w = (p.v[i].w * rinv) * g.w;
+        }
+    }
+}
+
 template <int ACT, int NW, int MAXQ>
 __device__ __forceinline__ void act_row_quantize(const ActRowPre<MAXQ>& p, int K, int8_t* qs, int qstride,
                                                  float* dv, int16_t* bsums, int w, int lane) {

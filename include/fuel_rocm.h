@@ -157,6 +157,48 @@ int frq_moe_ffn(frq_device *dev, int ggml_dtype, size_t t, size_t d, size_t ffn,
                 const float *x_dev, const float *logits_dev, const void *w_gate_dev, const void *w_up_dev,
                 const void *w_down_dev, float *out_dev);
 
+/* ---- decode-step fusions around the QMatMul ----
+ * The QMatMul (k_quants.rs:2284-2331) with its neighbours in fuel's LLaMA
+ * layer (fuel-core/src/lazy.rs:7363-7440) fused into one mat-vec launch:
+ *   a = x                                   (plain), or
+ *   a = (x * rsqrt(mean(x^2) + eps)) * gain (rms_norm_last_dim_f32 and
+ *       apply_affine_rms_norm, byte_kernels.rs:2339-2368, lazy.rs:10330-10346;
+ *       rms_gain_dev != NULL), or
+ *   a = silu(x) * x2 = x / (1 + exp(-x)) * x2 (the SwiGLU input,
+ *       lazy.rs:7433-7434; x2_dev != NULL),
+ *   y[r, :] = W a(x[r, :])  or, with accumulate, y[r, :] += W a(x[r, :])
+ *       (the residual adds, lazy.rs:7426, 7439).
+ * Rows r < m of x (and x2) are ldx floats apart, of y ldy apart.  x, x2 and
+ * gain must be 16-byte aligned with ldx % 4 == 0.  Asynchronous; allocates
+ * nothing, so it may be captured into a HIP graph. */
+int frq_qmatmul_fused(frq_device *dev, int ggml_dtype, size_t m, size_t n, size_t k, const void *w_dev,
+                      const float *x_dev, size_t ldx, const float *x2_dev, const float *rms_gain_dev,
+                      float rms_eps, int accumulate, float *y_dev, size_t ldy);
+/* Decode attention of one token (lazy.rs:7391-7423 at seq = 1 with a KV
+ * cache): q and k of qk_dev = [q | k] (n_heads * head_dim each) are rotated
+ * (rope_f32 rotate-half, byte_kernels.rs:1885-1964, with the rows `pos` of
+ * the [max_ctx, head_dim] tables of build_rope_tables, fuel-graph/src/
+ * lib.rs:10808-10868), k and v are rounded to f16 and written at row `pos` of
+ * the caches [n_heads, max_ctx, head_dim], then per head
+ * out = softmax((q . k_j) * scale over j <= pos) . v_j.  pos is read from
+ * device memory (*pos_dev) so that a captured call serves every position.
+ * n_kv_heads = n_heads; head_dim = 128.  work_dev: at least
+ * frq_attention_decode_workspace() bytes of scratch for the per-split
+ * partials (no initialization needed).  A pos outside [0, max_ctx) gives NaN
+ * outputs and writes no cache row. */
+size_t frq_attention_decode_workspace(size_t n_heads, size_t max_ctx);
+int frq_attention_decode(frq_device *dev, size_t n_heads, size_t head_dim, size_t max_ctx, const float *qk_dev,
+                         const float *v_dev, const float *rope_cos_dev, const float *rope_sin_dev,
+                         uint16_t *k_cache_dev, uint16_t *v_cache_dev, const int32_t *pos_dev, float scale,
+                         void *work_dev, size_t work_bytes, float *out_dev);
+/* Greedy next token and its embedding: next = tokens[pos + 1] while
+ * pos + 1 < prompt_len, else the first-index argmax of logits [vocab]
+ * (argmax_dim_f32, byte_kernels.rs:8246-8261), stored at tokens[pos + 1]
+ * (when pos + 1 < tokens_cap); x = table[next] ([vocab, dim] f32, dim % 4 == 0);
+ * *pos_dev += 1.  Asynchronous, capturable. */
+int frq_argmax_embed(frq_device *dev, const float *logits_dev, size_t vocab, const float *table_dev, size_t dim,
+                     int32_t *tokens_dev, size_t tokens_cap, size_t prompt_len, int32_t *pos_dev, float *x_dev);
+
 /* ---- integer taps (build-internal parity probes; no reference counterpart) ----
  * Quantize rows of f32 activations into fuel's activation blocks
  * (BlockQ8K::from_float k_quants.rs:2230-2267, BlockQ8_0::from_float

@@ -75,6 +75,11 @@ def lib():
             "fo_qmatmul_bytes": (i32, [i32, sz, sz, sz, sz, vp, sz, vp, sz, vp, sz, i32, i32]),
             "fo_moe_route": (None, [vp, sz, sz, sz, vp, vp, vp, vp, vp]),
             "fo_moe_ffn": (i32, [i32, sz, sz, sz, sz, sz, vp, vp, vp, vp, vp, vp, vp, i32, i32]),
+            "fo_rms_norm": (None, [vp, vp, sz, sz, f32, vp]),
+            "fo_rope_tables": (None, [C.c_double, sz, sz, sz, vp, vp]),
+            "fo_rope": (None, [vp, vp, vp, sz, sz, sz, vp]),
+            "fo_attention_decode": (None, [vp, vp, vp, sz, sz, sz, sz, f32, vp]),
+            "fo_argmax": (sz, [vp, sz]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -242,3 +247,47 @@ def moe_ffn(dtype, x, ids, w, w_gate, w_up, w_down, avx2=True, threads=0):
     if rc:
         raise ValueError(f"fo_moe_ffn status {rc}")
     return out
+
+
+# ---- LLaMA decoder pieces ----------------------------------------------------
+
+def rms_norm(x: np.ndarray, gain: np.ndarray, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    gain = np.ascontiguousarray(gain, np.float32)
+    dim = x.shape[-1]
+    y = np.empty_like(x)
+    lib().fo_rms_norm(_p(x), _p(gain), x.size // dim, dim, eps, _p(y))
+    return y
+
+
+def rope_tables(base: float, start_pos: int, seq: int, head_dim: int):
+    c = np.empty((seq, head_dim), np.float32)
+    s = np.empty((seq, head_dim), np.float32)
+    lib().fo_rope_tables(base, start_pos, seq, head_dim, _p(c), _p(s))
+    return c, s
+
+
+def rope(x: np.ndarray, cos_t: np.ndarray, sin_t: np.ndarray) -> np.ndarray:
+    """x [..., seq, head_dim] with tables [seq, head_dim]."""
+    x = np.ascontiguousarray(x, np.float32)
+    seq, hd = x.shape[-2:]
+    y = np.empty_like(x)
+    lib().fo_rope(_p(x), _p(np.ascontiguousarray(cos_t, np.float32)), _p(np.ascontiguousarray(sin_t, np.float32)),
+                  x.size // (seq * hd), seq, hd, _p(y))
+    return y
+
+
+def attention_decode(q: np.ndarray, k: np.ndarray, v: np.ndarray, n_ctx: int, scale: float) -> np.ndarray:
+    """q [heads, hd]; k, v [heads, stride, hd] (first n_ctx rows used)."""
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    heads, stride, hd = k.shape
+    out = np.empty((heads, hd), np.float32)
+    lib().fo_attention_decode(_p(q), _p(k), _p(v), heads, n_ctx, stride, hd, scale, _p(out))
+    return out
+
+
+def argmax(x: np.ndarray) -> int:
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    return int(lib().fo_argmax(_p(x), x.size))

@@ -1090,3 +1090,95 @@ int fo_moe_ffn(int t, size_t ntok, size_t d, size_t ffn, size_t ne, size_t topk,
     free(xs); free(g); free(u); free(yd); free(sel); free(gw);
     return rc;
 }
+
+/* ------------------------------------------------------------------ */
+/* LLaMA decoder pieces                                                 */
+/* ------------------------------------------------------------------ */
+
+void fo_rms_norm(const float *x, const float *gain, size_t rows, size_t dim, float eps, float *y) {
+    const float inv_n = 1.0f / (float)dim;
+    for (size_t r = 0; r < rows; r++) {
+        const float *xr = x + r * dim;
+        float sum_sq = 0.0f;
+        for (size_t j = 0; j < dim; j++) sum_sq += xr[j] * xr[j];
+        const float mean_sq = sum_sq * inv_n;
+        const float rms_inv = 1.0f / sqrtf(mean_sq + eps);
+        for (size_t j = 0; j < dim; j++) {
+            const float nrm = xr[j] * rms_inv; /* normalized tensor, then the gain multiply */
+            y[r * dim + j] = nrm * gain[j];
+        }
+    }
+}
+
+void fo_rope_tables(double base, size_t start_pos, size_t seq, size_t head_dim, float *cos_t, float *sin_t) {
+    const size_t half = head_dim / 2;
+    for (size_t p = 0; p < seq; p++) {
+        const double pos = (double)(start_pos + p);
+        for (size_t i = 0; i < half; i++) {
+            const double freq = pow(base, -2.0 * (double)i / (double)head_dim);
+            const double theta = pos * freq;
+            const float c = (float)cos(theta), s = (float)sin(theta);
+            cos_t[p * head_dim + i] = c;
+            cos_t[p * head_dim + i + half] = c;
+            sin_t[p * head_dim + i] = s;
+            sin_t[p * head_dim + i + half] = s;
+        }
+    }
+}
+
+void fo_rope(const float *x, const float *cos_t, const float *sin_t, size_t outer, size_t seq, size_t head_dim,
+             float *y) {
+    const size_t h = head_dim / 2;
+    for (size_t o = 0; o < outer; o++)
+        for (size_t s = 0; s < seq; s++) {
+            const float *xr = x + (o * seq + s) * head_dim;
+            float *yr = y + (o * seq + s) * head_dim;
+            const float *c = cos_t + s * head_dim, *sn = sin_t + s * head_dim;
+            for (size_t i = 0; i < h; i++) {
+                const float lo = xr[i], hi = xr[i + h];
+                yr[i] = lo * c[i] - hi * sn[i];
+                yr[i + h] = hi * c[i + h] + lo * sn[i + h];
+            }
+        }
+}
+
+void fo_attention_decode(const float *q, const float *k, const float *v, size_t heads, size_t n_ctx, size_t stride,
+                         size_t head_dim, float scale, float *out) {
+    float *sc = (float *)malloc((n_ctx ? n_ctx : 1) * sizeof(float));
+    for (size_t h = 0; h < heads; h++) {
+        const float *qh = q + h * head_dim;
+        const float *kh = k + h * stride * head_dim, *vh = v + h * stride * head_dim;
+        for (size_t j = 0; j < n_ctx; j++) {
+            float d = 0.0f;
+            for (size_t e = 0; e < head_dim; e++) d += qh[e] * kh[j * head_dim + e];
+            sc[j] = d * scale;
+        }
+        float mx = sc[0];
+        for (size_t j = 1; j < n_ctx; j++)
+            if (sc[j] > mx) mx = sc[j];
+        float sum = 0.0f;
+        for (size_t j = 0; j < n_ctx; j++) {
+            sc[j] = expf(sc[j] - mx);
+            sum += sc[j];
+        }
+        const float inv = 1.0f / sum;
+        for (size_t j = 0; j < n_ctx; j++) sc[j] *= inv;
+        for (size_t e = 0; e < head_dim; e++) {
+            float o = 0.0f;
+            for (size_t j = 0; j < n_ctx; j++) o += sc[j] * vh[j * head_dim + e];
+            out[h * head_dim + e] = o;
+        }
+    }
+    free(sc);
+}
+
+size_t fo_argmax(const float *x, size_t n) {
+    size_t best = 0;
+    float bv = n ? x[0] : 0.0f;
+    for (size_t i = 1; i < n; i++)
+        if (x[i] > bv) {
+            bv = x[i];
+            best = i;
+        }
+    return best;
+}

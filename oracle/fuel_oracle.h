@@ -135,6 +135,28 @@ int fo_moe_ffn(int ggml_dtype, size_t t, size_t d, size_t ffn, size_t e, size_t 
                const float *x, const int32_t *ids, const float *w, const void *w_gate,
                const void *w_up, const void *w_down, float *out, int use_avx2, int threads);
 
+/* ---- LLaMA decoder pieces (fuel-core/src/lazy.rs:7363-7440) ----
+ * rms_norm_last_dim_f32 (fuel-cpu-backend/src/byte_kernels.rs:2339-2368)
+ * followed by the affine gain (apply_affine_rms_norm, lazy.rs:10330-10346):
+ * y = (x * (1 / sqrt(sum(x^2) * (1/dim) + eps))) * gain, per row. */
+void fo_rms_norm(const float *x, const float *gain, size_t rows, size_t dim, float eps, float *y);
+/* build_rope_tables (fuel-graph/src/lib.rs:10808-10868): cos/sin
+ * [seq, head_dim] for positions start_pos.., computed in f64. */
+void fo_rope_tables(double base, size_t start_pos, size_t seq, size_t head_dim, float *cos_t, float *sin_t);
+/* rope_f32 rotate-half (byte_kernels.rs:1885-1964): x [outer, seq, head_dim],
+ * tables [seq, head_dim]. */
+void fo_rope(const float *x, const float *cos_t, const float *sin_t, size_t outer, size_t seq, size_t head_dim,
+             float *y);
+/* One query per head against cached keys / values [heads, stride, head_dim]
+ * (first n_ctx rows): scores = (q . k_j) * scale (lazy.rs:7416-7420),
+ * softmax_last_dim_f32 (byte_kernels.rs:2259-2305), out = sum_j p_j v_j
+ * (lazy.rs:7422). q / out: [heads, head_dim]. */
+void fo_attention_decode(const float *q, const float *k, const float *v, size_t heads, size_t n_ctx, size_t stride,
+                         size_t head_dim, float scale, float *out);
+/* argmax_dim_f32 over one row (byte_kernels.rs:8178-8261): first element
+ * taken, then strictly greater values. */
+size_t fo_argmax(const float *x, size_t n);
+
 #ifdef __cplusplus
 }
 #endif
