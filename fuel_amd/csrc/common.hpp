@@ -67,27 +67,20 @@ __device__ __forceinline__ int nearest_int(float v) {
     return (int)r;
 }
 
-// 16 bytes from a 2-byte aligned address, using only dword-aligned loads.
-// A dword that holds at least one requested byte lies in the same page as
-// that byte, so this never touches a page the caller's range does not.
-__device__ __forceinline__ uint4 load16_a2(const uint8_t* p) {
-    const uintptr_t a = (uintptr_t)p;
-    const uint32_t* q = (const uint32_t*)(a & ~(uintptr_t)3);
-    const uint32_t sh = (uint32_t)(a & 3);
-    const uint32_t w0 = q[0], w1 = q[1], w2 = q[2], w3 = q[3];
-    const uint32_t w4 = sh ? q[4] : 0u;
-    return uint4{__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh),
-                 __builtin_amdgcn_alignbyte(w3, w2, sh), __builtin_amdgcn_alignbyte(w4, w3, sh)};
+// 16 / 8 bytes at any byte address as one global load.  gfx950 under the HSA
+// ABI runs with unaligned global access enabled (the compiler itself emits
+// global_load_dwordx4 for an unaligned memcpy); the load reads exactly the
+// requested bytes.
+__device__ __forceinline__ uint4 load16_u(const uint8_t* p) {
+    uint4 v;
+    __builtin_memcpy(&v, p, 16);
+    return v;
 }
 
-// 8 bytes from a 2-byte aligned address (same page rule as load16_a2).
-__device__ __forceinline__ uint2 load8_a2(const uint8_t* p) {
-    const uintptr_t a = (uintptr_t)p;
-    const uint32_t* q = (const uint32_t*)(a & ~(uintptr_t)3);
-    const uint32_t sh = (uint32_t)(a & 3);
-    const uint32_t w0 = q[0], w1 = q[1];
-    const uint32_t w2 = sh ? q[2] : 0u;
-    return uint2{__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh)};
+__device__ __forceinline__ uint2 load8_u(const uint8_t* p) {
+    uint2 v;
+    __builtin_memcpy(&v, p, 8);
+    return v;
 }
 
 __device__ __forceinline__ uint32_t load_u16(const uint8_t* p) {

@@ -89,30 +89,8 @@ struct Q4K {
 // elements 128hh + 32qd + l0 + [0,16) for qd = 0..3 from ql[64hh+l0..+16]
 // (qd 0 low / qd 2 high nibbles), ql[64hh+32+l0..+16] (qd 1 / 3) and
 // qh[32hh+l0..+16] (2 bits per qd)  (k_quants.rs:2170-2186); the scale of qd
-// is scales[8hh + 2qd + (c&1)].  Loads are dword-aligned and realigned with
-// v_alignbyte (see load16_a2).
+// is scales[8hh + 2qd + (c&1)].  Each 16-byte piece is one unaligned load.
 // ------------------------------------------------------------------------
-struct A2x16 {  // 16 bytes at a 2-byte aligned address, as aligned dwords
-    uint32_t w[5];
-    uint32_t sh;
-};
-
-__device__ __forceinline__ void load_a2x16(const uint8_t* p, A2x16& r) {
-    const uintptr_t a = (uintptr_t)p;
-    const uint32_t* q = (const uint32_t*)(a & ~(uintptr_t)3);
-    r.sh = (uint32_t)(a & 3);
-    r.w[0] = q[0];
-    r.w[1] = q[1];
-    r.w[2] = q[2];
-    r.w[3] = q[3];
-    r.w[4] = r.sh ? q[4] : 0u;
-}
-
-__device__ __forceinline__ void realign16(const A2x16& r, uint32_t (&o)[4]) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) o[i] = __builtin_amdgcn_alignbyte(r.w[i + 1], r.w[i], r.sh);
-}
-
 struct Q6K {
     static constexpr int LPB = 4;
     static constexpr int BYTES = Q6K_BYTES;
@@ -124,9 +102,8 @@ struct Q6K {
         float d;
     };
     struct Raw {
-        A2x16 la, lb, qh;
-        uint32_t sw[3];  // dwords covering scales[8hh..8hh+8)
-        uint32_t ssh;
+        uint4 la, lb, qh;
+        uint2 sc;  // scales[8hh..8hh+8)
         uint32_t dbits;
     };
     __device__ static void load_act(const int8_t* qs, int qstride, const float* dv, const int16_t* bsums, int b,
@@ -143,24 +120,17 @@ struct Q6K {
     }
     __device__ static void load(const uint8_t* blk, int c, Raw& r) {
         const int hh = c >> 1, l0 = 16 * (c & 1);
-        load_a2x16(blk + 64 * hh + l0, r.la);
-        load_a2x16(blk + 64 * hh + 32 + l0, r.lb);
-        load_a2x16(blk + 128 + 32 * hh + l0, r.qh);
-        const uintptr_t a = (uintptr_t)(blk + 192 + 8 * hh);
-        const uint32_t* q = (const uint32_t*)(a & ~(uintptr_t)3);
-        r.ssh = (uint32_t)(a & 3);
-        r.sw[0] = q[0];
-        r.sw[1] = q[1];
-        r.sw[2] = r.ssh ? q[2] : 0u;
+        r.la = load16_u(blk + 64 * hh + l0);
+        r.lb = load16_u(blk + 64 * hh + 32 + l0);
+        r.qh = load16_u(blk + 128 + 32 * hh + l0);
+        r.sc = load8_u(blk + 192 + 8 * hh);
         r.dbits = load_u16(blk + 208);
     }
     __device__ static void dot(const Raw& r, const Act& x, int c, int& isum, int& msum, float& dw, float& dmw) {
-        uint32_t wa[4], wb[4], wh[4];
-        realign16(r.la, wa);
-        realign16(r.lb, wb);
-        realign16(r.qh, wh);
-        const uint32_t scx = __builtin_amdgcn_alignbyte(r.sw[1], r.sw[0], r.ssh);
-        const uint32_t scy = __builtin_amdgcn_alignbyte(r.sw[2], r.sw[1], r.ssh);
+        const uint32_t wa[4] = {r.la.x, r.la.y, r.la.z, r.la.w};
+        const uint32_t wb[4] = {r.lb.x, r.lb.y, r.lb.z, r.lb.w};
+        const uint32_t wh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+        const uint32_t scx = r.sc.x, scy = r.sc.y;
         const uint32_t a0[4] = {x.a[0].x, x.a[0].y, x.a[0].z, x.a[0].w};
         const uint32_t a1[4] = {x.a[1].x, x.a[1].y, x.a[1].z, x.a[1].w};
         const uint32_t a2[4] = {x.a[2].x, x.a[2].y, x.a[2].z, x.a[2].w};
@@ -197,7 +167,8 @@ struct Q6K {
 };
 
 // ------------------------------------------------------------------------
-// Q8_0 (34 B, 2-byte aligned): 2 lanes per block; lane c owns qs[16c..16c+16).
+// Q8_0 (34 B, 2-byte aligned): 2 lanes per block; lane c owns qs[16c..16c+16)
+// (one unaligned 16-byte load).
 // ------------------------------------------------------------------------
 struct Q80 {
     static constexpr int LPB = 2;
@@ -209,7 +180,7 @@ struct Q80 {
         float d;
     };
     struct Raw {
-        A2x16 q;
+        uint4 q;
         uint32_t dbits;
     };
     __device__ static void load_act(const int8_t* qs, int qstride, const float* dv, const int16_t*, int b, int c,
@@ -218,12 +189,11 @@ struct Q80 {
         r.d = dv[b];
     }
     __device__ static void load(const uint8_t* blk, int c, Raw& r) {
-        load_a2x16(blk + 2 + 16 * c, r.q);
+        r.q = load16_u(blk + 2 + 16 * c);
         r.dbits = load_u16(blk);
     }
     __device__ static void dot(const Raw& r, const Act& x, int, int& isum, int& msum, float& dw, float& dmw) {
-        uint32_t q[4];
-        realign16(r.q, q);
+        const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
         int s = 0;
         s = dot4(q[0], x.a.x, s);
         s = dot4(q[1], x.a.y, s);
