@@ -21,12 +21,22 @@
 
 namespace frq {
 
-// Workgroup size: 512 threads while the two-row ring of raw weight registers
-// stays small (<= 40 dwords per row), else 256; both leave room for 2-3
-// resident workgroups per CU without spilling.
+// Workgroup size for many rows: 512 threads while the two-row ring of raw
+// weight registers stays small (<= 40 dwords per row), else 256; both leave
+// room for 2-3 resident workgroups per CU without spilling.
 template <class F, int SPL>
 constexpr int qmv_wg() {
     return SPL * (int)(sizeof(typename F::Raw) / 4) <= 40 ? 512 : 256;
+}
+
+// Workgroup size for few rows (about two per wavefront at one workgroup per
+// CU): as large as the register budget allows, so that one workgroup per CU
+// quantizes the activation row once for all its wavefronts (1024 threads
+// need <= 128 VGPRs, 512 threads <= 256).
+template <class F, int SPL>
+constexpr int qmv_wg_big() {
+    constexpr int raw = SPL * (int)(sizeof(typename F::Raw) / 4);
+    return raw <= 36 ? 1024 : raw <= 48 ? 512 : qmv_wg<F, SPL>();
 }
 
 template <class F, int SPL>
@@ -172,10 +182,9 @@ __global__ __launch_bounds__(WG) void qmv_kernel(const uint8_t* __restrict__ W, 
 
 namespace {
 
-template <class F, int SPL, int MODE>
-hipError_t launch_qmv(const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy, const QmvOpts& ix,
-                      hipStream_t s, int num_cus) {
-    constexpr int WG = qmv_wg<F, SPL>();
+template <class F, int SPL, int WG, int MODE>
+hipError_t launch_qmv_wg(const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy, const QmvOpts& ix,
+                         hipStream_t s, int num_cus) {
     constexpr int NW = WG / 64;
     static int occ = -1;  // resident workgroups per CU for this instantiation
     if (occ < 0) {
@@ -193,6 +202,15 @@ hipError_t launch_qmv(const uint8_t* w, const float* x, float* y, int M, int N, 
     const int gx = need < cap ? need : cap;
     hipLaunchKernelGGL((qmv_kernel<F, SPL, WG, MODE>), dim3(gx, M), dim3(WG), lds, s, w, x, y, N, K, ldy, ix);
     return hipGetLastError();
+}
+
+template <class F, int SPL, int MODE>
+hipError_t launch_qmv(const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy, const QmvOpts& ix,
+                      hipStream_t s, int num_cus) {
+    constexpr int WGN = qmv_wg<F, SPL>(), WGB = qmv_wg_big<F, SPL>();
+    if (WGB != WGN && (size_t)N * (size_t)M <= (size_t)num_cus * (WGB / 64) * 2)
+        return launch_qmv_wg<F, SPL, WGB, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+    return launch_qmv_wg<F, SPL, WGN, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
 }
 
 template <class F, int MODE>
