@@ -738,6 +738,31 @@ int frq_qmatmul_fused(frq_device* dev, int dt, size_t m, size_t n, size_t k, con
     return FRQ_OK;
 }
 
+int frq_qmatmul_fused_pair(frq_device* dev, size_t m, size_t k, const float* x, size_t ldx, const float* gain,
+                           float eps, int dt1, size_t n1, const void* w1, float* y1, int dt2, size_t n2, const void* w2,
+                           float* y2) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (!qmv_pair_supported(dt1, dt2, (int)(k > 0x7fffffff ? 0 : k)) || k == 0)
+        return fail(FRQ_UNSUPPORTED, "qmatmul_fused_pair: dtypes %d/%d with k=%zu", dt1, dt2, k);
+    if (m > 65535 || n1 > (size_t)0x7fffffff || n2 > (size_t)0x7fffffff)
+        return fail(FRQ_UNSUPPORTED, "qmatmul_fused_pair: m=%zu n1=%zu n2=%zu", m, n1, n2);
+    if (m == 0 || n1 == 0 || n2 == 0) return FRQ_OK;
+    if (!x || !w1 || !w2 || !y1 || !y2) return fail(FRQ_INVALID, "qmatmul_fused_pair: null buffer");
+    if ((m > 1 && ldx < k) || ldx > (size_t)0x7fffffff) return fail(FRQ_INVALID, "qmatmul_fused_pair: ldx=%zu", ldx);
+    if (!aligned16(x) || (gain && !aligned16(gain)) || ldx % 4)
+        return fail(FRQ_MISALIGNED, "qmatmul_fused_pair: x and gain must be 16-byte aligned and ldx %% 4 == 0");
+    if (!aligned4(w1) || !aligned4(w2) || !aligned4(y1) || !aligned4(y2))
+        return fail(FRQ_MISALIGNED, "qmatmul_fused_pair: weights / outputs not 4-byte aligned");
+    QmvOpts o{};
+    o.ldx = (int)ldx;
+    o.rms_gain = gain;
+    o.rms_eps = eps;
+    HIP_TRY(launch_qmv_pair(dt1, static_cast<const uint8_t*>(w1), y1, (int)n1, dt2, static_cast<const uint8_t*>(w2), y2,
+                            (int)n2, x, (int)m, (int)k, o, dev->stream, dev->num_cus));
+    return FRQ_OK;
+}
+
 size_t frq_attention_decode_workspace(size_t n_heads, size_t max_ctx) {
     if (n_heads == 0 || n_heads > 65535 || max_ctx == 0 || max_ctx > (size_t)0x7fffffff / (n_heads * ATTN_HEAD_DIM))
         return 0;

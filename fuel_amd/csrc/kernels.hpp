@@ -50,6 +50,12 @@ hipError_t launch_qmv_indexed(int dtype, const uint8_t* w, const float* x, float
                               const QmvOpts& ix, hipStream_t s, int num_cus);
 hipError_t launch_qmv_fused(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
                             const QmvOpts& o, hipStream_t s, int num_cus);
+// Two fused mat-vecs of the same activation rows (ldx apart, optional RMS
+// norm from `o`) in one launch: y1 [M, n1] = W1 a(x), y2 [M, n2] = W2 a(x);
+// Q4K / Q6K weights, K <= 16384.
+bool qmv_pair_supported(int dt1, int dt2, int K);
+hipError_t launch_qmv_pair(int dt1, const uint8_t* w1, float* y1, int n1, int dt2, const uint8_t* w2, float* y2,
+                           int n2, const float* x, int M, int K, const QmvOpts& o, hipStream_t s, int num_cus);
 
 // moe.hip: top-k softmax routing of logits [T, E] (ids/w [T, topk]), the
 // expert batches of the routed entries (counting sort: expert_offsets [E+1],

@@ -87,11 +87,11 @@ __device__ __forceinline__ float block_sum_waves(float v, float* s_red, int w, i
     return t;
 }
 
+// The mat-vec of one workgroup: block bx of gxn walking the rows of W.
 template <class F, int SPL, int WG, int MODE>
-__global__ __launch_bounds__(WG) void qmv_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
-                                                 float* __restrict__ y, int N, int K, int ldy, QmvOpts ix) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ float s_red[WG / 64];
+__device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const float* __restrict__ x,
+                                         float* __restrict__ y, int N, int K, int ldy, const QmvOpts& ix, int bx,
+                                         int gxn, uint8_t* smem, float* s_red) {
     constexpr int NW = WG / 64;
     const int m = blockIdx.y;
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -102,8 +102,8 @@ __global__ __launch_bounds__(WG) void qmv_kernel(const uint8_t* __restrict__ W, 
     int8_t* s_qs = reinterpret_cast<int8_t*>(smem);
     float* s_d = reinterpret_cast<float*>(smem + lay.off_d);
     int16_t* s_bs = reinterpret_cast<int16_t*>(smem + lay.off_bs);
-    const int nw = gridDim.x * NW;
-    int row = blockIdx.x * NW + w;
+    const int nw = gxn * NW;
+    int row = bx * NW + w;
     const float* xr = x + (size_t)m * K;
     const uint8_t* W2 = W;
     int n_split = N;
@@ -111,8 +111,7 @@ __global__ __launch_bounds__(WG) void qmv_kernel(const uint8_t* __restrict__ W, 
     if constexpr (MODE == QMV_INDEXED) {  // MoE: gathered activation row, per-row expert, optional second matrix
         const int sel = ix.w_sel[m];
         if ((unsigned)sel >= (unsigned)ix.n_experts) {  // uniform over the workgroup
-            for (int r = blockIdx.x * WG + threadIdx.x; r < N; r += gridDim.x * WG)
-                y[(size_t)m * ldy + r] = __builtin_nanf("");
+            for (int r = bx * WG + threadIdx.x; r < N; r += gxn * WG) y[(size_t)m * ldy + r] = __builtin_nanf("");
             return;
         }
         const size_t xo = (size_t)(ix.x_row ? ix.x_row[m] : m / ix.x_div) * ix.ldx;
@@ -180,6 +179,28 @@ __global__ __launch_bounds__(WG) void qmv_kernel(const uint8_t* __restrict__ W, 
     }
 }
 
+template <class F, int SPL, int WG, int MODE>
+__global__ __launch_bounds__(WG) void qmv_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
+                                                 float* __restrict__ y, int N, int K, int ldy, QmvOpts ix) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ float s_red[WG / 64];
+    qmv_body<F, SPL, WG, MODE>(W, x, y, N, K, ldy, ix, blockIdx.x, gridDim.x, smem, s_red);
+}
+
+// Two matrices of the same activation rows in one launch: workgroups
+// [0, gx1) compute y1 = W1 a(x) (format F1, N1 rows), the others y2 = W2 a(x).
+template <class F1, class F2, int SPL, int WG>
+__global__ __launch_bounds__(WG) void qmv_pair_kernel(const uint8_t* __restrict__ W1, float* __restrict__ y1, int N1,
+                                                      int gx1, const uint8_t* __restrict__ W2, float* __restrict__ y2,
+                                                      int N2, const float* __restrict__ x, int K, QmvOpts ix) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ float s_red[WG / 64];
+    if ((int)blockIdx.x < gx1)
+        qmv_body<F1, SPL, WG, QMV_FUSED>(W1, x, y1, N1, K, N1, ix, blockIdx.x, gx1, smem, s_red);
+    else
+        qmv_body<F2, SPL, WG, QMV_FUSED>(W2, x, y2, N2, K, N2, ix, blockIdx.x - gx1, gridDim.x - gx1, smem, s_red);
+}
+
 namespace {
 
 template <class F, int SPL, int WG, int MODE>
@@ -243,7 +264,65 @@ hipError_t launch_dtype(int dtype, const uint8_t* w, const float* x, float* y, i
     }
 }
 
+template <class F1, class F2, int SPL>
+hipError_t launch_pair_spl(const uint8_t* w1, float* y1, int n1, const uint8_t* w2, float* y2, int n2, const float* x,
+                           int M, int K, const QmvOpts& o, hipStream_t s, int num_cus) {
+    constexpr int WG1 = qmv_wg_big<F1, SPL>(), WG2 = qmv_wg_big<F2, SPL>();
+    constexpr int WG = WG1 < WG2 ? WG1 : WG2;
+    constexpr int NW = WG / 64;
+    static int occ = -1;
+    if (occ < 0) {
+        int v = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, qmv_pair_kernel<F1, F2, SPL, WG>, WG, 16384) !=
+                hipSuccess || v < 1)
+            v = 1;
+        occ = v;
+    }
+    const size_t lds = (size_t)act_lds_layout(F1::ACT, K).bytes;
+    if (lds > 65536) return hipErrorInvalidValue;
+    // workgroups split in proportion to the bytes of the two matrices
+    const double b1 = (double)n1 * F1::BYTES, b2 = (double)n2 * F2::BYTES;
+    int total = num_cus * occ / (M > 0 ? M : 1);
+    if (total < 2) total = 2;
+    int gx1 = (int)(total * b1 / (b1 + b2) + 0.5);
+    gx1 = gx1 < 1 ? 1 : gx1 > total - 1 ? total - 1 : gx1;
+    int gx2 = total - gx1;
+    const int need1 = (n1 + NW - 1) / NW, need2 = (n2 + NW - 1) / NW;
+    gx1 = gx1 < need1 ? gx1 : need1;
+    gx2 = gx2 < need2 ? gx2 : need2;
+    hipLaunchKernelGGL((qmv_pair_kernel<F1, F2, SPL, WG>), dim3(gx1 + gx2, M), dim3(WG), lds, s, w1, y1, n1, gx1, w2,
+                       y2, n2, x, K, o);
+    return hipGetLastError();
+}
+
+template <class F1, class F2>
+hipError_t launch_pair_fmt(const uint8_t* w1, float* y1, int n1, const uint8_t* w2, float* y2, int n2, const float* x,
+                           int M, int K, const QmvOpts& o, hipStream_t s, int num_cus) {
+    const int spl = (K / QK_K + 15) / 16;  // both formats: 4 lanes per superblock, 16 superblocks per wave step
+    switch (spl) {
+        case 1: return launch_pair_spl<F1, F2, 1>(w1, y1, n1, w2, y2, n2, x, M, K, o, s, num_cus);
+        case 2: return launch_pair_spl<F1, F2, 2>(w1, y1, n1, w2, y2, n2, x, M, K, o, s, num_cus);
+        case 3: return launch_pair_spl<F1, F2, 3>(w1, y1, n1, w2, y2, n2, x, M, K, o, s, num_cus);
+        case 4: return launch_pair_spl<F1, F2, 4>(w1, y1, n1, w2, y2, n2, x, M, K, o, s, num_cus);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 }  // namespace
+
+bool qmv_pair_supported(int dt1, int dt2, int K) {
+    const bool kq1 = dt1 == GGML_Q4K || dt1 == GGML_Q6K, kq2 = dt2 == GGML_Q4K || dt2 == GGML_Q6K;
+    return kq1 && kq2 && K % QK_K == 0 && K <= 4 * 16 * QK_K;
+}
+
+hipError_t launch_qmv_pair(int dt1, const uint8_t* w1, float* y1, int n1, int dt2, const uint8_t* w2, float* y2,
+                           int n2, const float* x, int M, int K, const QmvOpts& o, hipStream_t s, int num_cus) {
+    if (dt1 == GGML_Q4K && dt2 == GGML_Q6K) return launch_pair_fmt<Q4K, Q6K>(w1, y1, n1, w2, y2, n2, x, M, K, o, s, num_cus);
+    if (dt1 == GGML_Q4K && dt2 == GGML_Q4K) return launch_pair_fmt<Q4K, Q4K>(w1, y1, n1, w2, y2, n2, x, M, K, o, s, num_cus);
+    if (dt1 == GGML_Q6K && dt2 == GGML_Q4K) return launch_pair_fmt<Q6K, Q4K>(w1, y1, n1, w2, y2, n2, x, M, K, o, s, num_cus);
+    if (dt1 == GGML_Q6K && dt2 == GGML_Q6K) return launch_pair_fmt<Q6K, Q6K>(w1, y1, n1, w2, y2, n2, x, M, K, o, s, num_cus);
+    return hipErrorInvalidValue;
+}
 
 hipError_t launch_qmv(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
                       hipStream_t s, int num_cus) {

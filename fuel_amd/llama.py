@@ -3,7 +3,7 @@
 The decode step of fuel's LLaMA layer (fuel-core/src/lazy.rs:7363-7440) with
 a KV cache, built from this library's C ABI:
 
-    per layer:  [q|k] = QMatMul_Q4K(rms_norm(x) * attn_gain)        (one fused launch, Wq|Wk stacked)
+    per layer:  [q|k] = QMatMul_Q4K(rms_norm(x) * attn_gain)        (one launch for both, Wq|Wk stacked)
                 v     = QMatMul_Q6K(rms_norm(x) * attn_gain)
                 a     = attention(rope(q), cache <- rope(k), v)      (RoPE + f16 cache append fused)
                 x    += QMatMul_Q4K(a)                               (residual fused)
@@ -11,7 +11,7 @@ a KV cache, built from this library's C ABI:
                 x    += QMatMul_down(silu(g) * u)                    (SwiGLU + residual fused)
     logits = QMatMul_Q6K(rms_norm(x) * final_gain); next = argmax; x = embed[next]; pos += 1
 
-Six launches per layer, 194 per token.  The position lives in device memory,
+Six launches per layer (the attention is two), 194 per token.  The position lives in device memory,
 so one captured HIP graph replays every step (prompt tokens are forced while
 they last).  Weights follow a Q4_K_M-style mix: Q4_K everywhere except attn_v,
 ffn_down of the even layers and the output matrix (Q6_K).  All weights are
@@ -236,9 +236,8 @@ class LlamaDecoder:
         x = vp(self.x.ptr)
         for li, lw in enumerate(self.layers):
             ag, fg = vp(self.attn_gain[li].ptr), vp(self.ffn_gain[li].ptr)
-            check(L.frq_qmatmul_fused(h, Q4K, 1, 2 * d, d, vp(lw["wqk"].ptr), x, d, None, ag, eps, 0,
-                                      vp(self.qk.ptr), 2 * d))
-            check(L.frq_qmatmul_fused(h, Q6K, 1, d, d, vp(lw["wv"].ptr), x, d, None, ag, eps, 0, vp(self.v.ptr), d))
+            check(L.frq_qmatmul_fused_pair(h, 1, d, x, d, ag, eps, Q4K, 2 * d, vp(lw["wqk"].ptr), vp(self.qk.ptr),
+                                           Q6K, d, vp(lw["wv"].ptr), vp(self.v.ptr)))
             check(L.frq_attention_decode(h, cfg.n_heads, cfg.head_dim, cfg.max_ctx, vp(self.qk.ptr), vp(self.v.ptr),
                                          vp(self.rcos.ptr), vp(self.rsin.ptr), vp(self.kc[li].ptr),
                                          vp(self.vc[li].ptr), vp(self.pos.ptr), self.scale, vp(self.work.ptr),

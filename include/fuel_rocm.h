@@ -174,6 +174,14 @@ int frq_moe_ffn(frq_device *dev, int ggml_dtype, size_t t, size_t d, size_t ffn,
 int frq_qmatmul_fused(frq_device *dev, int ggml_dtype, size_t m, size_t n, size_t k, const void *w_dev,
                       const float *x_dev, size_t ldx, const float *x2_dev, const float *rms_gain_dev,
                       float rms_eps, int accumulate, float *y_dev, size_t ldy);
+/* Two QMatMuls of the same activation rows in one launch (the [q|k] and v
+ * projections of a layer, lazy.rs:7384-7386): y1[r, :] = W1 a(x[r, :]) and
+ * y2[r, :] = W2 a(x[r, :]) with a() the plain or RMS-normalized activation of
+ * frq_qmatmul_fused; W1 / W2 are Q4K or Q6K (k % 256 == 0, k <= 16384); y1 /
+ * y2 rows are n1 / n2 floats.  Asynchronous, capturable. */
+int frq_qmatmul_fused_pair(frq_device *dev, size_t m, size_t k, const float *x_dev, size_t ldx,
+                           const float *rms_gain_dev, float rms_eps, int dtype1, size_t n1, const void *w1_dev,
+                           float *y1_dev, int dtype2, size_t n2, const void *w2_dev, float *y2_dev);
 /* Decode attention of one token (lazy.rs:7391-7423 at seq = 1 with a KV
  * cache): q and k of qk_dev = [q | k] (n_heads * head_dim each) are rotated
  * (rope_f32 rotate-half, byte_kernels.rs:1885-1964, with the rows `pos` of

@@ -75,6 +75,31 @@ def test_qmatmul_fused_swiglu_residual(dev, dt, n, ffn):
     assert rel_err(y.numpy(), want) < TOL
 
 
+@pytest.mark.parametrize("dt1,n1,dt2,n2,k,m", [(O.Q4K, 8192, O.Q6K, 4096, 4096, 1), (O.Q6K, 300, O.Q4K, 1000, 2048, 2),
+                                               (O.Q4K, 512, O.Q4K, 768, 11008, 1)])
+def test_qmatmul_fused_pair(dev, dt1, n1, dt2, n2, k, m):
+    """[q|k] and v from one launch equal the two single fused launches (same
+    kernels, same quantized activation) and the CPU path within 1e-3."""
+    say("fused pair", dt1, n1, dt2, n2, k, m)
+    w1 = O.quantize(dt1, O.normal((n1, k), seed=k, stream=1, std=0.02))
+    w2 = O.quantize(dt2, O.normal((n2, k), seed=k, stream=2, std=0.02))
+    x = O.normal((m, k), seed=k, stream=3, std=2.0)
+    g = 1 + O.normal((k,), seed=k, stream=4, std=0.2)
+    w1d, w2d, xd, gd = (dev.from_numpy(a) for a in (w1.view(np.uint8), w2.view(np.uint8), x, g))
+    y1, y2 = dev.alloc((m, n1), np.float32), dev.alloc((m, n2), np.float32)
+    F._native.check(L().frq_qmatmul_fused_pair(dev.handle, m, k, C.c_void_p(xd.ptr), k, C.c_void_p(gd.ptr), 1e-5,
+                                               dt1, n1, C.c_void_p(w1d.ptr), C.c_void_p(y1.ptr),
+                                               dt2, n2, C.c_void_p(w2d.ptr), C.c_void_p(y2.ptr)))
+    s1 = fused(dev, dt1, w1d, xd, n1, k, m=m, gain=gd).numpy()
+    s2 = fused(dev, dt2, w2d, xd, n2, k, m=m, gain=gd).numpy()
+    np.testing.assert_array_equal(y1.numpy(), s1)
+    np.testing.assert_array_equal(y2.numpy(), s2)
+    xn = O.rms_norm(x, g, 1e-5)
+    w1r, w2r = O.matmul(dt1, xn, w1), O.matmul(dt2, xn, w2)
+    for r in range(m):
+        assert rel_err(y1.numpy()[r], w1r[r]) < TOL and rel_err(y2.numpy()[r], w2r[r]) < TOL
+
+
 def test_qmatmul_fused_errors(dev):
     w = dev.alloc((144 * 16,), np.uint8)
     x = dev.alloc((4096,), np.float32)
