@@ -3,6 +3,7 @@
 // mirror) and the KernelRef-shaped qmatmul.  Host code only.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -21,6 +22,9 @@ struct frq_device {
     int num_cus = 0;
     void* ws = nullptr;  // activation workspace (quantized rows)
     size_t ws_bytes = 0;
+    // references: the open handle plus one per live storage; the struct is
+    // deleted when the last one is dropped (a storage may outlive close)
+    std::atomic<int> refs{1};
 };
 
 struct frq_qstorage {
@@ -122,8 +126,15 @@ int ensure_ws(frq_device* dev, size_t bytes) {
 
 int use_device(frq_device* dev) {
     if (!dev) return fail(FRQ_INVALID, "null device handle");
+    // HIP keeps the last error of the thread until it is read: drop one left
+    // by an earlier call so that the launch checks of this call see their own
+    (void)hipGetLastError();
     HIP_TRY(hipSetDevice(dev->ordinal));
     return FRQ_OK;
+}
+
+void release_device(frq_device* dev) {
+    if (dev->refs.fetch_sub(1) == 1) delete dev;
 }
 
 // Quantize rows x [rows, k] into the workspace (and optionally into fuel's
@@ -269,8 +280,12 @@ int frq_device_close(frq_device* dev) {
     (void)hipSetDevice(dev->ordinal);
     (void)hipStreamSynchronize(dev->stream);
     if (dev->ws) (void)hipFree(dev->ws);
+    dev->ws = nullptr;
+    dev->ws_bytes = 0;
     if (dev->own_stream) (void)hipStreamDestroy(dev->own_stream);
-    delete dev;
+    dev->own_stream = dev->stream = nullptr;
+    (void)hipGetLastError();
+    release_device(dev);  // storages still alive keep the struct until they are freed
     return FRQ_OK;
 }
 
@@ -359,6 +374,7 @@ static int new_storage(frq_device* dev, int t, size_t nbytes, frq_qstorage** out
             return fail(FRQ_WORKSPACE, "hipMalloc(%zu): %s", nbytes, hipGetErrorString(e));
         }
     }
+    dev->refs.fetch_add(1);
     *out = q;
     return FRQ_OK;
 }
@@ -401,9 +417,10 @@ int frq_qstorage_free(frq_qstorage* q) {
     if (!q) return FRQ_OK;
     if (q->d_ptr) {
         (void)hipSetDevice(q->dev->ordinal);
-        (void)hipStreamSynchronize(q->dev->stream);
-        (void)hipFree(q->d_ptr);
+        (void)hipFree(q->d_ptr);  // waits for work that may still use the blocks
+        (void)hipGetLastError();
     }
+    release_device(q->dev);
     delete q;
     return FRQ_OK;
 }

@@ -292,3 +292,17 @@ def test_qmatmul_q4k_mfma_ragged(dev, batch, m, n, k):
     F.qmatmul_f32_rocm_wrapper([dev.from_numpy(x.reshape(batch, m, k)), w], [out],
                                F.QMatMulParams(O.Q4K, batch, m, n, k))
     assert rel_err(out.numpy().reshape(batch * m, n), want) <= TOL
+
+
+def test_storage_outlives_device_close(dev):
+    """A quantized storage freed after its device handle was closed releases
+    cleanly, and the next calls on another handle see no error of it."""
+    say("storage outlives close")
+    d2 = F.RocmDevice(0)
+    q = d2.qzeros(256 * 64, F.Q4K)
+    d2.close()
+    del q                                    # frees the blocks through the closed handle's record
+    w = O.quantize(O.Q4K, O.normal((64, 256), seed=5, stream=1, std=0.02))
+    x = O.normal((1, 256), seed=5, stream=2)
+    got, _ = dev.load_quantized(O.Q4K, w.tobytes()).fwd((64, 256), dev.from_numpy(x))
+    assert rel_err(got.numpy()[0], O.matmul(O.Q4K, x, w)[0]) < TOL
