@@ -147,8 +147,131 @@ def gpu_leg(steps: int, warmup: int):
         hip.graph_destroy(g)
     for g in graphs:
         hip.graph_destroy(g)
+    batched = batched_leg(hip, dev, stream, mats) if BATCHED_M else None
+    mats.clear()  # frees the rotated weights
     dev.close()
-    return ms_per_step, step_bytes, per_shape, R
+    return ms_per_step, step_bytes, per_shape, R, batched
+
+
+BATCHED_M = (32, 128, 512)
+INT8_PEAK_TOPS = 5000.0
+
+
+def batched_leg(hip, dev, stream, mats):
+    """QMatMul with M = 32, 128, 512 activation rows at the
+    same shapes and rotated Q4_K weights (the int8-MFMA path).  Reported as
+    useful TOPS (2 M N K per call) against the dense int8 peak."""
+    import ctypes as C
+
+    import fuel_amd as F
+
+    lib = F.lib()
+    e0, e1 = hip.event_create(), hip.event_create()
+    out = {}
+    for si, m in enumerate(mats):
+        k, n = m["k"], m["n"]
+        for M in BATCHED_M:
+            x = F.fill_normal(dev, (M, k), SEED, 300 + 10 * si + BATCHED_M.index(M))
+            y = dev.alloc((M, n), np.float32)
+
+            def call(r):
+                w = m["ws"][r % len(m["ws"])]
+                F._native.check(lib.frq_qmatmul(dev.handle, F.Q4K, 1, M, n, k, C.c_void_p(x.ptr), x.nbytes,
+                                                C.c_void_p(w.device_ptr()), m["nbytes"], C.c_void_p(y.ptr), y.nbytes))
+
+            call(0)  # sizes the workspace outside the capture
+            dev.synchronize()
+            Rm = len(m["ws"])
+            g = hip.capture(stream, lambda: [call(r) for r in range(Rm)])
+            hip.graph_launch(g, stream)
+            reps = max(2, 60 // Rm)
+            hip.stream_sync(stream)
+            hip.event_record(e0, stream)
+            for _ in range(reps):
+                hip.graph_launch(g, stream)
+            hip.event_record(e1, stream)
+            hip.event_sync(e1)
+            us = hip.elapsed_ms(e0, e1) * 1e3 / (reps * Rm)
+            hip.graph_destroy(g)
+            tops = 2.0 * M * n * k / us / 1e6
+            out[f"{k}x{n}_M{M}"] = {"us": round(us, 2), "TOPS": round(tops, 1),
+                                    "int8_peak_frac": round(tops / INT8_PEAK_TOPS, 4),
+                                    "weight_GB_s": round(m["nbytes"] / us / 1e3, 1)}
+            x.free()
+            y.free()
+    return out
+
+
+MOE_T = (1, 16, 512)
+
+
+def moe_leg():
+    """Qwen3-MoE-style expert layer, 128 experts, top-8 of
+    N(0,1) router logits, d 2048, expert FFN 768, Q4_K experts from N(0,0.02);
+    T = 1, 16, 512 tokens.  Four copies of the 340 MB expert set are rotated
+    (1.36 GB, beyond the Infinity Cache) and every call routes fresh logits.
+    Algorithmic bytes: the distinct routed experts' weights + x in + out."""
+    import ctypes as C
+
+    import fuel_amd as F
+    from fuel_amd.hiprt import HipRuntime
+
+    E, TOPK, D, FFN, COPIES = 128, 8, 2048, 768, 4
+    hip = HipRuntime()
+    dev = F.RocmDevice(0)
+    stream = hip.stream_create()
+    dev.set_stream(stream)
+    lib = F.lib()
+
+    def experts(rows, cols, stream_id):
+        w32 = F.fill_normal(dev, (E, rows, cols), SEED, stream_id, 0.0, 0.02)
+        q = dev.qzeros(E * rows * cols, F.Q4K)
+        q.quantize(w32)
+        dev.synchronize()
+        w32.free()
+        return q
+
+    sets = [(experts(FFN, D, 400 + 3 * c), experts(FFN, D, 401 + 3 * c), experts(D, FFN, 402 + 3 * c))
+            for c in range(COPIES)]
+    per_expert = sum(q.storage_size_in_bytes() for q in sets[0]) // E
+    e0, e1 = hip.event_create(), hip.event_create()
+    res = {}
+    for T in MOE_T:
+        NL = 8
+        x = F.fill_normal(dev, (T, D), SEED, 500 + T)
+        logits = [F.fill_normal(dev, (T, E), SEED, 600 + 10 * T + i) for i in range(NL)]
+        out = dev.alloc((T, D), np.float32)
+
+        def call(i):
+            g, u, d_ = sets[i % COPIES]
+            F._native.check(lib.frq_moe_ffn(dev.handle, F.Q4K, T, D, FFN, E, TOPK, C.c_void_p(x.ptr),
+                                            C.c_void_p(logits[i % NL].ptr), C.c_void_p(g.device_ptr()),
+                                            C.c_void_p(u.device_ptr()), C.c_void_p(d_.device_ptr()),
+                                            C.c_void_p(out.ptr)))
+
+        call(0)
+        dev.synchronize()
+        R = 8
+        g = hip.capture(stream, lambda: [call(i) for i in range(R)])
+        hip.graph_launch(g, stream)
+        hip.stream_sync(stream)
+        reps = 10
+        hip.event_record(e0, stream)
+        for _ in range(reps):
+            hip.graph_launch(g, stream)
+        hip.event_record(e1, stream)
+        hip.event_sync(e1)
+        us = hip.elapsed_ms(e0, e1) * 1e3 / (reps * R)
+        hip.graph_destroy(g)
+        distinct = float(np.mean([len(np.unique(F.moe_route(dev, lg, TOPK)[0])) for lg in logits]))
+        nbytes = distinct * per_expert + 2 * T * D * 4
+        res[f"T{T}"] = {"us_per_layer": round(us, 2), "distinct_experts_mean": distinct,
+                        "algorithmic_bytes": int(nbytes), "GB_s": round(nbytes / us / 1e3, 1),
+                        "path": "grouped int8-MFMA" if T * TOPK >= E else "indexed mat-vec"}
+        x.free()
+        out.free()
+    dev.close()
+    return res
 
 
 DECODE_PROMPT = 512
@@ -326,6 +449,8 @@ def main() -> int:
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="first run device copies of this size (counter calibration)")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-batched", action="store_true", help="skip the config-3 M = 32/128/512 leg")
+    ap.add_argument("--no-moe", action="store_true", help="skip the config-5 MoE leg")
     ap.add_argument("--decode-only", action="store_true", help="run only the config-4 decode legs")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -346,7 +471,10 @@ def main() -> int:
         print(json.dumps({"metric": "decode tokens/s, LLaMA-2-7B-shaped Q4_K_M mix (BASELINE config 4)",
                           "value": dres["tokens_per_s"], "unit": "tokens/s", "decode": dres}), flush=True)
         return 0
-    ms_per_step, step_bytes, per_shape, rot = gpu_leg(args.steps, args.warmup)
+    global BATCHED_M
+    if args.no_batched:
+        BATCHED_M = ()
+    ms_per_step, step_bytes, per_shape, rot, batched = gpu_leg(args.steps, args.warmup)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     dom_key = "4096x32000" if "4096x32000" in per_shape else next(iter(per_shape))
     dom = per_shape[dom_key]
@@ -392,6 +520,11 @@ def main() -> int:
             "traffic": traffic,
         },
     }
+    if batched:
+        out["batched"] = batched
+    if not args.no_moe:
+        out["moe"] = moe_leg()
+        say(f"[bench] moe {out['moe']}")
     if not args.no_decode:
         dres, dec, dev, tokens, logits0 = decode_leg()
         say(f"[bench] decode {dres}")

@@ -27,12 +27,12 @@ COPY_BYTES = 256 << 20
 
 def run(cmd: list[str], log: str, limit: int) -> None:
     print("+", " ".join(cmd), flush=True)
-    with open(log, "w") as f:
+    with open(os.path.join(ROOT, log), "w") as f:
         subprocess.run(cmd, check=True, stdout=f, stderr=subprocess.STDOUT, cwd=ROOT, timeout=limit)
 
 
 def rows(d: str, name: str):
-    for f in glob.glob(os.path.join(d, "**", name), recursive=True):
+    for f in glob.glob(os.path.join(ROOT, d, "**", name), recursive=True):
         yield from csv.DictReader(open(f))
 
 
@@ -42,11 +42,11 @@ def main() -> int:
     ap.add_argument("--out", default="gpurun_out/profiles")
     ap.add_argument("--summarize-only", action="store_true", help="re-read existing pass outputs")
     args = ap.parse_args()
-    out = os.path.join(ROOT, args.out)
-    os.makedirs(out, exist_ok=True)
+    os.makedirs(os.path.join(ROOT, args.out), exist_ok=True)
+    out = args.out  # relative to the repository root, where every pass runs
     os.environ.setdefault("TMPDIR", "/tmp")
     bench = ["python3", "bench.py", "--shape", args.shape, "--steps", "50", "--warmup", "5", "--no-cpu",
-             "--no-decode", "--copy-bytes", str(COPY_BYTES)]
+             "--no-decode", "--no-batched", "--no-moe", "--copy-bytes", str(COPY_BYTES)]
     cmds = {
         "trace": ["rocprofv3", "--kernel-trace", "--stats", "--output-format", "csv", "-d", f"{out}/trace", "-o", "run",
                   "--"] + bench,
@@ -100,8 +100,8 @@ def main() -> int:
         "traffic_over_algorithmic": round((fetch_b + write_b) / algo, 4),
         "commands": {k2: " ".join(v) for k2, v in cmds.items()},
     }
-    json.dump(res, open(f"{out}/qmv_q4k_{args.shape}_traffic.json", "w"), indent=1)
-    with open(f"{out}/qmv_q4k_{args.shape}.md", "w") as f:
+    json.dump(res, open(os.path.join(ROOT, out, f"qmv_q4k_{args.shape}_traffic.json"), "w"), indent=1)
+    with open(os.path.join(ROOT, out, f"qmv_q4k_{args.shape}.md"), "w") as f:
         f.write(f"# Q4_K mat-vec K x N = {args.shape}, M = 1 (qmv_kernel<Q4K>)\n\n")
         f.write(f"Made by `python3 bench_profile.py --shape {args.shape}` (repository root, one MI355X), "
                 "which runs:\n\n")
