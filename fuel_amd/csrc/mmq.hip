@@ -3,25 +3,40 @@
 //
 // Exact integer formulation.  Per superblock b, with q4 the weight nibbles,
 // sc_j / m_j the 6-bit scale / min of sub-block j and q8 the Q8K activation:
-//   isum = sum_j sc_j * sum_{e in j} q4_e q8_e ,  msum = sum_j m_j * sum_{e in j} q8_e
+//   isum = sum_j sc_j * sum_{e in j} q4_e q8_e ,  msum = sum_j m_j * S_j
+// with S_j = sum_{e in j} q8_e (two of the activation's 16-element bsums).
 // A 6-bit scale times a nibble does not fit int8, so sc_j = 8*a_j + b_j with
 // a_j, b_j <= 7: q4*a_j and q4*b_j are <= 105 and a dword holding four nibbles
 // can be multiplied by a_j without carries between its bytes.  Then
 //   isum = 8 * (X . Ba) + (X . Bb),   msum = X . Bm
-// with Ba = q4*a_j, Bb = q4*b_j, Bm = m_j (broadcast over the sub-block): three
-// int8 GEMMs over K = 256 per superblock on v_mfma_i32_16x16x64_i8, exact in
-// int32, followed by one f32 step y += d_w*d_x*isum - dmin_w*d_x*msum.
+// with Bm the sub-block mins broadcast over their 32 elements: three int8
+// GEMMs over K = 256 per superblock on v_mfma_i32_16x16x64_i8, exact in int32.
+// (The kernel is bound by its VALU work, not the matrix cores: msum on the
+// MFMA pipe costs less than its 8-term dot products on the VALU.)  Then one
+// f32 step per superblock: y += d_x * (d_w*isum - dmin_w*msum).
 //
-// Workgroup: 4 wavefronts on a WM x WN grid, each owning RT x CT tiles of 16x16
-// outputs.  Per superblock the workgroup stages the quantized activation rows
-// (272-byte LDS row stride) and the raw weight blocks of its columns in LDS;
-// each lane then builds its B fragments in registers from the raw nibbles.
+// Workgroup: WM x WN wavefronts, each owning RT x CT tiles of 16x16 outputs.
+// Per superblock the workgroup stages the quantized activation rows (272-byte
+// LDS row stride), their scales and the raw weight blocks of its columns in
+// LDS, double-buffered: the next superblock's global loads are in
+// flight while the current one is multiplied, and one barrier per superblock
+// separates the two buffers' roles.  Lanes build their B fragments in
+// registers from the raw nibbles.
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace frq {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// Four nibble bytes (<= 15) times a small factor (<= 7), byte by byte: each
+// product is <= 105, so two 16-bit lane multiplies (one full-rate packed
+// instruction) produce them without carries between bytes.
+__device__ __forceinline__ int bytes_times(uint32_t q, uint32_t f) {
+    const u16x2 p = __builtin_bit_cast(u16x2, q) * u16x2{(unsigned short)f, (unsigned short)f};
+    return __builtin_bit_cast(int, p);
+}
 
 namespace {
 
@@ -31,112 +46,140 @@ template <int RT, int CT, int WM, int WN>
 struct MmqTile {
     static constexpr int NT = 64 * WM * WN;
     static constexpr int BM = 16 * RT * WM, BN = 16 * CT * WN;
-    static constexpr int A_CH = BM * 16;                   // 16-byte activation chunks per superblock
-    static constexpr int W_CH = BN * 9;                    // 16-byte weight chunks per superblock
-    static constexpr int A_PT = (A_CH + NT - 1) / NT;      // per thread
+    static constexpr int A_CH = BM * 16;  // 16-byte activation chunks per superblock
+    static constexpr int W_CH = BN * 9;   // 16-byte weight chunks per superblock
+    static constexpr int A_PT = (A_CH + NT - 1) / NT;
     static constexpr int W_PT = (W_CH + NT - 1) / NT;
+    // LDS per buffer: activations, weights, activation scales
+    static constexpr int LDS_A = BM * A_STRIDE, LDS_W = BN * Q4K_BYTES, LDS_D = BM * 4;
+    static constexpr int LDS_BUF = LDS_A + LDS_W + LDS_D;
 };
 
-// Global -> register prefetch of one superblock's activation rows and raw
-// weight blocks.  arow: this thread's activation row per chunk (-1: padding
-// row, staged as zeros); wrow: its weight row base per chunk; dxrow: the row
-// whose scale it stages (-1: none).
+// Register copy of one superblock's share of a thread: activation chunks,
+// weight chunks, one activation scale.
 template <int RT, int CT, int WM, int WN>
-__device__ __forceinline__ void mmq_fetch(const ActView& act, int K, int b, int tid,
-                                          const int (&arow)[MmqTile<RT, CT, WM, WN>::A_PT],
-                                          const uint8_t* const (&wrow)[MmqTile<RT, CT, WM, WN>::W_PT], int dxrow,
-                                          uint4 (&ra)[MmqTile<RT, CT, WM, WN>::A_PT],
-                                          uint4 (&rw)[MmqTile<RT, CT, WM, WN>::W_PT], float& rdx) {
+struct MmqRegs {
     using T = MmqTile<RT, CT, WM, WN>;
-    const int KB = K / QK_K;
+    uint4 a[T::A_PT], w[T::W_PT];
+    float dx;
+};
+
+// Global loads of superblock b: 32-bit per-lane offsets from uniform base
+// pointers (the SGPR-base addressing form: no 64-bit address arithmetic per
+// load).  aoff < 0 marks a padding row (staged as zeros).
+template <int RT, int CT, int WM, int WN>
+__device__ __forceinline__ void mmq_fetch(const int8_t* __restrict__ qs, const float* __restrict__ dv,
+                                          const uint8_t* __restrict__ wbase, int b, int tid,
+                                          const int (&aoff)[MmqTile<RT, CT, WM, WN>::A_PT],
+                                          const uint32_t (&woff)[MmqTile<RT, CT, WM, WN>::W_PT], int dxoff,
+                                          MmqRegs<RT, CT, WM, WN>& g) {
+    using T = MmqTile<RT, CT, WM, WN>;
+    const uint32_t ab = (uint32_t)b * QK_K, wb = (uint32_t)b * Q4K_BYTES;
 #pragma unroll
     for (int i = 0; i < T::A_PT; i++) {
-        const int ch = (tid + i * T::NT) & 15;
-        ra[i] = uint4{0u, 0u, 0u, 0u};
-        if (arow[i] >= 0)
-            ra[i] = *reinterpret_cast<const uint4*>(act.qs + (size_t)arow[i] * K + (size_t)b * QK_K + 16 * ch);
+        g.a[i] = uint4{0u, 0u, 0u, 0u};  // (set on every path: a conditionally-set array lives in scratch)
+        if (aoff[i] >= 0) g.a[i] = *reinterpret_cast<const uint4*>(qs + ((uint32_t)aoff[i] + ab));
+    }
+#pragma unroll
+    for (int i = 0; i < T::W_PT; i++) {
+        g.w[i] = uint4{0u, 0u, 0u, 0u};
+        if (tid + i * T::NT < T::W_CH) g.w[i] = *reinterpret_cast<const uint4*>(wbase + (woff[i] + wb));
+    }
+    g.dx = dxoff >= 0 ? dv[(uint32_t)dxoff + (uint32_t)b] : 0.0f;
+}
+
+// Registers -> LDS buffer.
+template <int RT, int CT, int WM, int WN>
+__device__ __forceinline__ void mmq_stage(uint8_t* buf, int tid, const MmqRegs<RT, CT, WM, WN>& g) {
+    using T = MmqTile<RT, CT, WM, WN>;
+    int8_t* s_a = reinterpret_cast<int8_t*>(buf);
+    uint8_t* s_w = buf + T::LDS_A;
+    float* s_d = reinterpret_cast<float*>(buf + T::LDS_A + T::LDS_W);
+#pragma unroll
+    for (int i = 0; i < T::A_PT; i++) {
+        const int idx = tid + i * T::NT;
+        if (idx < T::A_CH) *reinterpret_cast<uint4*>(s_a + (idx >> 4) * A_STRIDE + 16 * (idx & 15)) = g.a[i];
     }
 #pragma unroll
     for (int i = 0; i < T::W_PT; i++) {
         const int idx = tid + i * T::NT;
-        rw[i] = uint4{0u, 0u, 0u, 0u};  // (a conditionally-set array would live in scratch)
-        if (idx < T::W_CH) rw[i] = *reinterpret_cast<const uint4*>(wrow[i] + (size_t)b * Q4K_BYTES + 16 * (idx % 9));
+        if (idx < T::W_CH) *reinterpret_cast<uint4*>(s_w + (idx / 9) * Q4K_BYTES + 16 * (idx % 9)) = g.w[i];
     }
-    rdx = dxrow >= 0 ? act.d[(size_t)dxrow * KB + b] : 0.0f;
+    if (tid < T::BM) s_d[tid] = g.dx;
 }
 
-template <int RT, int CT, int WM, int WN>
-__device__ __forceinline__ void mmq_stage(int8_t* s_a, uint8_t* s_w, float* s_dx, int tid,
-                                          const uint4 (&ra)[MmqTile<RT, CT, WM, WN>::A_PT],
-                                          const uint4 (&rw)[MmqTile<RT, CT, WM, WN>::W_PT], float rdx) {
-    using T = MmqTile<RT, CT, WM, WN>;
-#pragma unroll
-    for (int i = 0; i < T::A_PT; i++) {
-        const int idx = tid + i * T::NT;
-        if (idx < T::A_CH) *reinterpret_cast<uint4*>(s_a + (idx >> 4) * A_STRIDE + 16 * (idx & 15)) = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < T::W_PT; i++) {
-        const int idx = tid + i * T::NT;
-        if (idx < T::W_CH) *reinterpret_cast<uint4*>(s_w + (idx / 9) * Q4K_BYTES + 16 * (idx % 9)) = rw[i];
-    }
-    if (tid < T::BM) s_dx[tid] = rdx;
-}
-
-// grid = (M tiles, N tiles, K splits).  With ksplit > 1 each workgroup sums a
-// contiguous range of superblocks into part[split][M][N]; mmq_reduce_kernel
-// adds the splits in order afterwards (deterministic).
-// GROUPED (MoE): workgroup x is tile x of the expert-sorted rows (g.tile_*);
-// its rows end at its expert's end offset, its weights are that expert's, and
-// activation row m is g.x_row[m] (gathered token rows) when x_row is set.
+// grid: non-grouped, a 1-D list of (M tile, N tile, K split) tiles in an
+// XCD-aware order (consecutive workgroups go to different XCDs on MI355X, so
+// tile t of XCD x is x's own contiguous range: the M tiles sharing a weight
+// tile share that XCD's L2).  With ksplit > 1 each workgroup sums a contiguous
+// range of superblocks into part[split][M][N]; mmq_reduce_kernel adds the
+// splits in order afterwards (deterministic).
+// GROUPED (MoE): grid (tile table bound, N tiles); workgroup x takes tile x of
+// the expert-sorted rows (g.tile_*); its rows end at its expert's end offset,
+// its weights are that expert's, and activation row m is g.x_row[m] (gathered
+// token rows) when x_row is set.
 template <int RT, int CT, int WM, int WN, bool GROUPED>
 __global__ __launch_bounds__(64 * WM * WN) void mmq_q4k_kernel(const uint8_t* __restrict__ W, ActView act,
-                                                               float* __restrict__ y, int M, int N, int K,
-                                                               int ldy, MmqGroup g) {
+                                                               float* __restrict__ y, int M, int N, int K, int ldy,
+                                                               int mt, int nt, int nsplit, MmqGroup g) {
     using T = MmqTile<RT, CT, WM, WN>;
     constexpr int BM = T::BM, BN = T::BN;
-    __shared__ __align__(16) int8_t s_a[BM * A_STRIDE];
-    __shared__ __align__(16) uint8_t s_w[BN * Q4K_BYTES];
-    __shared__ float s_dx[BM];
+    __shared__ __align__(16) uint8_t smem[2 * T::LDS_BUF];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
-    const int n0 = blockIdx.y * BN;
     const int KB = K / QK_K;
     const size_t row_bytes = (size_t)KB * Q4K_BYTES;
-    const int nsplit = gridDim.z;
-    const int b0 = (int)((long long)KB * blockIdx.z / nsplit), b1 = (int)((long long)KB * (blockIdx.z + 1) / nsplit);
     const int l16 = lane & 15, kb = lane >> 4;
 
-    int m0 = blockIdx.x * BM, mend = M, n_split = N;
+    int mtile, ntile, split;
+    if constexpr (GROUPED) {
+        mtile = blockIdx.x;
+        ntile = blockIdx.y;
+        split = 0;
+    } else {
+        const int total = mt * nt * nsplit, L = blockIdx.x;
+        const int x = L & 7, slot = L >> 3, q = total >> 3, r = total & 7;
+        const int t = x * q + (x < r ? x : r) + slot;  // XCD x's contiguous range of tiles
+        mtile = t % mt;
+        ntile = (t / mt) % nt;
+        split = t / (mt * nt);
+    }
+    const int b0 = (int)((long long)KB * split / nsplit), b1 = (int)((long long)KB * (split + 1) / nsplit);
+    const int n0 = ntile * BN;
+    int m0 = mtile * BM, mend = M, n_split = N;
     const uint8_t* W1 = W;
     const uint8_t* W2 = W;
     const int* x_row = nullptr;
     if constexpr (GROUPED) {
-        const int tile = blockIdx.x;
-        if (tile >= *g.ntiles) return;  // uniform: the tile table is shorter than the grid bound
-        const int e = g.tile_expert[tile];
-        m0 = g.tile_row0[tile];
+        if (mtile >= *g.ntiles) return;  // uniform: the tile table is shorter than the grid bound
+        const int e = g.tile_expert[mtile];
+        m0 = g.tile_row0[mtile];
         mend = g.expert_offsets[e + 1];
         W1 = W + (size_t)e * g.expert_bytes;
         W2 = g.w2 ? g.w2 + (size_t)e * g.expert_bytes : W1;
         if (g.w2) n_split = g.n_split;
         x_row = g.x_row;
     }
-    int arow[T::A_PT];
+    // per-thread byte offsets of each staged chunk in superblock 0 (-1: padding row)
+    int aoff[T::A_PT];
 #pragma unroll
     for (int i = 0; i < T::A_PT; i++) {
         const int idx = tid + i * T::NT;
         const int m = m0 + (idx >> 4);
-        arow[i] = idx < T::A_CH && m < mend ? (x_row ? x_row[m] : m) : -1;
+        aoff[i] = idx < T::A_CH && m < mend ? (x_row ? x_row[m] : m) * K + 16 * (idx & 15) : -1;
     }
-    const int dxrow = tid < BM && m0 + tid < mend ? (x_row ? x_row[m0 + tid] : m0 + tid) : -1;
-    const uint8_t* wrow[T::W_PT];
+    const int dxoff = tid < BM && m0 + tid < mend ? (x_row ? x_row[m0 + tid] : m0 + tid) * KB : -1;
+    // the workgroup's columns lie on one side of n_split (a multiple of BN)
+    const bool second = n0 >= n_split;
+    const uint8_t* wbase = second ? W2 : W1;
+    uint32_t woff[T::W_PT];
 #pragma unroll
     for (int i = 0; i < T::W_PT; i++) {
-        int n = n0 + (tid + i * T::NT) / 9;
+        const int idx = tid + i * T::NT;
+        int n = n0 + idx / 9;
         n = n < N ? n : N - 1;  // tail columns re-read a valid block; their outputs are dropped
-        wrow[i] = n < n_split ? W1 + (size_t)n * row_bytes : W2 + (size_t)(n - n_split) * row_bytes;
+        woff[i] = (uint32_t)(second ? n - n_split : n) * (uint32_t)row_bytes + 16u * (uint32_t)(idx % 9);
     }
 
     float facc[RT][CT][4];
@@ -147,36 +190,35 @@ __global__ __launch_bounds__(64 * WM * WN) void mmq_q4k_kernel(const uint8_t* __
 #pragma unroll
             for (int i = 0; i < 4; i++) facc[r][c][i] = 0.0f;
 
-    uint4 ra[T::A_PT], rw[T::W_PT];
-    float rdx;
-    if (b0 < b1) mmq_fetch<RT, CT, WM, WN>(act, K, b0, tid, arow, wrow, dxrow, ra, rw, rdx);
+    MmqRegs<RT, CT, WM, WN> regs;
+    if (b0 < b1) {
+        mmq_fetch<RT, CT, WM, WN>(act.qs, act.d, wbase, b0, tid, aoff, woff, dxoff, regs);
+        mmq_stage<RT, CT, WM, WN>(smem, tid, regs);
+    }
+    __syncthreads();
 
     for (int b = b0; b < b1; b++) {
-        __syncthreads();  // the previous superblock's LDS reads are done
-        mmq_stage<RT, CT, WM, WN>(s_a, s_w, s_dx, tid, ra, rw, rdx);
-        __syncthreads();
-        if (b + 1 < b1) mmq_fetch<RT, CT, WM, WN>(act, K, b + 1, tid, arow, wrow, dxrow, ra, rw, rdx);
+        uint8_t* buf = smem + ((b - b0) & 1) * T::LDS_BUF;
+        const bool more = b + 1 < b1;
+        if (more) mmq_fetch<RT, CT, WM, WN>(act.qs, act.d, wbase, b + 1, tid, aoff, woff, dxoff, regs);  // in flight
+        const int8_t* s_a = reinterpret_cast<const int8_t*>(buf);
+        const uint8_t* s_w = buf + T::LDS_A;
+        const float* s_d = reinterpret_cast<const float*>(buf + T::LDS_A + T::LDS_W);
 
-        v4i ia[RT][CT], ib[RT][CT], im[RT][CT];
-#pragma unroll
-        for (int r = 0; r < RT; r++)
-#pragma unroll
-            for (int c = 0; c < CT; c++) {
-                ia[r][c] = v4i{0, 0, 0, 0};
-                ib[r][c] = v4i{0, 0, 0, 0};
-                im[r][c] = v4i{0, 0, 0, 0};
-            }
-
-        // per column tile: this lane's column header -> scale / min bytes
+        v4i ia[RT][CT], ib[RT][CT], im[RT][CT];  // set by the first K step (zero accumulator input)
+        const v4i zero = v4i{0, 0, 0, 0};
+        // per column tile: this lane's column header -> scale / min bytes, d / dmin
         uint32_t scw[CT][2], mnw[CT][2];
+        float dw[CT], dmw[CT];
 #pragma unroll
         for (int c = 0; c < CT; c++) {
-            const uint8_t* blk = s_w + (wn * CT * 16 + c * 16 + l16) * Q4K_BYTES;
-            const uint4 hd = *reinterpret_cast<const uint4*>(blk);
-            scw[c][0] = hd.y & 0x3f3f3f3fu;                                             // scales 0..3
-            scw[c][1] = (hd.w & 0x0f0f0f0fu) | (((hd.y >> 6) & 0x03030303u) << 4);      // scales 4..7
-            mnw[c][0] = hd.z & 0x3f3f3f3fu;                                             // mins 0..3
+            const uint4 hd = *reinterpret_cast<const uint4*>(s_w + (wn * CT * 16 + c * 16 + l16) * Q4K_BYTES);
+            scw[c][0] = hd.y & 0x3f3f3f3fu;                                                 // scales 0..3
+            scw[c][1] = (hd.w & 0x0f0f0f0fu) | (((hd.y >> 6) & 0x03030303u) << 4);          // scales 4..7
+            mnw[c][0] = hd.z & 0x3f3f3f3fu;                                                 // mins 0..3
             mnw[c][1] = ((hd.w >> 4) & 0x0f0f0f0fu) | (((hd.z >> 6) & 0x03030303u) << 4);  // mins 4..7
+            dw[c] = f16_to_f32(hd.x & 0xffffu);
+            dmw[c] = f16_to_f32(hd.x >> 16);
         }
 
 #pragma unroll
@@ -184,10 +226,9 @@ __global__ __launch_bounds__(64 * WM * WN) void mmq_q4k_kernel(const uint8_t* __
             const int j = 2 * t + (kb >> 1);
             v4i afr[RT];
 #pragma unroll
-            for (int r = 0; r < RT; r++) {
-                const int8_t* pa = s_a + (wm * RT * 16 + r * 16 + l16) * A_STRIDE + 64 * t + 16 * kb;
-                afr[r] = *reinterpret_cast<const v4i*>(pa);
-            }
+            for (int r = 0; r < RT; r++)
+                afr[r] = *reinterpret_cast<const v4i*>(s_a + (wm * RT * 16 + r * 16 + l16) * A_STRIDE + 64 * t +
+                                                       16 * kb);
 #pragma unroll
             for (int c = 0; c < CT; c++) {
                 const uint8_t* blk = s_w + (wn * CT * 16 + c * 16 + l16) * Q4K_BYTES;
@@ -201,38 +242,37 @@ __global__ __launch_bounds__(64 * WM * WN) void mmq_q4k_kernel(const uint8_t* __
                 const uint32_t a = sc >> 3, bb = sc & 7u;
                 const uint32_t q0 = (raw.x >> sh) & 0x0f0f0f0fu, q1 = (raw.y >> sh) & 0x0f0f0f0fu;
                 const uint32_t q2 = (raw.z >> sh) & 0x0f0f0f0fu, q3 = (raw.w >> sh) & 0x0f0f0f0fu;
-                const v4i ba = v4i{(int)(q0 * a), (int)(q1 * a), (int)(q2 * a), (int)(q3 * a)};
-                const v4i bbv = v4i{(int)(q0 * bb), (int)(q1 * bb), (int)(q2 * bb), (int)(q3 * bb)};
-                const int mb = (int)(mn * 0x01010101u);
+                const v4i ba = v4i{bytes_times(q0, a), bytes_times(q1, a), bytes_times(q2, a), bytes_times(q3, a)};
+                const v4i bbv = v4i{bytes_times(q0, bb), bytes_times(q1, bb), bytes_times(q2, bb), bytes_times(q3, bb)};
+                const int mb = (int)(__builtin_amdgcn_perm(0u, mn, 0x00000000u));  // the byte in all four lanes
                 const v4i bm = v4i{mb, mb, mb, mb};
 #pragma unroll
                 for (int r = 0; r < RT; r++) {
-                    ia[r][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r], ba, ia[r][c], 0, 0, 0);
-                    ib[r][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r], bbv, ib[r][c], 0, 0, 0);
-                    im[r][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r], bm, im[r][c], 0, 0, 0);
+                    ia[r][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r], ba, t == 0 ? zero : ia[r][c], 0, 0, 0);
+                    ib[r][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r], bbv, t == 0 ? zero : ib[r][c], 0, 0, 0);
+                    im[r][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r], bm, t == 0 ? zero : im[r][c], 0, 0, 0);
                 }
             }
         }
 
-        // ---- f32 step: y += d_w*d_x*isum - dmin_w*d_x*msum ----
+        // ---- f32 step: y += d_x * (d_w*isum - dmin_w*msum) ----
 #pragma unroll
-        for (int c = 0; c < CT; c++) {
-            const uint8_t* blk = s_w + (wn * CT * 16 + c * 16 + l16) * Q4K_BYTES;
-            const uint32_t dd = *reinterpret_cast<const uint32_t*>(blk);
-            const float dw = f16_to_f32(dd & 0xffffu), dmw = f16_to_f32(dd >> 16);
+        for (int r = 0; r < RT; r++)
 #pragma unroll
-            for (int r = 0; r < RT; r++)
+            for (int i = 0; i < 4; i++) {
+                const float dx = s_d[wm * RT * 16 + r * 16 + 4 * kb + i];
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float dx = s_dx[wm * RT * 16 + r * 16 + 4 * kb + i];
+                for (int c = 0; c < CT; c++) {
                     const int isum = 8 * ia[r][c][i] + ib[r][c][i];
-                    facc[r][c][i] = fmaf(dw * dx, (float)isum, facc[r][c][i]);
-                    facc[r][c][i] = fmaf(-(dmw * dx), (float)im[r][c][i], facc[r][c][i]);
+                    const float t = fmaf(-dmw[c], (float)im[r][c][i], dw[c] * (float)isum);
+                    facc[r][c][i] = fmaf(dx, t, facc[r][c][i]);
                 }
-        }
+            }
+        if (more) mmq_stage<RT, CT, WM, WN>(smem + ((b + 1 - b0) & 1) * T::LDS_BUF, tid, regs);
+        __syncthreads();
     }
 
-    float* out = nsplit > 1 ? y + (size_t)blockIdx.z * M * N : y;  // split partials: [z][M][N]
+    float* out = nsplit > 1 ? y + (size_t)split * M * N : y;  // split partials: [z][M][N]
     const int ld = nsplit > 1 ? N : ldy;
 #pragma unroll
     for (int r = 0; r < RT; r++)
@@ -272,9 +312,8 @@ hipError_t launch_cfg(const uint8_t* w, ActView act, float* y, float* part, size
         if (ks > kmax) ks = kmax;
         while (ks > 1 && (size_t)ks * M * N > part_elems) ks--;
     }
-    dim3 grid(mt, nt, ks);
-    hipLaunchKernelGGL((mmq_q4k_kernel<RT, CT, WM, WN, false>), grid, dim3(T::NT), 0, s, w, act, ks > 1 ? part : y,
-                       M, N, K, ldy, MmqGroup{});
+    hipLaunchKernelGGL((mmq_q4k_kernel<RT, CT, WM, WN, false>), dim3(mt * nt * ks), dim3(T::NT), 0, s, w, act,
+                       ks > 1 ? part : y, M, N, K, ldy, mt, nt, ks, MmqGroup{});
     if (ks > 1) {
         const size_t total = (size_t)M * N;
         hipLaunchKernelGGL(mmq_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, y, M, N,
@@ -288,7 +327,8 @@ hipError_t launch_grouped_cfg(const uint8_t* w, ActView act, float* y, int max_t
                               const MmqGroup& g, hipStream_t s) {
     using T = MmqTile<RT, CT, WM, WN>;
     dim3 grid(max_tiles, (N + T::BN - 1) / T::BN, 1);
-    hipLaunchKernelGGL((mmq_q4k_kernel<RT, CT, WM, WN, true>), grid, dim3(T::NT), 0, s, w, act, y, 0, N, K, ldy, g);
+    hipLaunchKernelGGL((mmq_q4k_kernel<RT, CT, WM, WN, true>), grid, dim3(T::NT), 0, s, w, act, y, 0, N, K, ldy, 0, 0,
+                       1, g);
     return hipGetLastError();
 }
 
@@ -299,6 +339,7 @@ int mmq_group_rows(int rows_per_expert) { return rows_per_expert >= 24 ? 32 : 16
 hipError_t launch_mmq_grouped(int dtype, const uint8_t* w, ActView act, float* y, int bm, int max_tiles, int N, int K,
                               int ldy, const MmqGroup& g, hipStream_t s) {
     if (dtype != GGML_Q4K || max_tiles <= 0) return max_tiles == 0 ? hipSuccess : hipErrorInvalidValue;
+    if (g.w2 && g.n_split % 64) return hipErrorInvalidValue;  // a column tile must not straddle W | W2
     if (bm == 32) return launch_grouped_cfg<2, 1, 1, 4>(w, act, y, max_tiles, N, K, ldy, g, s);  // 32 x 64
     if (bm == 16) return launch_grouped_cfg<1, 1, 1, 4>(w, act, y, max_tiles, N, K, ldy, g, s);  // 16 x 64
     return hipErrorInvalidValue;
