@@ -163,7 +163,9 @@ int run_qmatmul(frq_device* dev, int t, const uint8_t* w, const float* x, size_t
     // for the k-quants (4 lanes per superblock), K <= 8 * 32 * 32 for Q8_0
     const size_t kmax = t == GGML_Q8_0 ? 8192 : 32768;
     if (k > kmax) return fail(FRQ_UNSUPPORTED, "qmatmul: k=%zu exceeds %zu for dtype %d", k, kmax, t);
-    if (rows >= MMQ_MIN_ROWS && mmq_supported(t)) {
+    // the MFMA kernel addresses the weights with 32-bit offsets
+    const bool w32 = n * (k / block_elems(t)) * type_size(t) <= 0xffffffffull;
+    if (rows >= MMQ_MIN_ROWS && mmq_supported(t) && w32) {
         // many activation rows: quantize them once, then the int8-MFMA GEMM
         // workspace: quantized rows, then the split-K partial sums
         const size_t abytes = align256(act_bytes(vec_dot_type(t), rows, k));

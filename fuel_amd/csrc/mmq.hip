@@ -1,19 +1,28 @@
 // Batched / prefill quantized matmul (M >= 16) on gfx950 int8 MFMA:
-// fuel's matmul<BlockQ4K> (k_quants.rs:2284-2331) for many activation rows.
+// fuel's matmul<BlockQ4K> and matmul<BlockQ6K> (k_quants.rs:2284-2331) for
+// many activation rows, with the same per-superblock integer sums as the
+// scalar vec_dots (k_quants.rs:1388-1468, 1946-2003) and one f32 step per
+// superblock.  Activations are Q8K rows (one int8 per element, one f32 scale
+// per 256), quantized once per call.
 //
-// Exact integer formulation.  Per superblock b, with q4 the weight nibbles,
-// sc_j / m_j the 6-bit scale / min of sub-block j and q8 the Q8K activation:
+// Q4_K.  Per superblock, with q4 the weight nibbles, sc_j / m_j the 6-bit
+// scale / min of sub-block j and q8 the activation:
 //   isum = sum_j sc_j * sum_{e in j} q4_e q8_e ,  msum = sum_j m_j * S_j
-// with S_j = sum_{e in j} q8_e (two of the activation's 16-element bsums).
-// A 6-bit scale times a nibble does not fit int8, so sc_j = 8*a_j + b_j with
-// a_j, b_j <= 7: q4*a_j and q4*b_j are <= 105 and a dword holding four nibbles
-// can be multiplied by a_j without carries between its bytes.  Then
+// with S_j = sum_{e in j} q8_e.  A 6-bit scale times a nibble does not fit
+// int8, so sc_j = 8*a_j + b_j with a_j, b_j <= 7: q4*a_j and q4*b_j are <= 105
+// and fit a byte.  Then
 //   isum = 8 * (X . Ba) + (X . Bb),   msum = X . Bm
 // with Bm the sub-block mins broadcast over their 32 elements: three int8
-// GEMMs over K = 256 per superblock on v_mfma_i32_16x16x64_i8, exact in int32.
-// (The kernel is bound by its VALU work, not the matrix cores: msum on the
-// MFMA pipe costs less than its 8-term dot products on the VALU.)  Then one
-// f32 step per superblock: y += d_x * (d_w*isum - dmin_w*msum).
+// GEMMs over K = 256 per superblock, exact in int32.  (The kernel is bound by
+// its VALU work, not the matrix cores: msum on the MFMA pipe costs less than
+// its 8-term dot products on the VALU.)  f32 step: y += d_x*(d*isum - dmin*msum).
+//
+// Q6_K.  w_e = (q6_e - 32) * sc_g, with sc_g the int8 scale of 16-element
+// group g, lies in [-4096, 4064]: split w = 128*wh + wl with wl = w & 127 in
+// [0, 127] and wh = w >> 7 (arithmetic) in [-32, 31], both bytes, so
+//   isum = 128 * (X . Wh) + (X . Wl)
+// is two exact int8 GEMMs.  The products are formed two per 16-bit lane with
+// one packed multiply-add.  f32 step: y += d_x * (d * isum).
 //
 // Workgroup: WM x WN wavefronts, each owning RT x CT tiles of 16x16 outputs.
 // Per superblock the workgroup stages the quantized activation rows (272-byte
@@ -21,7 +30,7 @@
 // LDS, double-buffered: the next superblock's global loads are in
 // flight while the current one is multiplied, and one barrier per superblock
 // separates the two buffers' roles.  Lanes build their B fragments in
-// registers from the raw nibbles.
+// registers from the raw blocks.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -29,6 +38,9 @@ namespace frq {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x2 __attribute__((ext_vector_type(2)));
+
+namespace {
 
 // Four nibble bytes (<= 15) times a small factor (<= 7), byte by byte: each
 // product is <= 105, so two 16-bit lane multiplies (one full-rate packed
@@ -38,28 +50,151 @@ __device__ __forceinline__ int bytes_times(uint32_t q, uint32_t f) {
     return __builtin_bit_cast(int, p);
 }
 
-namespace {
+// Four 6-bit codes u (bytes of q, <= 63) -> w = (u - 32) * sc split into the
+// byte planes wl = w & 127 and wh = w >> 7.  Each 16-bit lane holds one
+// product exactly (|w| <= 4096), so the arithmetic runs two codes per packed
+// instruction: even bytes, then odd bytes.
+__device__ __forceinline__ void q6_planes(uint32_t q, uint32_t sc16, uint32_t c16, int& wl, int& wh) {
+    const u16x2 ev = __builtin_bit_cast(u16x2, q & 0x00ff00ffu);
+    const u16x2 od = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(0u, q, 0x0c030c01u));  // bytes 1, 3
+    const u16x2 f = __builtin_bit_cast(u16x2, sc16), c = __builtin_bit_cast(u16x2, c16);
+    const u16x2 pe = ev * f + c, po = od * f + c;  // (u - 32) * sc mod 2^16
+    // interleave the low bytes of the four lanes back into code order
+    const uint32_t sel = 0x06020400u;  // [pe.b0, po.b0, pe.b2, po.b2]
+    wl = (int)(__builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, po), __builtin_bit_cast(uint32_t, pe), sel) &
+               0x7f7f7f7fu);
+    const i16x2 he = __builtin_bit_cast(i16x2, pe) >> (short)7, ho = __builtin_bit_cast(i16x2, po) >> (short)7;
+    wh = (int)__builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, ho), __builtin_bit_cast(uint32_t, he), sel);
+}
 
 constexpr int A_STRIDE = QK_K + 16;  // LDS bytes per activation row per superblock
 
-template <int RT, int CT, int WM, int WN>
+// ---- format policies ----
+// CH 16-byte chunks are staged per column and superblock: chunk ch comes from
+// global byte src(ch) of the block and lands at LDS byte 16*ch of the
+// column's STRIDE-byte slot.
+
+struct MmqQ4K {
+    static constexpr int BYTES = Q4K_BYTES, STRIDE = Q4K_BYTES, CH = 9, NACC = 3;
+    __device__ static uint32_t src(int ch) { return 16u * (uint32_t)ch; }
+    struct Hdr {
+        uint32_t sc[2], mn[2];  // 6-bit scales / mins of sub-blocks 0..3, 4..7 (one byte each)
+        float d, dmin;
+    };
+    __device__ static void header(const uint8_t* col, Hdr& h) {
+        const uint4 hd = *reinterpret_cast<const uint4*>(col);
+        h.sc[0] = hd.y & 0x3f3f3f3fu;
+        h.sc[1] = (hd.w & 0x0f0f0f0fu) | (((hd.y >> 6) & 0x03030303u) << 4);
+        h.mn[0] = hd.z & 0x3f3f3f3fu;
+        h.mn[1] = ((hd.w >> 4) & 0x0f0f0f0fu) | (((hd.z >> 6) & 0x03030303u) << 4);
+        h.d = f16_to_f32(hd.x & 0xffffu);
+        h.dmin = f16_to_f32(hd.x >> 16);
+    }
+    // K step t (elements 64t..64t+63): lane group kb holds elements 64t+16kb+[0,16).
+    template <int RT, int CT>
+    __device__ static void step(int t, int kb, int c, const uint8_t* col, const Hdr& h, const v4i (&afr)[RT],
+                                v4i (&acc)[RT][CT][NACC]) {
+        // element 64t + 16kb + i lives in qs[32t + 16(kb&1) + i], nibble kb>>1
+        const uint4 raw = *reinterpret_cast<const uint4*>(col + 16 + 32 * t + 16 * (kb & 1));
+        const uint32_t sh = 4u * (uint32_t)(kb >> 1);
+        // sub-block j = 2t + (kb>>1) sits in word t>>1 (compile-time), byte j&3
+        const uint32_t jsh = 8u * (uint32_t)((2 * t + (kb >> 1)) & 3);
+        const uint32_t sc = (h.sc[t >> 1] >> jsh) & 0xffu;
+        const uint32_t mn = (h.mn[t >> 1] >> jsh) & 0xffu;
+        const uint32_t a = sc >> 3, bb = sc & 7u;
+        const uint32_t q0 = (raw.x >> sh) & 0x0f0f0f0fu, q1 = (raw.y >> sh) & 0x0f0f0f0fu;
+        const uint32_t q2 = (raw.z >> sh) & 0x0f0f0f0fu, q3 = (raw.w >> sh) & 0x0f0f0f0fu;
+        const v4i ba = v4i{bytes_times(q0, a), bytes_times(q1, a), bytes_times(q2, a), bytes_times(q3, a)};
+        const v4i bbv = v4i{bytes_times(q0, bb), bytes_times(q1, bb), bytes_times(q2, bb), bytes_times(q3, bb)};
+        const int mb = (int)(__builtin_amdgcn_perm(0u, mn, 0x00000000u));  // the byte in all four lanes
+        const v4i bm = v4i{mb, mb, mb, mb};
+        const v4i zero = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            acc[r][c][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r], ba, t == 0 ? zero : acc[r][c][0], 0, 0, 0);
+            acc[r][c][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r], bbv, t == 0 ? zero : acc[r][c][1], 0, 0, 0);
+            acc[r][c][2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r], bm, t == 0 ? zero : acc[r][c][2], 0, 0, 0);
+        }
+    }
+    // d*isum - dmin*msum of output element i of the lane's 16x16 tile
+    __device__ static float finish(const v4i (&a)[NACC], int i, const Hdr& h) {
+        const int isum = 8 * a[0][i] + a[1][i];
+        return fmaf(-h.dmin, (float)a[2][i], h.d * (float)isum);
+    }
+};
+
+struct MmqQ6K {
+    // 210-byte blocks sit at 2-byte alignment: chunks 0..12 are bytes
+    // 0..207 (ql, qh, scales) and chunk 13 is bytes 194..209, which puts d at
+    // LDS byte 222 and never reads past the block.
+    static constexpr int BYTES = Q6K_BYTES, STRIDE = 224, CH = 14, NACC = 2;
+    __device__ static uint32_t src(int ch) { return ch < 13 ? 16u * (uint32_t)ch : 194u; }
+    struct Hdr {
+        uint32_t sc[4];  // int8 scales 4t..4t+3 in word t
+        float d;
+    };
+    __device__ static void header(const uint8_t* col, Hdr& h) {
+        const uint4 s = *reinterpret_cast<const uint4*>(col + 192);
+        h.sc[0] = s.x;
+        h.sc[1] = s.y;
+        h.sc[2] = s.z;
+        h.sc[3] = s.w;
+        h.d = f16_to_f32(*reinterpret_cast<const uint16_t*>(col + 222));
+    }
+    // Element 64t + 16kb + i is element 128hh + 32qd + l of fuel's layout
+    // (k_quants.rs:2170-2186) with hh = t>>1, qd = 2(t&1) + (kb>>1),
+    // l = 16(kb&1) + i: low (t even) / high (t odd) nibble of
+    // ql[64hh + 32(kb>>1) + l] and bits 2qd..2qd+1 of qh[32hh + l]; its scale
+    // is scales[4t + kb].
+    template <int RT, int CT>
+    __device__ static void step(int t, int kb, int c, const uint8_t* col, const Hdr& h, const v4i (&afr)[RT],
+                                v4i (&acc)[RT][CT][NACC]) {
+        const uint4 ql = *reinterpret_cast<const uint4*>(col + 64 * (t >> 1) + 32 * (kb >> 1) + 16 * (kb & 1));
+        const uint4 qh = *reinterpret_cast<const uint4*>(col + 128 + 32 * (t >> 1) + 16 * (kb & 1));
+        const uint32_t ls = 4u * (uint32_t)(t & 1);                   // compile-time
+        const uint32_t hs = 4u * (uint32_t)(t & 1) + 2u * (uint32_t)(kb >> 1);
+        const int sc = (int)(int8_t)((h.sc[t] >> (8 * kb)) & 0xffu);
+        const uint32_t f = (uint32_t)sc & 0xffffu, cst = (uint32_t)(-32 * sc) & 0xffffu;
+        const uint32_t sc16 = f | (f << 16), c16 = cst | (cst << 16);
+        const uint32_t l4[4] = {ql.x, ql.y, ql.z, ql.w}, h4[4] = {qh.x, qh.y, qh.z, qh.w};
+        int wl[4], wh[4];
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+            const uint32_t u = ((l4[d] >> ls) & 0x0f0f0f0fu) | (((h4[d] >> hs) & 0x03030303u) << 4);
+            q6_planes(u, sc16, c16, wl[d], wh[d]);
+        }
+        const v4i bh = v4i{wh[0], wh[1], wh[2], wh[3]}, bl = v4i{wl[0], wl[1], wl[2], wl[3]};
+        const v4i zero = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            acc[r][c][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r], bh, t == 0 ? zero : acc[r][c][0], 0, 0, 0);
+            acc[r][c][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r], bl, t == 0 ? zero : acc[r][c][1], 0, 0, 0);
+        }
+    }
+    __device__ static float finish(const v4i (&a)[NACC], int i, const Hdr& h) {
+        const int isum = 128 * a[0][i] + a[1][i];
+        return h.d * (float)isum;
+    }
+};
+
+template <class F, int RT, int CT, int WM, int WN>
 struct MmqTile {
     static constexpr int NT = 64 * WM * WN;
     static constexpr int BM = 16 * RT * WM, BN = 16 * CT * WN;
-    static constexpr int A_CH = BM * 16;  // 16-byte activation chunks per superblock
-    static constexpr int W_CH = BN * 9;   // 16-byte weight chunks per superblock
+    static constexpr int A_CH = BM * 16;     // 16-byte activation chunks per superblock
+    static constexpr int W_CH = BN * F::CH;  // 16-byte weight chunks per superblock
     static constexpr int A_PT = (A_CH + NT - 1) / NT;
     static constexpr int W_PT = (W_CH + NT - 1) / NT;
     // LDS per buffer: activations, weights, activation scales
-    static constexpr int LDS_A = BM * A_STRIDE, LDS_W = BN * Q4K_BYTES, LDS_D = BM * 4;
+    static constexpr int LDS_A = BM * A_STRIDE, LDS_W = BN * F::STRIDE, LDS_D = BM * 4;
     static constexpr int LDS_BUF = LDS_A + LDS_W + LDS_D;
 };
 
 // Register copy of one superblock's share of a thread: activation chunks,
 // weight chunks, one activation scale.
-template <int RT, int CT, int WM, int WN>
+template <class F, int RT, int CT, int WM, int WN>
 struct MmqRegs {
-    using T = MmqTile<RT, CT, WM, WN>;
+    using T = MmqTile<F, RT, CT, WM, WN>;
     uint4 a[T::A_PT], w[T::W_PT];
     float dx;
 };
@@ -67,14 +202,14 @@ struct MmqRegs {
 // Global loads of superblock b: 32-bit per-lane offsets from uniform base
 // pointers (the SGPR-base addressing form: no 64-bit address arithmetic per
 // load).  aoff < 0 marks a padding row (staged as zeros).
-template <int RT, int CT, int WM, int WN>
+template <class F, int RT, int CT, int WM, int WN>
 __device__ __forceinline__ void mmq_fetch(const int8_t* __restrict__ qs, const float* __restrict__ dv,
                                           const uint8_t* __restrict__ wbase, int b, int tid,
-                                          const int (&aoff)[MmqTile<RT, CT, WM, WN>::A_PT],
-                                          const uint32_t (&woff)[MmqTile<RT, CT, WM, WN>::W_PT], int dxoff,
-                                          MmqRegs<RT, CT, WM, WN>& g) {
-    using T = MmqTile<RT, CT, WM, WN>;
-    const uint32_t ab = (uint32_t)b * QK_K, wb = (uint32_t)b * Q4K_BYTES;
+                                          const int (&aoff)[MmqTile<F, RT, CT, WM, WN>::A_PT],
+                                          const uint32_t (&woff)[MmqTile<F, RT, CT, WM, WN>::W_PT], int dxoff,
+                                          MmqRegs<F, RT, CT, WM, WN>& g) {
+    using T = MmqTile<F, RT, CT, WM, WN>;
+    const uint32_t ab = (uint32_t)b * QK_K, wb = (uint32_t)b * F::BYTES;
 #pragma unroll
     for (int i = 0; i < T::A_PT; i++) {
         g.a[i] = uint4{0u, 0u, 0u, 0u};  // (set on every path: a conditionally-set array lives in scratch)
@@ -83,15 +218,15 @@ __device__ __forceinline__ void mmq_fetch(const int8_t* __restrict__ qs, const f
 #pragma unroll
     for (int i = 0; i < T::W_PT; i++) {
         g.w[i] = uint4{0u, 0u, 0u, 0u};
-        if (tid + i * T::NT < T::W_CH) g.w[i] = *reinterpret_cast<const uint4*>(wbase + (woff[i] + wb));
+        if (tid + i * T::NT < T::W_CH) g.w[i] = load16_u(wbase + (woff[i] + wb));
     }
     g.dx = dxoff >= 0 ? dv[(uint32_t)dxoff + (uint32_t)b] : 0.0f;
 }
 
 // Registers -> LDS buffer.
-template <int RT, int CT, int WM, int WN>
-__device__ __forceinline__ void mmq_stage(uint8_t* buf, int tid, const MmqRegs<RT, CT, WM, WN>& g) {
-    using T = MmqTile<RT, CT, WM, WN>;
+template <class F, int RT, int CT, int WM, int WN>
+__device__ __forceinline__ void mmq_stage(uint8_t* buf, int tid, const MmqRegs<F, RT, CT, WM, WN>& g) {
+    using T = MmqTile<F, RT, CT, WM, WN>;
     int8_t* s_a = reinterpret_cast<int8_t*>(buf);
     uint8_t* s_w = buf + T::LDS_A;
     float* s_d = reinterpret_cast<float*>(buf + T::LDS_A + T::LDS_W);
@@ -103,7 +238,7 @@ __device__ __forceinline__ void mmq_stage(uint8_t* buf, int tid, const MmqRegs<R
 #pragma unroll
     for (int i = 0; i < T::W_PT; i++) {
         const int idx = tid + i * T::NT;
-        if (idx < T::W_CH) *reinterpret_cast<uint4*>(s_w + (idx / 9) * Q4K_BYTES + 16 * (idx % 9)) = g.w[i];
+        if (idx < T::W_CH) *reinterpret_cast<uint4*>(s_w + (idx / F::CH) * F::STRIDE + 16 * (idx % F::CH)) = g.w[i];
     }
     if (tid < T::BM) s_d[tid] = g.dx;
 }
@@ -118,18 +253,18 @@ __device__ __forceinline__ void mmq_stage(uint8_t* buf, int tid, const MmqRegs<R
 // the expert-sorted rows (g.tile_*); its rows end at its expert's end offset,
 // its weights are that expert's, and activation row m is g.x_row[m] (gathered
 // token rows) when x_row is set.
-template <int RT, int CT, int WM, int WN, bool GROUPED>
-__global__ __launch_bounds__(64 * WM * WN) void mmq_q4k_kernel(const uint8_t* __restrict__ W, ActView act,
-                                                               float* __restrict__ y, int M, int N, int K, int ldy,
-                                                               int mt, int nt, int nsplit, MmqGroup g) {
-    using T = MmqTile<RT, CT, WM, WN>;
+template <class F, int RT, int CT, int WM, int WN, bool GROUPED>
+__global__ __launch_bounds__(64 * WM * WN) void mmq_kernel(const uint8_t* __restrict__ W, ActView act,
+                                                           float* __restrict__ y, int M, int N, int K, int ldy,
+                                                           int mt, int nt, int nsplit, MmqGroup g) {
+    using T = MmqTile<F, RT, CT, WM, WN>;
     constexpr int BM = T::BM, BN = T::BN;
     __shared__ __align__(16) uint8_t smem[2 * T::LDS_BUF];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
     const int KB = K / QK_K;
-    const size_t row_bytes = (size_t)KB * Q4K_BYTES;
+    const size_t row_bytes = (size_t)KB * F::BYTES;
     const int l16 = lane & 15, kb = lane >> 4;
 
     int mtile, ntile, split;
@@ -177,9 +312,9 @@ __global__ __launch_bounds__(64 * WM * WN) void mmq_q4k_kernel(const uint8_t* __
 #pragma unroll
     for (int i = 0; i < T::W_PT; i++) {
         const int idx = tid + i * T::NT;
-        int n = n0 + idx / 9;
+        int n = n0 + idx / F::CH;
         n = n < N ? n : N - 1;  // tail columns re-read a valid block; their outputs are dropped
-        woff[i] = (uint32_t)(second ? n - n_split : n) * (uint32_t)row_bytes + 16u * (uint32_t)(idx % 9);
+        woff[i] = (uint32_t)(second ? n - n_split : n) * (uint32_t)row_bytes + F::src(idx % F::CH);
     }
 
     float facc[RT][CT][4];
@@ -190,85 +325,48 @@ __global__ __launch_bounds__(64 * WM * WN) void mmq_q4k_kernel(const uint8_t* __
 #pragma unroll
             for (int i = 0; i < 4; i++) facc[r][c][i] = 0.0f;
 
-    MmqRegs<RT, CT, WM, WN> regs;
+    MmqRegs<F, RT, CT, WM, WN> regs;
     if (b0 < b1) {
-        mmq_fetch<RT, CT, WM, WN>(act.qs, act.d, wbase, b0, tid, aoff, woff, dxoff, regs);
-        mmq_stage<RT, CT, WM, WN>(smem, tid, regs);
+        mmq_fetch<F, RT, CT, WM, WN>(act.qs, act.d, wbase, b0, tid, aoff, woff, dxoff, regs);
+        mmq_stage<F, RT, CT, WM, WN>(smem, tid, regs);
     }
     __syncthreads();
 
     for (int b = b0; b < b1; b++) {
         uint8_t* buf = smem + ((b - b0) & 1) * T::LDS_BUF;
         const bool more = b + 1 < b1;
-        if (more) mmq_fetch<RT, CT, WM, WN>(act.qs, act.d, wbase, b + 1, tid, aoff, woff, dxoff, regs);  // in flight
+        if (more) mmq_fetch<F, RT, CT, WM, WN>(act.qs, act.d, wbase, b + 1, tid, aoff, woff, dxoff, regs);
         const int8_t* s_a = reinterpret_cast<const int8_t*>(buf);
         const uint8_t* s_w = buf + T::LDS_A;
         const float* s_d = reinterpret_cast<const float*>(buf + T::LDS_A + T::LDS_W);
 
-        v4i ia[RT][CT], ib[RT][CT], im[RT][CT];  // set by the first K step (zero accumulator input)
-        const v4i zero = v4i{0, 0, 0, 0};
-        // per column tile: this lane's column header -> scale / min bytes, d / dmin
-        uint32_t scw[CT][2], mnw[CT][2];
-        float dw[CT], dmw[CT];
+        v4i acc[RT][CT][F::NACC];  // set by the first K step (zero accumulator input)
+        typename F::Hdr hdr[CT];   // per column tile: this lane's column header
 #pragma unroll
-        for (int c = 0; c < CT; c++) {
-            const uint4 hd = *reinterpret_cast<const uint4*>(s_w + (wn * CT * 16 + c * 16 + l16) * Q4K_BYTES);
-            scw[c][0] = hd.y & 0x3f3f3f3fu;                                                 // scales 0..3
-            scw[c][1] = (hd.w & 0x0f0f0f0fu) | (((hd.y >> 6) & 0x03030303u) << 4);          // scales 4..7
-            mnw[c][0] = hd.z & 0x3f3f3f3fu;                                                 // mins 0..3
-            mnw[c][1] = ((hd.w >> 4) & 0x0f0f0f0fu) | (((hd.z >> 6) & 0x03030303u) << 4);  // mins 4..7
-            dw[c] = f16_to_f32(hd.x & 0xffffu);
-            dmw[c] = f16_to_f32(hd.x >> 16);
-        }
+        for (int c = 0; c < CT; c++) F::header(s_w + (wn * CT * 16 + c * 16 + l16) * F::STRIDE, hdr[c]);
 
 #pragma unroll
-        for (int t = 0; t < 4; t++) {  // K steps of 64: sub-blocks 2t (kb < 2) and 2t+1 (kb >= 2)
-            const int j = 2 * t + (kb >> 1);
+        for (int t = 0; t < 4; t++) {  // K steps of 64
             v4i afr[RT];
 #pragma unroll
             for (int r = 0; r < RT; r++)
                 afr[r] = *reinterpret_cast<const v4i*>(s_a + (wm * RT * 16 + r * 16 + l16) * A_STRIDE + 64 * t +
                                                        16 * kb);
 #pragma unroll
-            for (int c = 0; c < CT; c++) {
-                const uint8_t* blk = s_w + (wn * CT * 16 + c * 16 + l16) * Q4K_BYTES;
-                // element 64t + 16kb + i lives in qs[32t + 16(kb&1) + i], nibble kb>>1
-                const uint4 raw = *reinterpret_cast<const uint4*>(blk + 16 + 32 * t + 16 * (kb & 1));
-                const uint32_t sh = 4u * (uint32_t)(kb >> 1);
-                // sub-block j = 2t + (kb>>1) sits in word t>>1 (compile-time), byte j&3
-                const uint32_t jsh = 8u * (uint32_t)(j & 3);
-                const uint32_t sc = (scw[c][t >> 1] >> jsh) & 0xffu;
-                const uint32_t mn = (mnw[c][t >> 1] >> jsh) & 0xffu;
-                const uint32_t a = sc >> 3, bb = sc & 7u;
-                const uint32_t q0 = (raw.x >> sh) & 0x0f0f0f0fu, q1 = (raw.y >> sh) & 0x0f0f0f0fu;
-                const uint32_t q2 = (raw.z >> sh) & 0x0f0f0f0fu, q3 = (raw.w >> sh) & 0x0f0f0f0fu;
-                const v4i ba = v4i{bytes_times(q0, a), bytes_times(q1, a), bytes_times(q2, a), bytes_times(q3, a)};
-                const v4i bbv = v4i{bytes_times(q0, bb), bytes_times(q1, bb), bytes_times(q2, bb), bytes_times(q3, bb)};
-                const int mb = (int)(__builtin_amdgcn_perm(0u, mn, 0x00000000u));  // the byte in all four lanes
-                const v4i bm = v4i{mb, mb, mb, mb};
-#pragma unroll
-                for (int r = 0; r < RT; r++) {
-                    ia[r][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r], ba, t == 0 ? zero : ia[r][c], 0, 0, 0);
-                    ib[r][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r], bbv, t == 0 ? zero : ib[r][c], 0, 0, 0);
-                    im[r][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r], bm, t == 0 ? zero : im[r][c], 0, 0, 0);
-                }
-            }
+            for (int c = 0; c < CT; c++)
+                F::template step<RT, CT>(t, kb, c, s_w + (wn * CT * 16 + c * 16 + l16) * F::STRIDE, hdr[c], afr, acc);
         }
 
-        // ---- f32 step: y += d_x * (d_w*isum - dmin_w*msum) ----
+        // ---- f32 step per superblock ----
 #pragma unroll
         for (int r = 0; r < RT; r++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const float dx = s_d[wm * RT * 16 + r * 16 + 4 * kb + i];
 #pragma unroll
-                for (int c = 0; c < CT; c++) {
-                    const int isum = 8 * ia[r][c][i] + ib[r][c][i];
-                    const float t = fmaf(-dmw[c], (float)im[r][c][i], dw[c] * (float)isum);
-                    facc[r][c][i] = fmaf(dx, t, facc[r][c][i]);
-                }
+                for (int c = 0; c < CT; c++) facc[r][c][i] = fmaf(dx, F::finish(acc[r][c], i, hdr[c]), facc[r][c][i]);
             }
-        if (more) mmq_stage<RT, CT, WM, WN>(smem + ((b + 1 - b0) & 1) * T::LDS_BUF, tid, regs);
+        if (more) mmq_stage<F, RT, CT, WM, WN>(smem + ((b + 1 - b0) & 1) * T::LDS_BUF, tid, regs);
         __syncthreads();
     }
 
@@ -297,10 +395,10 @@ __global__ void mmq_reduce_kernel(const float* __restrict__ part, float* __restr
     y[(i / N) * ldy + i % N] = s;
 }
 
-template <int RT, int CT, int WM, int WN>
+template <class F, int RT, int CT, int WM, int WN>
 hipError_t launch_cfg(const uint8_t* w, ActView act, float* y, float* part, size_t part_elems, int M, int N, int K,
                       int ldy, int num_cus, hipStream_t s) {
-    using T = MmqTile<RT, CT, WM, WN>;
+    using T = MmqTile<F, RT, CT, WM, WN>;
     const int mt = (M + T::BM - 1) / T::BM, nt = (N + T::BN - 1) / T::BN;
     const int KB = K / QK_K;
     // split K when the tile grid cannot fill two workgroups per CU, keeping >= 2 superblocks per split
@@ -312,7 +410,7 @@ hipError_t launch_cfg(const uint8_t* w, ActView act, float* y, float* part, size
         if (ks > kmax) ks = kmax;
         while (ks > 1 && (size_t)ks * M * N > part_elems) ks--;
     }
-    hipLaunchKernelGGL((mmq_q4k_kernel<RT, CT, WM, WN, false>), dim3(mt * nt * ks), dim3(T::NT), 0, s, w, act,
+    hipLaunchKernelGGL((mmq_kernel<F, RT, CT, WM, WN, false>), dim3(mt * nt * ks), dim3(T::NT), 0, s, w, act,
                        ks > 1 ? part : y, M, N, K, ldy, mt, nt, ks, MmqGroup{});
     if (ks > 1) {
         const size_t total = (size_t)M * N;
@@ -322,14 +420,30 @@ hipError_t launch_cfg(const uint8_t* w, ActView act, float* y, float* part, size
     return hipGetLastError();
 }
 
-template <int RT, int CT, int WM, int WN>
+template <class F, int RT, int CT, int WM, int WN>
 hipError_t launch_grouped_cfg(const uint8_t* w, ActView act, float* y, int max_tiles, int N, int K, int ldy,
                               const MmqGroup& g, hipStream_t s) {
-    using T = MmqTile<RT, CT, WM, WN>;
+    using T = MmqTile<F, RT, CT, WM, WN>;
     dim3 grid(max_tiles, (N + T::BN - 1) / T::BN, 1);
-    hipLaunchKernelGGL((mmq_q4k_kernel<RT, CT, WM, WN, true>), grid, dim3(T::NT), 0, s, w, act, y, 0, N, K, ldy, 0, 0,
+    hipLaunchKernelGGL((mmq_kernel<F, RT, CT, WM, WN, true>), grid, dim3(T::NT), 0, s, w, act, y, 0, N, K, ldy, 0, 0,
                        1, g);
     return hipGetLastError();
+}
+
+template <class F>
+hipError_t launch_grouped_fmt(const uint8_t* w, ActView act, float* y, int bm, int max_tiles, int N, int K, int ldy,
+                              const MmqGroup& g, hipStream_t s) {
+    if (bm == 32) return launch_grouped_cfg<F, 2, 1, 1, 4>(w, act, y, max_tiles, N, K, ldy, g, s);  // 32 x 64
+    if (bm == 16) return launch_grouped_cfg<F, 1, 1, 1, 4>(w, act, y, max_tiles, N, K, ldy, g, s);  // 16 x 64
+    return hipErrorInvalidValue;
+}
+
+template <class F>
+hipError_t launch_fmt(const uint8_t* w, ActView act, float* y, float* part, size_t part_elems, int M, int N, int K,
+                      int ldy, int num_cus, hipStream_t s) {
+    if (M >= 128) return launch_cfg<F, 4, 2, 2, 2>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s);  // 128 x 64
+    if (M >= 64) return launch_cfg<F, 2, 2, 2, 2>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s);   // 64 x 64
+    return launch_cfg<F, 2, 1, 1, 4>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s);                // 32 x 64
 }
 
 }  // namespace
@@ -338,14 +452,13 @@ int mmq_group_rows(int rows_per_expert) { return rows_per_expert >= 24 ? 32 : 16
 
 hipError_t launch_mmq_grouped(int dtype, const uint8_t* w, ActView act, float* y, int bm, int max_tiles, int N, int K,
                               int ldy, const MmqGroup& g, hipStream_t s) {
-    if (dtype != GGML_Q4K || max_tiles <= 0) return max_tiles == 0 ? hipSuccess : hipErrorInvalidValue;
+    if (!mmq_supported(dtype) || max_tiles <= 0) return max_tiles == 0 ? hipSuccess : hipErrorInvalidValue;
     if (g.w2 && g.n_split % 64) return hipErrorInvalidValue;  // a column tile must not straddle W | W2
-    if (bm == 32) return launch_grouped_cfg<2, 1, 1, 4>(w, act, y, max_tiles, N, K, ldy, g, s);  // 32 x 64
-    if (bm == 16) return launch_grouped_cfg<1, 1, 1, 4>(w, act, y, max_tiles, N, K, ldy, g, s);  // 16 x 64
-    return hipErrorInvalidValue;
+    if (dtype == GGML_Q4K) return launch_grouped_fmt<MmqQ4K>(w, act, y, bm, max_tiles, N, K, ldy, g, s);
+    return launch_grouped_fmt<MmqQ6K>(w, act, y, bm, max_tiles, N, K, ldy, g, s);
 }
 
-bool mmq_supported(int dtype) { return dtype == GGML_Q4K; }
+bool mmq_supported(int dtype) { return dtype == GGML_Q4K || dtype == GGML_Q6K; }
 
 size_t mmq_partial_elems(int M, int N, int num_cus) {
     // enough split partials for the widest split launch_cfg picks (2 x CUs tiles)
@@ -354,10 +467,9 @@ size_t mmq_partial_elems(int M, int N, int num_cus) {
 
 hipError_t launch_mmq(int dtype, const uint8_t* w, ActView act, float* y, float* part, size_t part_elems, int M,
                       int N, int K, int ldy, int num_cus, hipStream_t s) {
-    if (dtype != GGML_Q4K) return hipErrorInvalidValue;
-    if (M >= 128) return launch_cfg<4, 2, 2, 2>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s);  // 128 x 64
-    if (M >= 64) return launch_cfg<2, 2, 2, 2>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s);   // 64 x 64
-    return launch_cfg<2, 1, 1, 4>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s);                // 32 x 64
+    if (dtype == GGML_Q4K) return launch_fmt<MmqQ4K>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s);
+    if (dtype == GGML_Q6K) return launch_fmt<MmqQ6K>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace frq

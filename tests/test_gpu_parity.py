@@ -251,47 +251,71 @@ def test_normal_matches_host_generator(dev):
 
 # ---- batched / prefill: int8 MFMA path (M >= 16) ----
 
+@pytest.mark.parametrize("dt", [O.Q4K, O.Q6K])
 @pytest.mark.parametrize("m", [16, 32, 128, 512])
-def test_qmatmul_q4k_mfma_rows(dev, m):
-    say("mfma q4k m", m)
+def test_qmatmul_mfma_rows(dev, dt, m):
+    say("mfma dt", dt, "m", m)
     k, n = 4096, 4096
-    wq = weights(O.Q4K, n, k)
+    wq = weights(dt, n, k)
     x = acts(m, k)
-    want = O.matmul(O.Q4K, x, wq)
+    want = O.matmul(dt, x, wq)
     out = dev.alloc((m, n), np.float32)
     F.qmatmul_f32_rocm_wrapper([dev.from_numpy(x), dev.from_numpy(as_u32(wq))], [out],
-                               F.QMatMulParams(O.Q4K, 1, m, n, k))
+                               F.QMatMulParams(dt, 1, m, n, k))
     err = rel_err(out.numpy(), want)
     say("  rel_err", err)
     assert err <= TOL
 
 
+@pytest.mark.parametrize("dt", [O.Q4K, O.Q6K])
 @pytest.mark.parametrize("k,n", SHAPES_7B)
-def test_qmatmul_q4k_mfma_m32_7b_shapes(dev, k, n):
-    say("mfma q4k m=32", k, n)
-    wq = weights(O.Q4K, n, k)
+def test_qmatmul_mfma_m32_7b_shapes(dev, dt, k, n):
+    say("mfma m=32", dt, k, n)
+    wq = weights(dt, n, k)
     x = acts(32, k)
-    want = O.matmul(O.Q4K, x, wq)
+    want = O.matmul(dt, x, wq)
     out = dev.alloc((32, n), np.float32)
     F.qmatmul_f32_rocm_wrapper([dev.from_numpy(x), dev.from_numpy(as_u32(wq))], [out],
-                               F.QMatMulParams(O.Q4K, 1, 32, n, k))
+                               F.QMatMulParams(dt, 1, 32, n, k))
     assert rel_err(out.numpy(), want) <= TOL
 
 
+@pytest.mark.parametrize("dt", [O.Q4K, O.Q6K])
 @pytest.mark.parametrize("batch,m,n,k", [(1, 40, 100, 512), (3, 17, 130, 768), (1, 200, 70, 256)])
-def test_qmatmul_q4k_mfma_ragged(dev, batch, m, n, k):
-    # row and column tails that do not fill a tile
-    wq = weights(O.Q4K, n, k)
+def test_qmatmul_mfma_ragged(dev, dt, batch, m, n, k):
+    # row and column tails that do not fill a tile; the last Q6_K block of the
+    # weights ends the allocation (its 2-byte-aligned tail chunk stays inside)
+    say("mfma ragged", dt, batch, m, n, k)
+    wq = weights(dt, n, k)
+    assert wq.nbytes % 4 == 0  # fuel's U32 weight storage: these shapes give whole words
     x = acts(batch * m, k)
-    want = O.matmul(O.Q4K, x, wq)
-    w = dev.from_numpy(np.frombuffer(wq.tobytes() + bytes((-wq.nbytes) % 4), np.uint32))
-    # fuel's U32 weight storage needs a 4-byte multiple; pad only when n*kb*144 is not one
+    want = O.matmul(dt, x, wq)
     out = dev.alloc((batch, m, n), np.float32)
-    if wq.nbytes % 4:
-        pytest.skip("Q4K blocks are always a 4-byte multiple")
-    F.qmatmul_f32_rocm_wrapper([dev.from_numpy(x.reshape(batch, m, k)), w], [out],
-                               F.QMatMulParams(O.Q4K, batch, m, n, k))
+    F.qmatmul_f32_rocm_wrapper([dev.from_numpy(x.reshape(batch, m, k)), dev.from_numpy(as_u32(wq))], [out],
+                               F.QMatMulParams(dt, batch, m, n, k))
     assert rel_err(out.numpy().reshape(batch * m, n), want) <= TOL
+
+
+def test_qmatmul_q6k_mfma_extreme_scales(dev):
+    """Q6_K blocks at the ends of the code and scale ranges (codes 0 and 63,
+    scales -128 and 127) against the exact integer sum: the 7-bit plane split
+    of (q - 32) * sc must carry the full [-4096, 4064] product range."""
+    say("mfma q6k extremes")
+    m, n, k = 32, 64, 512
+    rng = np.random.default_rng(5)
+    blocks = np.zeros((n, k // 256), dtype=O.BLOCK_DTYPE[O.Q6K])
+    raw = blocks.view(np.uint8).reshape(n, k // 256, 210)
+    raw[..., :192] = rng.choice(np.array([0x00, 0xff, 0xf0, 0x0f], np.uint8), size=raw[..., :192].shape)
+    raw[..., 192:208] = rng.choice(np.array([0x80, 0x7f, 0x01, 0xff], np.uint8), size=raw[..., 192:208].shape)
+    raw[..., 208:210] = np.frombuffer(np.float16(1.0 / 4096).tobytes(), np.uint8)
+    x = acts(m, k)
+    want = O.matmul(O.Q6K, x, blocks)
+    out = dev.alloc((m, n), np.float32)
+    F.qmatmul_f32_rocm_wrapper([dev.from_numpy(x), dev.from_numpy(as_u32(blocks))], [out],
+                               F.QMatMulParams(O.Q6K, 1, m, n, k))
+    err = rel_err(out.numpy(), want)
+    say("  rel_err", err)
+    assert err <= TOL
 
 
 def test_storage_outlives_device_close(dev):
