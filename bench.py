@@ -14,12 +14,16 @@ kernel (the 4096x32000 Q4_K mat-vec) timed alone the same way.  `cpu_baseline`
 is the oracle's restatement of fuel's CPU path (matmul<BlockQ4K> with the AVX2
 vec_dot) on the host cores, on the same four shapes.
 
+The same shapes are then timed with Q6_K weights (`per_shape_q6k`, the rest
+of config 2), and config 3's M = 32/128/512 rows run on both formats
+(`batched.Q4_K`, `batched.Q6_K`: the int8-MFMA path).
+
 The same run measures BASELINE config 4 (`decode`): greedy decode of a
 random-init LLaMA-2-7B-shaped Q4_K_M-mix decoder after a 512-token prompt,
 256 generated tokens timed, with fuel's CPU path (the oracle's restatement)
 timed on the same weights and KV state beside it (`decode.cpu_baseline`).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-decode] [--decode-only]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-decode] [--decode-only] [--no-q6k]
 """
 from __future__ import annotations
 
@@ -68,22 +72,22 @@ def copy_calibration(nbytes: int, reps: int = 3) -> None:
     dev.close()
 
 
-def gpu_leg(steps: int, warmup: int):
-    import fuel_amd as F
-    from fuel_amd.hiprt import HipRuntime
+TYPE_SIZE = {12: 144, 14: 210}  # GGUF codes: Q4_K, Q6_K
+TYPE_NAME = {12: "Q4_K", 14: "Q6_K"}
 
-    hip = HipRuntime()
-    dev = F.RocmDevice(0)
-    stream = hip.stream_create()
-    dev.set_stream(stream)
-    lib = F.lib()
+
+def make_mats(dev, dtype: int, seed_base: int):
+    """The four shapes' weights, N(0,0.02) quantized on the device and copied
+    until each shape's rotation exceeds ROTATE_BYTES, plus x [1,K] and y [1,N]."""
     import ctypes as C
 
+    import fuel_amd as F
+
+    lib = F.lib()
     mats = []
-    t0 = time.time()
     for si, (k, n) in enumerate(SHAPES):
-        w32 = F.fill_normal(dev, (n, k), SEED, 100 + si, 0.0, 0.02)
-        q0 = dev.qzeros(n * k, F.Q4K)
+        w32 = F.fill_normal(dev, (n, k), SEED, seed_base + si, 0.0, 0.02)
+        q0 = dev.qzeros(n * k, dtype)
         q0.quantize(w32)
         dev.synchronize()
         w32.free()
@@ -91,28 +95,72 @@ def gpu_leg(steps: int, warmup: int):
         copies = max(2, math.ceil(ROTATE_BYTES / nbytes))
         ws = [q0]
         for _ in range(copies - 1):
-            q = dev.qzeros(n * k, F.Q4K)
+            q = dev.qzeros(n * k, dtype)
             F._native.check(lib.frq_memcpy_dtod(dev.handle, C.c_void_p(q.device_ptr()), C.c_void_p(q0.device_ptr()), nbytes))
             ws.append(q)
-        x = F.fill_normal(dev, (1, k), SEED, 200 + si)
+        x = F.fill_normal(dev, (1, k), SEED, seed_base + 100 + si)
         y = dev.alloc((1, n), np.float32)
-        mats.append(dict(k=k, n=n, ws=ws, x=x, y=y, nbytes=nbytes))
+        mats.append(dict(k=k, n=n, ws=ws, x=x, y=y, nbytes=nbytes, dtype=dtype))
     dev.synchronize()
+    return mats
+
+
+def qmatmul_call(dev, mat, i):
+    import ctypes as C
+
+    import fuel_amd as F
+
+    w = mat["ws"][i % len(mat["ws"])]
+    F._native.check(F.lib().frq_qmatmul(dev.handle, mat["dtype"], 1, 1, mat["n"], mat["k"],
+                                        C.c_void_p(mat["x"].ptr), mat["x"].nbytes, C.c_void_p(w.device_ptr()),
+                                        mat["nbytes"], C.c_void_p(mat["y"].ptr), mat["y"].nbytes))
+
+
+def shape_times(hip, dev, stream, mats):
+    """Per-shape mat-vec time: graphs of back-to-back launches over the rotation."""
+    e0, e1 = hip.event_create(), hip.event_create()
+    per_shape = {}
+    for m in mats:
+        qmatmul_call(dev, m, 0)
+        dev.synchronize()
+        Rm = len(m["ws"])
+        g = hip.capture(stream, lambda m=m, Rm=Rm: [qmatmul_call(dev, m, r) for r in range(Rm)])
+        hip.graph_launch(g, stream)
+        reps = max(2, 400 // Rm)
+        hip.stream_sync(stream)
+        hip.event_record(e0, stream)
+        for _ in range(reps):
+            hip.graph_launch(g, stream)
+        hip.event_record(e1, stream)
+        hip.event_sync(e1)
+        us = hip.elapsed_ms(e0, e1) * 1e3 / (reps * Rm)
+        b = algo_bytes(m["k"], m["n"], TYPE_SIZE[m["dtype"]])
+        per_shape[f"{m['k']}x{m['n']}"] = {"us": round(us, 3), "GB_s": round(b / us / 1e3, 1),
+                                           "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "launches": reps * Rm}
+        hip.graph_destroy(g)
+    return per_shape
+
+
+def gpu_leg(steps: int, warmup: int, q6k: bool = True):
+    import fuel_amd as F
+    from fuel_amd.hiprt import HipRuntime
+
+    hip = HipRuntime()
+    dev = F.RocmDevice(0)
+    stream = hip.stream_create()
+    dev.set_stream(stream)
+
+    t0 = time.time()
+    mats = make_mats(dev, F.Q4K, 100)
     say(f"[bench] weights generated and quantized on device in {time.time() - t0:.1f}s; "
         f"copies per shape: {[len(m['ws']) for m in mats]}")
-
-    def qmatmul(mat, i):
-        w = mat["ws"][i % len(mat["ws"])]
-        F._native.check(lib.frq_qmatmul(dev.handle, F.Q4K, 1, 1, mat["n"], mat["k"], C.c_void_p(mat["x"].ptr),
-                                        mat["x"].nbytes, C.c_void_p(w.device_ptr()), mat["nbytes"],
-                                        C.c_void_p(mat["y"].ptr), mat["y"].nbytes))
 
     # one graph per rotation index: a step = the four QMatMuls
     R = max(len(m["ws"]) for m in mats)
     for m in mats:           # first launches outside capture (workspace sizing, lazy init)
-        qmatmul(m, 0)
+        qmatmul_call(dev, m, 0)
     dev.synchronize()
-    graphs = [hip.capture(stream, lambda r=r: [qmatmul(m, r) for m in mats]) for r in range(R)]
+    graphs = [hip.capture(stream, lambda r=r: [qmatmul_call(dev, m, r) for m in mats]) for r in range(R)]
     e0, e1 = hip.event_create(), hip.event_create()
 
     for i in range(warmup):
@@ -126,31 +174,24 @@ def gpu_leg(steps: int, warmup: int):
     ms_total = hip.elapsed_ms(e0, e1)
     ms_per_step = ms_total / steps
     step_bytes = sum(algo_bytes(m["k"], m["n"]) for m in mats)
-
-    # per-shape kernel time: graphs of back-to-back launches over the rotation
-    per_shape = {}
-    for m in mats:
-        Rm = len(m["ws"])
-        g = hip.capture(stream, lambda m=m, Rm=Rm: [qmatmul(m, r) for r in range(Rm)])
-        hip.graph_launch(g, stream)
-        reps = max(2, 400 // Rm)
-        hip.stream_sync(stream)
-        hip.event_record(e0, stream)
-        for _ in range(reps):
-            hip.graph_launch(g, stream)
-        hip.event_record(e1, stream)
-        hip.event_sync(e1)
-        us = hip.elapsed_ms(e0, e1) * 1e3 / (reps * Rm)
-        b = algo_bytes(m["k"], m["n"])
-        per_shape[f"{m['k']}x{m['n']}"] = {"us": round(us, 3), "GB_s": round(b / us / 1e3, 1),
-                                           "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "launches": reps * Rm}
-        hip.graph_destroy(g)
     for g in graphs:
         hip.graph_destroy(g)
-    batched = batched_leg(hip, dev, stream, mats) if BATCHED_M else None
+
+    per_shape = shape_times(hip, dev, stream, mats)
+    batched = {}
+    if BATCHED_M:
+        batched["Q4_K"] = batched_leg(hip, dev, stream, mats)
     mats.clear()  # frees the rotated weights
+    per_shape_q6k = None
+    if q6k:  # config 2's Q6_K sweep and config 3's Q6_K rows
+        mats = make_mats(dev, F.Q6K, 700)
+        per_shape_q6k = shape_times(hip, dev, stream, mats)
+        say(f"[bench] Q6_K sweep {per_shape_q6k}")
+        if BATCHED_M:
+            batched["Q6_K"] = batched_leg(hip, dev, stream, mats)
+        mats.clear()
     dev.close()
-    return ms_per_step, step_bytes, per_shape, R, batched
+    return ms_per_step, step_bytes, per_shape, R, batched, per_shape_q6k
 
 
 BATCHED_M = (32, 128, 512)
@@ -159,7 +200,7 @@ INT8_PEAK_TOPS = 5000.0
 
 def batched_leg(hip, dev, stream, mats):
     """QMatMul with M = 32, 128, 512 activation rows at the
-    same shapes and rotated Q4_K weights (the int8-MFMA path).  Reported as
+    same shapes and rotated weights (the int8-MFMA path).  Reported as
     useful TOPS (2 M N K per call) against the dense int8 peak."""
     import ctypes as C
 
@@ -169,14 +210,14 @@ def batched_leg(hip, dev, stream, mats):
     e0, e1 = hip.event_create(), hip.event_create()
     out = {}
     for si, m in enumerate(mats):
-        k, n = m["k"], m["n"]
+        k, n, dt = m["k"], m["n"], m["dtype"]
         for M in BATCHED_M:
             x = F.fill_normal(dev, (M, k), SEED, 300 + 10 * si + BATCHED_M.index(M))
             y = dev.alloc((M, n), np.float32)
 
             def call(r):
                 w = m["ws"][r % len(m["ws"])]
-                F._native.check(lib.frq_qmatmul(dev.handle, F.Q4K, 1, M, n, k, C.c_void_p(x.ptr), x.nbytes,
+                F._native.check(lib.frq_qmatmul(dev.handle, dt, 1, M, n, k, C.c_void_p(x.ptr), x.nbytes,
                                                 C.c_void_p(w.device_ptr()), m["nbytes"], C.c_void_p(y.ptr), y.nbytes))
 
             call(0)  # sizes the workspace outside the capture
@@ -451,6 +492,7 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-batched", action="store_true", help="skip the config-3 M = 32/128/512 leg")
     ap.add_argument("--no-moe", action="store_true", help="skip the config-5 MoE leg")
+    ap.add_argument("--no-q6k", action="store_true", help="skip the Q6_K sweep and Q6_K batched rows")
     ap.add_argument("--decode-only", action="store_true", help="run only the config-4 decode legs")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -474,7 +516,8 @@ def main() -> int:
     global BATCHED_M
     if args.no_batched:
         BATCHED_M = ()
-    ms_per_step, step_bytes, per_shape, rot, batched = gpu_leg(args.steps, args.warmup)
+    ms_per_step, step_bytes, per_shape, rot, batched, per_shape_q6k = gpu_leg(args.steps, args.warmup,
+                                                                              not args.no_q6k)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     dom_key = "4096x32000" if "4096x32000" in per_shape else next(iter(per_shape))
     dom = per_shape[dom_key]
@@ -507,6 +550,7 @@ def main() -> int:
         },
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
         "per_shape": per_shape,
+        "per_shape_q6k": per_shape_q6k,
         "decode_tokens_per_s": None,
         "roofline": {
             "bound": "hbm",

@@ -46,7 +46,7 @@ def main() -> int:
     out = args.out  # relative to the repository root, where every pass runs
     os.environ.setdefault("TMPDIR", "/tmp")
     bench = ["python3", "bench.py", "--shape", args.shape, "--steps", "50", "--warmup", "5", "--no-cpu",
-             "--no-decode", "--no-batched", "--no-moe", "--copy-bytes", str(COPY_BYTES)]
+             "--no-decode", "--no-batched", "--no-moe", "--no-q6k", "--copy-bytes", str(COPY_BYTES)]
     cmds = {
         "trace": ["rocprofv3", "--kernel-trace", "--stats", "--output-format", "csv", "-d", f"{out}/trace", "-o", "run",
                   "--"] + bench,
