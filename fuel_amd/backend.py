@@ -195,18 +195,20 @@ class RocmQStorage:
 
     def fwd(self, self_shape: Sequence[int], inp: RocmStorage):
         """QMatMul forward: input [..., k] -> fresh output [..., n]
-        (fuel-cpu-backend/src/quantized.rs:85-142 semantics)."""
+        (fuel-cpu-backend/src/quantized.rs:85-142 semantics): f32 input gives
+        f32 output (matmul), f16 input gives f16 output (matmul_f16)."""
         n, k = (int(d) for d in self_shape)
-        if inp.dtype != np.float32:
-            raise FuelRocmError(N.FRQ_UNSUPPORTED, f"fwd: expected f32 input, got {inp.dtype}")
+        if inp.dtype not in (np.float32, np.float16):
+            raise FuelRocmError(N.FRQ_UNSUPPORTED, "Expected f32/f16")
         if len(inp.shape) < 2:
             raise FuelRocmError(N.FRQ_INVALID, f"input tensor has only one dimension {inp.shape}")
         if inp.shape[-1] != k:
             raise FuelRocmError(N.FRQ_INVALID, f"input tensor {inp.shape} incompatible with {tuple(self_shape)}")
         out_shape = tuple(inp.shape[:-1]) + (n,)
-        y = self.dev.alloc(out_shape, np.float32)
+        y = self.dev.alloc(out_shape, inp.dtype)
         m = int(np.prod(inp.shape[:-1]))
-        check(lib().frq_qstorage_fwd(self._h, n, k, C.c_void_p(inp.ptr), m, C.c_void_p(y.ptr)))
+        fwd = lib().frq_qstorage_fwd if inp.dtype == np.float32 else lib().frq_qstorage_fwd_f16
+        check(fwd(self._h, n, k, C.c_void_p(inp.ptr), m, C.c_void_p(y.ptr)))
         return y, out_shape
 
     def indexed_moe_forward(self, self_shape: Sequence[int], inp: RocmStorage, ids: RocmStorage):

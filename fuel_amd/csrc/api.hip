@@ -183,6 +183,33 @@ int run_qmatmul(frq_device* dev, int t, const uint8_t* w, const float* x, size_t
     return FRQ_OK;
 }
 
+// matmul_f16 (k_quants.rs:2333-2374): f16 rows x [rows, k] widened exactly to
+// f32, then the same quantize and block dots as run_qmatmul; each f32 output
+// is rounded to f16 (f16::from_f32, nearest even) as it is stored.
+int run_qmatmul_f16(frq_device* dev, int t, const uint8_t* w, const uint16_t* x, size_t rows, size_t n, size_t k,
+                    uint16_t* y) {
+    if (rows == 0 || n == 0) return FRQ_OK;
+    if (k > (size_t)0x7fffffff || n > (size_t)0x7fffffff || rows > 65535)
+        return fail(FRQ_UNSUPPORTED, "qmatmul_f16: rows=%zu n=%zu k=%zu exceed the launch limits", rows, n, k);
+    const size_t kmax = t == GGML_Q8_0 ? 8192 : 32768;
+    if (k > kmax) return fail(FRQ_UNSUPPORTED, "qmatmul_f16: k=%zu exceeds %zu for dtype %d", k, kmax, t);
+    const bool w32 = n * (k / block_elems(t)) * type_size(t) <= 0xffffffffull;
+    if (rows >= MMQ_MIN_ROWS && mmq_supported(t) && w32) {
+        const size_t abytes = align256(act_bytes(GGML_Q8K, rows, k));
+        const size_t pelems = mmq_partial_elems((int)rows, (int)n, dev->num_cus);
+        int rc = ensure_ws(dev, abytes + pelems * sizeof(float));
+        if (rc) return rc;
+        const ActView act = act_view(dev->ws, GGML_Q8K, rows, k);
+        HIP_TRY(launch_quantize_q8k_h(x, (int)rows, (int)k, act, dev->stream));
+        float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(dev->ws) + abytes);
+        HIP_TRY(launch_mmq(t, w, act, reinterpret_cast<float*>(y), part, pelems, (int)rows, (int)n, (int)k, (int)n,
+                           dev->num_cus, dev->stream, true));
+        return FRQ_OK;
+    }
+    HIP_TRY(launch_qmv_half(t, w, x, y, (int)rows, (int)n, (int)k, (int)n, dev->stream, dev->num_cus));
+    return FRQ_OK;
+}
+
 bool aligned4(const void* p) { return ((uintptr_t)p & 3u) == 0; }
 
 // Largest K a mat-vec lane group covers (8 register slots per lane).
@@ -493,6 +520,21 @@ int frq_qstorage_fwd(const frq_qstorage* q, size_t n, size_t k, const float* x, 
                     q->nbytes);
     if (!aligned4(x) || !aligned4(y)) return fail(FRQ_MISALIGNED, "fwd: f32 buffers must be 4-byte aligned");
     return run_qmatmul(q->dev, q->dtype, q->d_ptr, x, m, n, k, y);
+}
+
+int frq_qstorage_fwd_f16(const frq_qstorage* q, size_t n, size_t k, const uint16_t* x, size_t m, uint16_t* y) {
+    if (!q) return fail(FRQ_INVALID, "null storage");
+    int rc = use_device(q->dev);
+    if (rc) return rc;
+    if (!is_weight_type(q->dtype)) return fail(FRQ_UNSUPPORTED, "fwd_f16: dtype %d", q->dtype);
+    if (k % block_elems(q->dtype))
+        return fail(FRQ_INVALID, "fwd_f16: k=%zu is not a multiple of %zu", k, block_elems(q->dtype));
+    if (n * (k / block_elems(q->dtype)) * type_size(q->dtype) != q->nbytes)
+        return fail(FRQ_INVALID, "fwd_f16: shape [%zu, %zu] does not match %zu storage bytes", n, k, q->nbytes);
+    // rows are read 4 halves (8 bytes) per lane: k is a multiple of 32, so 8-byte alignment of x suffices
+    if (((uintptr_t)x & 7u) != 0 || ((uintptr_t)y & 1u) != 0)
+        return fail(FRQ_MISALIGNED, "fwd_f16: x must be 8-byte and y 2-byte aligned");
+    return run_qmatmul_f16(q->dev, q->dtype, q->d_ptr, x, m, n, k, y);
 }
 
 // ---- KernelRef seam ----

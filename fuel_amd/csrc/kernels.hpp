@@ -15,11 +15,16 @@ hipError_t launch_quantize_q8k(const float* x, int rows, int K, ActView act, uin
 hipError_t launch_quantize_q8k_swiglu(const float* x, int ldx, int rows, int K, ActView act, hipStream_t s);
 hipError_t launch_quantize_q8_0(const float* x, int rows, int K, ActView act, uint8_t* aos,
                                 hipStream_t s);
+// Q8K rows of f16 activations (widened exactly to f32 first).
+hipError_t launch_quantize_q8k_h(const uint16_t* x, int rows, int K, ActView act, hipStream_t s);
 
 // mmvq.hip: y[m, n] = sum_b blockdot(W[n, b], quantize(x[m])_b) for rows m < M,
 // activation quantization fused into the kernel.
 hipError_t launch_qmv(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K,
                       int ldy, hipStream_t s, int num_cus);
+// The same over f16 activations and f16 outputs (matmul_f16).
+hipError_t launch_qmv_half(int dtype, const uint8_t* w, const uint16_t* x, uint16_t* y, int M, int N, int K, int ldy,
+                           hipStream_t s, int num_cus);
 
 // Options of the generalized mat-vec.
 // Indexed (MoE mul_mat_id): launch row m reads activation row x_row[m] (or
@@ -81,11 +86,12 @@ hipError_t launch_moe_combine(const float* yd, const int* ids, const float* w, c
                               int d, float* out, hipStream_t s);
 // mmq.hip: int8-MFMA matmul for M >= 16 over activations already quantized
 // into the workspace (quantize_q8k), y [M, N] with row stride ldy.
-// `part` (part_elems floats, may be null) holds split-K partial sums.
+// `part` (part_elems floats, may be null) holds split-K partial sums.  With
+// y_half set, y holds f16 outputs (round to nearest even of the f32 sums).
 bool mmq_supported(int dtype);
 size_t mmq_partial_elems(int M, int N, int num_cus);
 hipError_t launch_mmq(int dtype, const uint8_t* w, ActView act, float* y, float* part, size_t part_elems, int M,
-                      int N, int K, int ldy, int num_cus, hipStream_t s);
+                      int N, int K, int ldy, int num_cus, hipStream_t s, bool y_half = false);
 
 // Grouped (MoE) int8-MFMA matmul: workgroup x takes tile x of the tile table
 // (rows [tile_row0, expert end) of one expert, up to bm of them); its weights

@@ -256,7 +256,7 @@ __device__ __forceinline__ void mmq_stage(uint8_t* buf, int tid, const MmqRegs<F
 template <class F, int RT, int CT, int WM, int WN, bool GROUPED>
 __global__ __launch_bounds__(64 * WM * WN) void mmq_kernel(const uint8_t* __restrict__ W, ActView act,
                                                            float* __restrict__ y, int M, int N, int K, int ldy,
-                                                           int mt, int nt, int nsplit, MmqGroup g) {
+                                                           int mt, int nt, int nsplit, int y_half, MmqGroup g) {
     using T = MmqTile<F, RT, CT, WM, WN>;
     constexpr int BM = T::BM, BN = T::BN;
     __shared__ __align__(16) uint8_t smem[2 * T::LDS_BUF];
@@ -372,6 +372,7 @@ __global__ __launch_bounds__(64 * WM * WN) void mmq_kernel(const uint8_t* __rest
 
     float* out = nsplit > 1 ? y + (size_t)split * M * N : y;  // split partials: [z][M][N]
     const int ld = nsplit > 1 ? N : ldy;
+    const bool half_out = y_half && nsplit == 1;  // (split partials stay f32; the reduce rounds)
 #pragma unroll
     for (int r = 0; r < RT; r++)
 #pragma unroll
@@ -380,24 +381,32 @@ __global__ __launch_bounds__(64 * WM * WN) void mmq_kernel(const uint8_t* __rest
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int m = m0 + wm * RT * 16 + r * 16 + 4 * kb + i;
-                if (m < mend && n < N) out[(size_t)m * ld + n] = facc[r][c][i];
+                if (m < mend && n < N) {
+                    if (half_out)
+                        reinterpret_cast<uint16_t*>(out)[(size_t)m * ld + n] =
+                            f32_to_f16_rne(facc[r][c][i]);
+                    else
+                        out[(size_t)m * ld + n] = facc[r][c][i];
+                }
             }
         }
 }
 
 // y[m][n] = sum over splits z (in order) of part[z][m][n]
 __global__ void mmq_reduce_kernel(const float* __restrict__ part, float* __restrict__ y, int M, int N, int ldy,
-                                  int nsplit) {
+                                  int nsplit, int y_half) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (size_t)M * N) return;
     float s = part[i];
     for (int z = 1; z < nsplit; z++) s += part[(size_t)z * M * N + i];
-    y[(i / N) * ldy + i % N] = s;
+    const size_t o = (i / N) * ldy + i % N;
+    if (y_half) reinterpret_cast<uint16_t*>(y)[o] = f32_to_f16_rne(s);
+    else y[o] = s;
 }
 
 template <class F, int RT, int CT, int WM, int WN>
 hipError_t launch_cfg(const uint8_t* w, ActView act, float* y, float* part, size_t part_elems, int M, int N, int K,
-                      int ldy, int num_cus, hipStream_t s) {
+                      int ldy, int num_cus, hipStream_t s, bool y_half) {
     using T = MmqTile<F, RT, CT, WM, WN>;
     const int mt = (M + T::BM - 1) / T::BM, nt = (N + T::BN - 1) / T::BN;
     const int KB = K / QK_K;
@@ -411,11 +420,11 @@ hipError_t launch_cfg(const uint8_t* w, ActView act, float* y, float* part, size
         while (ks > 1 && (size_t)ks * M * N > part_elems) ks--;
     }
     hipLaunchKernelGGL((mmq_kernel<F, RT, CT, WM, WN, false>), dim3(mt * nt * ks), dim3(T::NT), 0, s, w, act,
-                       ks > 1 ? part : y, M, N, K, ldy, mt, nt, ks, MmqGroup{});
+                       ks > 1 ? part : y, M, N, K, ldy, mt, nt, ks, (int)y_half, MmqGroup{});
     if (ks > 1) {
         const size_t total = (size_t)M * N;
         hipLaunchKernelGGL(mmq_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, y, M, N,
-                           ldy, ks);
+                           ldy, ks, (int)y_half);
     }
     return hipGetLastError();
 }
@@ -426,7 +435,7 @@ hipError_t launch_grouped_cfg(const uint8_t* w, ActView act, float* y, int max_t
     using T = MmqTile<F, RT, CT, WM, WN>;
     dim3 grid(max_tiles, (N + T::BN - 1) / T::BN, 1);
     hipLaunchKernelGGL((mmq_kernel<F, RT, CT, WM, WN, true>), grid, dim3(T::NT), 0, s, w, act, y, 0, N, K, ldy, 0, 0,
-                       1, g);
+                       1, 0, g);
     return hipGetLastError();
 }
 
@@ -440,10 +449,10 @@ hipError_t launch_grouped_fmt(const uint8_t* w, ActView act, float* y, int bm, i
 
 template <class F>
 hipError_t launch_fmt(const uint8_t* w, ActView act, float* y, float* part, size_t part_elems, int M, int N, int K,
-                      int ldy, int num_cus, hipStream_t s) {
-    if (M >= 128) return launch_cfg<F, 4, 2, 2, 2>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s);  // 128 x 64
-    if (M >= 64) return launch_cfg<F, 2, 2, 2, 2>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s);   // 64 x 64
-    return launch_cfg<F, 2, 1, 1, 4>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s);                // 32 x 64
+                      int ldy, int num_cus, hipStream_t s, bool yh) {
+    if (M >= 128) return launch_cfg<F, 4, 2, 2, 2>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s, yh);  // 128 x 64
+    if (M >= 64) return launch_cfg<F, 2, 2, 2, 2>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s, yh);   // 64 x 64
+    return launch_cfg<F, 2, 1, 1, 4>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s, yh);                // 32 x 64
 }
 
 }  // namespace
@@ -466,9 +475,9 @@ size_t mmq_partial_elems(int M, int N, int num_cus) {
 }
 
 hipError_t launch_mmq(int dtype, const uint8_t* w, ActView act, float* y, float* part, size_t part_elems, int M,
-                      int N, int K, int ldy, int num_cus, hipStream_t s) {
-    if (dtype == GGML_Q4K) return launch_fmt<MmqQ4K>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s);
-    if (dtype == GGML_Q6K) return launch_fmt<MmqQ6K>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s);
+                      int N, int K, int ldy, int num_cus, hipStream_t s, bool y_half) {
+    if (dtype == GGML_Q4K) return launch_fmt<MmqQ4K>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s, y_half);
+    if (dtype == GGML_Q6K) return launch_fmt<MmqQ6K>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s, y_half);
     return hipErrorInvalidValue;
 }
 

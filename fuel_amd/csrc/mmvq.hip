@@ -73,7 +73,9 @@ __device__ __forceinline__ float qmv_row(const typename F::Raw (&r)[SPL], const 
     return dpp_wave_sum(acc);
 }
 
-enum QmvMode { QMV_PLAIN = 0, QMV_INDEXED = 1, QMV_FUSED = 2 };
+// QMV_HALF: f16 activations in (x holds halves), f16 outputs (y holds
+// halves, f16::from_f32 = round to nearest even of the f32 row sum).
+enum QmvMode { QMV_PLAIN = 0, QMV_INDEXED = 1, QMV_FUSED = 2, QMV_HALF = 3 };
 
 // Sum over the workgroup of one float per wavefront (valid in lane 63 of each
 // wavefront), broadcast to every thread.
@@ -130,7 +132,12 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
         if (ix.x2) xr2 = ix.x2 + xo;
     }
     float* yr = y + (size_t)m * ldy;
+    uint16_t* yh = reinterpret_cast<uint16_t*>(y) + (size_t)m * ldy;  // QMV_HALF
     const bool acc_out = MODE == QMV_FUSED && ix.accumulate;
+    auto store = [&](int r, float v) {
+        if constexpr (MODE == QMV_HALF) yh[r] = f32_to_f16_rne(v);
+        else yr[r] = v;
+    };
 
     // 1. activation loads first (s_waitcnt vmcnt is in order: the quantize step
     //    then waits for these only), 2. first weight row, 3. quantize to LDS.
@@ -138,8 +145,12 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
     constexpr int CHUNKS = SPL * (64 / F::LPB) * F::ELEMS / QK_K;
     constexpr int MAXQ = (CHUNKS + NW - 1) / NW;
     ActRowPre<MAXQ> pre;
-    if (MODE != QMV_PLAIN && xr2) act_row_load_swiglu<F::ACT, NW, MAXQ>(xr, xr2, K, w, lane, pre);
-    else act_row_load<F::ACT, NW, MAXQ>(xr, K, w, lane, pre);
+    if constexpr (MODE == QMV_HALF)
+        act_row_load_h<F::ACT, NW, MAXQ>(reinterpret_cast<const uint16_t*>(x) + (size_t)m * K, K, w, lane, pre);
+    else if (MODE != QMV_PLAIN && xr2)
+        act_row_load_swiglu<F::ACT, NW, MAXQ>(xr, xr2, K, w, lane, pre);
+    else
+        act_row_load<F::ACT, NW, MAXQ>(xr, K, w, lane, pre);
     // rows >= n_split live in the second matrix (row - n_split)
     auto wrow = [&](int r) { return r < n_split ? W + (size_t)r * row_bytes : W2 + (size_t)(r - n_split) * row_bytes; };
     typename F::Raw ra[SPL], rb[SPL];
@@ -166,7 +177,7 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
         if (acc_out && lane == 63) resb = yr[lrow];
         qmv_load_row<F, SPL>(wrow(lrow), gi, c, KB, rb);
         float t = qmv_row<F, SPL>(ra, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
-        if (lane == 63) yr[row] = acc_out ? resa + t : t;
+        if (lane == 63) store(row, acc_out ? resa + t : t);
         row = nrow;
         if (row >= N) break;
         nrow = row + nw;
@@ -174,7 +185,7 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
         if (acc_out && lane == 63) resa = yr[lrow];
         qmv_load_row<F, SPL>(wrow(lrow), gi, c, KB, ra);
         t = qmv_row<F, SPL>(rb, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
-        if (lane == 63) yr[row] = acc_out ? resb + t : t;
+        if (lane == 63) store(row, acc_out ? resb + t : t);
         row = nrow;
     }
 }
@@ -332,6 +343,12 @@ hipError_t launch_qmv(int dtype, const uint8_t* w, const float* x, float* y, int
 hipError_t launch_qmv_indexed(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
                               const QmvOpts& ix, hipStream_t s, int num_cus) {
     return launch_dtype<QMV_INDEXED>(dtype, w, x, y, M, N, K, ldy, ix, s, num_cus);
+}
+
+hipError_t launch_qmv_half(int dtype, const uint8_t* w, const uint16_t* x, uint16_t* y, int M, int N, int K, int ldy,
+                           hipStream_t s, int num_cus) {
+    return launch_dtype<QMV_HALF>(dtype, w, reinterpret_cast<const float*>(x), reinterpret_cast<float*>(y), M, N, K,
+                                  ldy, QmvOpts{}, s, num_cus);
 }
 
 // ------------------------------------------------------------------------

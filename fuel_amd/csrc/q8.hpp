@@ -150,6 +150,25 @@ __device__ __forceinline__ void act_row_load(const float* __restrict__ x, int K,
     }
 }
 
+// f16 activation row (matmul_f16, k_quants.rs:2333-2374): each half is
+// widened exactly to f32 (half::f16::to_f32) before quantization.
+template <int ACT, int NW, int MAXQ>
+__device__ __forceinline__ void act_row_load_h(const uint16_t* __restrict__ x, int K, int w, int lane,
+                                               ActRowPre<MAXQ>& p) {
+    const int nchunks = (K + QK_K - 1) / QK_K;
+#pragma unroll
+    for (int i = 0; i < MAXQ; i++) {
+        const int ch = w + NW * i;
+        p.v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        const bool live = ch < nchunks && (ACT == GGML_Q8K || ch * QK_K + 4 * lane < K);
+        if (live) {
+            const uint2 h = reinterpret_cast<const uint2*>(x + (size_t)ch * QK_K)[lane];
+            p.v[i] = make_float4(f16_to_f32(h.x & 0xffffu), f16_to_f32(h.x >> 16), f16_to_f32(h.y & 0xffffu),
+                                 f16_to_f32(h.y >> 16));
+        }
+    }
+}
+
 // SwiGLU input: silu(g) * u = g / (1 + exp(-g)) * u, element by element in the
 // order of fuel's SiLU (byte_kernels.rs silu: x / (1 + (-x).exp())).
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }

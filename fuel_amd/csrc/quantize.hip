@@ -24,6 +24,20 @@ __global__ __launch_bounds__(64) void quantize_q8k_kernel(const float* __restric
     }
 }
 
+// f16 rows (matmul_f16): each half widened exactly to f32, then the same
+// from_float as above; grid = (K/256, rows).
+__global__ __launch_bounds__(64) void quantize_q8k_h_kernel(const uint16_t* __restrict__ x, int K, ActView act) {
+    const int b = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
+    const int KB = K / QK_K;
+    const uint2 h = reinterpret_cast<const uint2*>(x + (size_t)m * K + (size_t)b * QK_K)[lane];
+    const float4 v = make_float4(f16_to_f32(h.x & 0xffffu), f16_to_f32(h.x >> 16), f16_to_f32(h.y & 0xffffu),
+                                 f16_to_f32(h.y >> 16));
+    const Q8KWave r = q8k_quantize_vals(v, lane);
+    reinterpret_cast<uint32_t*>(act.qs + (size_t)m * K + (size_t)b * QK_K)[lane] = r.packed;
+    if ((lane & 3) == 0) act.bsums[((size_t)m * KB + b) * 16 + (lane >> 2)] = (int16_t)r.bsum;
+    if (lane == 0) act.d[(size_t)m * KB + b] = r.d;
+}
+
 // SwiGLU input of the down projection: rows of silu(g) * u, g and u side by
 // side in one row of stride ldx; grid = (K/256, rows).
 __global__ __launch_bounds__(64) void quantize_q8k_swiglu_kernel(const float* __restrict__ x, int ldx, int K,
@@ -65,6 +79,12 @@ hipError_t launch_quantize_q8k(const float* x, int rows, int K, ActView act, uin
                                hipStream_t s) {
     dim3 grid(K / QK_K, rows);
     hipLaunchKernelGGL(quantize_q8k_kernel, grid, dim3(64), 0, s, x, K, act, aos);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_q8k_h(const uint16_t* x, int rows, int K, ActView act, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(quantize_q8k_h_kernel, dim3(K / QK_K, rows), dim3(64), 0, s, x, K, act);
     return hipGetLastError();
 }
 

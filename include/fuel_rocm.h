@@ -111,6 +111,13 @@ int frq_qstorage_quantize(frq_qstorage *qs, const float *src_dev, size_t elem_co
  * output buffer (the host-side mirror allocates it). */
 int frq_qstorage_fwd(const frq_qstorage *qs, size_t n, size_t k, const float *x_dev, size_t m,
                      float *y_dev);
+/* fwd over an f16 input (DType::F16 branch of fwd, fuel-cpu-backend/src/
+ * quantized.rs:127-137 -> matmul_t_f16 / matmul_f16, fuel-quantized/src/
+ * k_quants.rs:2333-2374): x [m, k] f16 is widened exactly to f32, quantized
+ * and dotted as in fwd; each output is rounded to f16 (f16::from_f32, round
+ * to nearest even).  x 8-byte aligned, y 2-byte aligned. */
+int frq_qstorage_fwd_f16(const frq_qstorage *qs, size_t n, size_t k, const uint16_t *x_dev, size_t m,
+                         uint16_t *y_dev);
 
 /* ---- KernelRef seam: (QMatMul, [F32, U32, F32]) ----
  * qmatmul_f32 wrapper semantics (fuel-dispatch/src/dispatch.rs:1638-1718 and

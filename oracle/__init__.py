@@ -221,6 +221,14 @@ def matmul(dtype: int, x: np.ndarray, w: np.ndarray, avx2: bool = True, threads:
     return y
 
 
+def matmul_f16(dtype: int, x16: np.ndarray, w: np.ndarray, avx2: bool = True, threads: int = 0) -> np.ndarray:
+    """fuel_quantized::matmul_f16::<T> (k_quants.rs:2333-2374): x [m,k] f16
+    (as uint16 bits) widened to f32 (f16::to_f32), the f32 matmul, then each
+    output rounded by f16::from_f32; returns uint16 bits [m, n]."""
+    x32 = f16_bits_to_f32(np.ascontiguousarray(x16, np.uint16))
+    return f32_to_f16_bits(matmul(dtype, x32, w, avx2, threads))
+
+
 def moe_route(logits: np.ndarray, topk: int):
     logits = np.ascontiguousarray(logits, np.float32)
     t, e = logits.shape

@@ -170,6 +170,33 @@ def test_qstorage_fwd_dequantize_data(dev, dt):
     assert np.array_equal(deq16, O.dequantize(dt, wq).reshape(-1).astype(np.float16).view(np.uint16))
 
 
+# f16 output rounding adds at most half an f16 ulp (2^-11 relative) per element
+TOL_F16 = TOL + 2.0 ** -11
+
+
+@pytest.mark.parametrize("dt", [O.Q4K, O.Q6K, O.Q8_0])
+@pytest.mark.parametrize("m,n,k", [(1, 300, 4096), (3, 64, 1024), (32, 1024, 4096), (512, 256, 2048)])
+def test_qstorage_fwd_f16(dev, dt, m, n, k):
+    """matmul_f16 through fwd: f16 rows in, f16 rows out.  Against the oracle's
+    matmul_f16 within the f32 tolerance plus the output rounding, and bit-exact
+    against the device's own f32 path on the widened rows rounded by the
+    oracle's f16::from_f32 (same kernels, same sums: only the I/O differs)."""
+    say("fwd f16", dt, m, n, k)
+    wq = weights(dt, n, k)
+    qs = dev.load_quantized(dt, wq.tobytes())
+    x16 = O.f32_to_f16_bits(acts(m, k))
+    x32 = O.f16_bits_to_f32(x16)
+    y16, shape = qs.fwd((n, k), dev.from_numpy(x16.view(np.float16)))
+    assert shape == (m, n) and y16.dtype == np.float16
+    got = y16.numpy().view(np.uint16)
+    want = O.matmul_f16(dt, x16, wq)
+    err = rel_err(O.f16_bits_to_f32(got), O.f16_bits_to_f32(want))
+    say("  rel_err", err)
+    assert err <= TOL_F16
+    y32, _ = qs.fwd((n, k), dev.from_numpy(x32))
+    assert np.array_equal(got, O.f32_to_f16_bits(y32.numpy()))
+
+
 def test_qzeros_and_errors(dev):
     z = dev.qzeros(512, O.Q4K)
     assert z.data() == bytes(2 * 144)
