@@ -22,10 +22,11 @@ from .backend import (
     quantize_q8k,
     type_size,
 )
+from .gguf import GgufFile
 
 __all__ = [
     "F16", "F32", "Q4K", "Q6K", "Q8K", "Q8_0", "FuelRocmError", "LIB_PATH", "SIGNATURES", "lib",
     "QMatMulParams", "RocmDevice", "RocmQStorage", "RocmStorage", "block_isums", "block_size",
     "device_count", "fill_normal", "fill_random_bits", "moe_ffn", "moe_route",
-    "qmatmul_f32_rocm_wrapper", "quantize_q8_0", "quantize_q8k", "type_size",
+    "qmatmul_f32_rocm_wrapper", "quantize_q8_0", "quantize_q8k", "type_size", "GgufFile",
 ]

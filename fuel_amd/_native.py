@@ -80,6 +80,24 @@ SIGNATURES = {
     "frq_block_isums": (_i32, [_vp, _i32, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
     "frq_fill_random_bits": (_i32, [_vp, _vp, _sz, C.c_uint64, C.c_uint64, C.c_uint32, C.c_uint32]),
     "frq_fill_normal": (_i32, [_vp, _vp, _sz, C.c_uint64, C.c_uint32, C.c_float, C.c_float]),
+    "frq_gguf_open": (_i32, [C.c_char_p, _vp]),
+    "frq_gguf_close": (_i32, [_vp]),
+    "frq_gguf_version": (_i32, [_vp]),
+    "frq_gguf_tensor_data_offset": (C.c_uint64, [_vp]),
+    "frq_gguf_tensor_count": (_sz, [_vp]),
+    "frq_gguf_tensor_info": (_i32, [_vp, _sz, _vp, _vp, _vp, _vp, _sz, _vp, _vp]),
+    "frq_gguf_find_tensor": (_i32, [_vp, C.c_char_p, _vp]),
+    "frq_gguf_tensor_data": (_i32, [_vp, _sz, _vp, _vp]),
+    "frq_gguf_load_quantized": (_i32, [_vp, _vp, _sz, _vp]),
+    "frq_gguf_meta_count": (_sz, [_vp]),
+    "frq_gguf_meta_at": (_i32, [_vp, _sz, _vp, _vp]),
+    "frq_gguf_meta_find": (_i32, [_vp, C.c_char_p, _vp]),
+    "frq_gguf_value_type": (_i32, [_vp]),
+    "frq_gguf_value_scalar": (_i32, [_vp, _vp, _vp, _vp]),
+    "frq_gguf_value_u64": (_i32, [_vp, _vp]),
+    "frq_gguf_value_string": (_i32, [_vp, _vp, _vp]),
+    "frq_gguf_value_array": (_i32, [_vp, _vp]),
+    "frq_gguf_value_array_at": (_i32, [_vp, _sz, _vp]),
 }
 
 _lib = None

@@ -11,6 +11,7 @@
 
 #include "../../include/fuel_rocm.h"
 #include "common.hpp"
+#include "gguf.hpp"
 #include "kernels.hpp"
 
 using namespace frq;
@@ -25,6 +26,10 @@ struct frq_device {
     // references: the open handle plus one per live storage; the struct is
     // deleted when the last one is dropped (a storage may outlive close)
     std::atomic<int> refs{1};
+};
+
+struct frq_gguf {
+    std::unique_ptr<frq::gguf::File> f;
 };
 
 struct frq_qstorage {
@@ -877,6 +882,155 @@ int frq_fill_normal(frq_device* dev, float* y, size_t n, uint64_t seed, uint32_t
     if (n && !y) return fail(FRQ_INVALID, "null output");
     if (!aligned4(y)) return fail(FRQ_MISALIGNED, "fill_normal: output not 4-byte aligned");
     HIP_TRY(launch_normal(y, n, seed, stream, mean, stdv, dev->stream));
+    return FRQ_OK;
+}
+
+// ---- GGUF files ----
+
+namespace {
+const frq::gguf::Value* gv(const frq_gguf_value* v) { return reinterpret_cast<const frq::gguf::Value*>(v); }
+const frq_gguf_value* gh(const frq::gguf::Value* v) { return reinterpret_cast<const frq_gguf_value*>(v); }
+}  // namespace
+
+int frq_gguf_open(const char* path, frq_gguf** out) {
+    if (!path || !out) return fail(FRQ_INVALID, "gguf_open: null argument");
+    *out = nullptr;
+    std::string err;
+    std::unique_ptr<frq::gguf::File> f = frq::gguf::open(path, err);
+    if (!f) return fail(FRQ_INVALID, "%s", err.c_str());
+    *out = new frq_gguf{std::move(f)};
+    return FRQ_OK;
+}
+
+int frq_gguf_close(frq_gguf* g) {
+    delete g;
+    return FRQ_OK;
+}
+
+int frq_gguf_version(const frq_gguf* g) { return g ? g->f->version : -1; }
+uint64_t frq_gguf_tensor_data_offset(const frq_gguf* g) { return g ? g->f->tensor_data_offset : 0; }
+size_t frq_gguf_tensor_count(const frq_gguf* g) { return g ? g->f->tensors.size() : 0; }
+size_t frq_gguf_meta_count(const frq_gguf* g) { return g ? g->f->metadata.size() : 0; }
+
+int frq_gguf_tensor_info(const frq_gguf* g, size_t index, const char** name, int* ggml_dtype, size_t* n_dims,
+                         uint64_t* dims, size_t dims_cap, uint64_t* offset, uint64_t* nbytes) {
+    if (!g) return fail(FRQ_INVALID, "null gguf");
+    if (index >= g->f->tensors.size()) return fail(FRQ_INVALID, "gguf: tensor index %zu of %zu", index, g->f->tensors.size());
+    const frq::gguf::TensorInfo& t = g->f->tensors[index];
+    if (name) *name = t.name.c_str();
+    if (ggml_dtype) *ggml_dtype = t.ggml_dtype;
+    if (n_dims) *n_dims = t.dims.size();
+    if (dims) {
+        if (t.dims.size() > dims_cap)
+            return fail(FRQ_INVALID, "gguf: tensor %s has %zu dims, buffer holds %zu", t.name.c_str(), t.dims.size(),
+                        dims_cap);
+        for (size_t i = 0; i < t.dims.size(); i++) dims[i] = t.dims[i];
+    }
+    if (offset) *offset = t.offset;
+    if (nbytes) *nbytes = t.nbytes;
+    return FRQ_OK;
+}
+
+int frq_gguf_find_tensor(const frq_gguf* g, const char* name, size_t* index) {
+    if (!g || !name || !index) return fail(FRQ_INVALID, "gguf_find_tensor: null argument");
+    auto it = g->f->tensor_index.find(name);
+    if (it == g->f->tensor_index.end()) return fail(FRQ_INVALID, "gguf: missing tensor \"%s\"", name);
+    *index = it->second;
+    return FRQ_OK;
+}
+
+int frq_gguf_tensor_data(const frq_gguf* g, size_t index, const void** host, uint64_t* nbytes) {
+    if (!g || !host || !nbytes) return fail(FRQ_INVALID, "gguf_tensor_data: null argument");
+    const frq::gguf::File& f = *g->f;
+    if (index >= f.tensors.size()) return fail(FRQ_INVALID, "gguf: tensor index %zu of %zu", index, f.tensors.size());
+    const frq::gguf::TensorInfo& t = f.tensors[index];
+    const unsigned __int128 start = (unsigned __int128)f.tensor_data_offset + t.offset;
+    if (start + t.nbytes > f.map_bytes)
+        return fail(FRQ_INVALID, "gguf: tensor %s bytes [%llu, +%llu) lie outside the %zu-byte file", t.name.c_str(),
+                    (unsigned long long)start, (unsigned long long)t.nbytes, f.map_bytes);
+    *host = f.map + (size_t)start;
+    *nbytes = t.nbytes;
+    return FRQ_OK;
+}
+
+int frq_gguf_load_quantized(frq_device* dev, const frq_gguf* g, size_t index, frq_qstorage** out) {
+    const void* host = nullptr;
+    uint64_t nbytes = 0;
+    int rc = frq_gguf_tensor_data(g, index, &host, &nbytes);
+    if (rc) return rc;
+    const int dt = g->f->tensors[index].ggml_dtype;
+    if (!type_size(dt))
+        return fail(FRQ_UNSUPPORTED, "gguf: tensor %s has dtype %d, not a quantized storage type",
+                    g->f->tensors[index].name.c_str(), dt);
+    return frq_qstorage_load(dev, dt, host, (size_t)nbytes, out);
+}
+
+int frq_gguf_meta_at(const frq_gguf* g, size_t index, const char** key, const frq_gguf_value** value) {
+    if (!g) return fail(FRQ_INVALID, "null gguf");
+    if (index >= g->f->metadata.size())
+        return fail(FRQ_INVALID, "gguf: metadata index %zu of %zu", index, g->f->metadata.size());
+    if (key) *key = g->f->metadata[index].first.c_str();
+    if (value) *value = gh(&g->f->metadata[index].second);
+    return FRQ_OK;
+}
+
+int frq_gguf_meta_find(const frq_gguf* g, const char* key, const frq_gguf_value** value) {
+    if (!g || !key || !value) return fail(FRQ_INVALID, "gguf_meta_find: null argument");
+    auto it = g->f->meta_index.find(key);
+    if (it == g->f->meta_index.end()) return fail(FRQ_INVALID, "cannot find %s in metadata", key);
+    *value = gh(&g->f->metadata[it->second].second);
+    return FRQ_OK;
+}
+
+int frq_gguf_value_type(const frq_gguf_value* v) { return v ? gv(v)->type : -1; }
+
+int frq_gguf_value_scalar(const frq_gguf_value* v, uint64_t* u, int64_t* i, double* f) {
+    if (!v) return fail(FRQ_INVALID, "null value");
+    const frq::gguf::Value& x = *gv(v);
+    if (x.type == frq::gguf::VT_STRING || x.type == frq::gguf::VT_ARRAY)
+        return fail(FRQ_INVALID, "gguf: value of type %d is not a scalar", x.type);
+    if (u) *u = x.u;
+    if (i) *i = x.i;
+    if (f) *f = x.f;
+    return FRQ_OK;
+}
+
+int frq_gguf_value_u64(const frq_gguf_value* v, uint64_t* out) {
+    if (!v || !out) return fail(FRQ_INVALID, "null argument");
+    const frq::gguf::Value& x = *gv(v);
+    // Value::to_u64: U64, U8 / U16 / U32 and Bool upcast (gguf.rs:262-272)
+    if (x.type == frq::gguf::VT_U64 || x.type == frq::gguf::VT_U8 || x.type == frq::gguf::VT_U16 ||
+        x.type == frq::gguf::VT_U32 || x.type == frq::gguf::VT_BOOL) {
+        *out = x.u;
+        return FRQ_OK;
+    }
+    return fail(FRQ_INVALID, "not a u64 or upcastable to u64 (value type %d)", x.type);
+}
+
+int frq_gguf_value_string(const frq_gguf_value* v, const char** s, size_t* len) {
+    if (!v || !s || !len) return fail(FRQ_INVALID, "null argument");
+    const frq::gguf::Value& x = *gv(v);
+    if (x.type != frq::gguf::VT_STRING) return fail(FRQ_INVALID, "not a string (value type %d)", x.type);
+    *s = x.s.c_str();
+    *len = x.s.size();
+    return FRQ_OK;
+}
+
+int frq_gguf_value_array(const frq_gguf_value* v, size_t* len) {
+    if (!v || !len) return fail(FRQ_INVALID, "null argument");
+    const frq::gguf::Value& x = *gv(v);
+    if (x.type != frq::gguf::VT_ARRAY) return fail(FRQ_INVALID, "not a vec (value type %d)", x.type);
+    *len = x.a.size();
+    return FRQ_OK;
+}
+
+int frq_gguf_value_array_at(const frq_gguf_value* v, size_t j, const frq_gguf_value** elem) {
+    size_t len = 0;
+    int rc = frq_gguf_value_array(v, &len);
+    if (rc) return rc;
+    if (!elem) return fail(FRQ_INVALID, "null argument");
+    if (j >= len) return fail(FRQ_INVALID, "gguf: array index %zu of %zu", j, len);
+    *elem = gh(&gv(v)->a[j]);
     return FRQ_OK;
 }
 

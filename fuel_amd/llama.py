@@ -29,6 +29,7 @@ from ._native import check, lib
 from .backend import RocmDevice, fill_normal
 
 Q4K, Q6K = N.Q4K, N.Q6K
+N_TYPE_SIZE = {N.Q8_0: 34, Q4K: 144, Q6K: 210}
 LAYER_MATS = ("wq", "wk", "wv", "wo", "wg", "wu", "wd")
 
 
@@ -98,33 +99,40 @@ class _Buf:
             pass
 
 
+# GGUF tensor names of the layer matrices (llama.cpp's LLaMA layout, as the
+# lazy loader reads them: fuel-core/src/lazy_quantized_llama.rs:224-236)
+GGUF_NAMES = {"wq": "attn_q", "wk": "attn_k", "wv": "attn_v", "wo": "attn_output", "wg": "ffn_gate",
+              "wu": "ffn_up", "wd": "ffn_down"}
+
+
 class LlamaDecoder:
-    def __init__(self, dev: RocmDevice, cfg: LlamaConfig, seed: int = 1234, std: float = 0.02):
+    def __init__(self, dev: RocmDevice, cfg: LlamaConfig, seed: int = 1234, std: float = 0.02, _weights=None):
         if cfg.head_dim != 128 or cfg.n_heads * cfg.head_dim != cfg.dim:
             raise ValueError("this decoder needs head_dim 128 and n_heads * head_dim == dim")
         self.dev, self.cfg, self.seed, self.std = dev, cfg, seed, std
         L = lib()
         self.L = L
         d, f, H, HD, Cx = cfg.dim, cfg.ffn, cfg.n_heads, cfg.head_dim, cfg.max_ctx
-        tsz = {Q4K: 144, Q6K: 210}
-        self.layers = []
-        for li in range(cfg.n_layers):
-            dts = cfg.layer_dtypes(li)
-            lw = {
-                "wqk": self._quantized(Q4K, [("wq", li), ("wk", li)], d, d),
-                "wv": self._quantized(Q6K, [("wv", li)], d, d),
-                "wo": self._quantized(Q4K, [("wo", li)], d, d),
-                "wgu": self._quantized(Q4K, [("wg", li), ("wu", li)], f, d),
-                "wd": self._quantized(dts["wd"], [("wd", li)], d, f),
-                "dt_down": dts["wd"],
-            }
-            self.layers.append(lw)
-        self.wout = self._quantized(Q6K, [("out", None)], cfg.vocab, d)
-        self.embed = fill_normal(dev, (cfg.vocab, d), seed, 1, 0.0, std)
-        ones = np.ones(d, np.float32)
-        self.attn_gain = [dev.from_numpy(ones) for _ in range(cfg.n_layers)]
-        self.ffn_gain = [dev.from_numpy(ones) for _ in range(cfg.n_layers)]
-        self.final_gain = dev.from_numpy(ones)
+        if _weights is None:  # random-init weights generated on the device
+            self.layers = []
+            for li in range(cfg.n_layers):
+                dts = cfg.layer_dtypes(li)
+                self.layers.append({
+                    "wqk": self._quantized(Q4K, [("wq", li), ("wk", li)], d, d), "dt_qk": Q4K,
+                    "wv": self._quantized(Q6K, [("wv", li)], d, d), "dt_v": Q6K,
+                    "wo": self._quantized(Q4K, [("wo", li)], d, d), "dt_o": Q4K,
+                    "wgu": self._quantized(Q4K, [("wg", li), ("wu", li)], f, d), "dt_gu": Q4K,
+                    "wd": self._quantized(dts["wd"], [("wd", li)], d, f), "dt_down": dts["wd"],
+                })
+            self.wout, self.dt_out = self._quantized(Q6K, [("out", None)], cfg.vocab, d), Q6K
+            self.embed = fill_normal(dev, (cfg.vocab, d), seed, 1, 0.0, std)
+            ones = np.ones(d, np.float32)
+            self.attn_gain = [dev.from_numpy(ones) for _ in range(cfg.n_layers)]
+            self.ffn_gain = [dev.from_numpy(ones) for _ in range(cfg.n_layers)]
+            self.final_gain = dev.from_numpy(ones)
+        else:
+            (self.layers, self.wout, self.dt_out, self.embed, self.attn_gain, self.ffn_gain,
+             self.final_gain) = _weights
         c, s = rope_tables(cfg.rope_theta, Cx, HD)
         self.rcos, self.rsin = dev.from_numpy(c), dev.from_numpy(s)
         cache_bytes = H * Cx * HD * 2
@@ -144,6 +152,102 @@ class LlamaDecoder:
         self.prompt_len = 0
         self.scale = float(np.float32(1.0 / np.sqrt(float(HD))))
         dev.synchronize()
+
+    @classmethod
+    def from_gguf(cls, dev: RocmDevice, path: str, max_ctx: int = 768) -> "LlamaDecoder":
+        """A decoder over the tensors of a GGUF file in llama.cpp's LLaMA
+        layout, uploaded verbatim (quantized blocks in [out, in] order; the
+        lazy loader's names and slices, fuel-core/src/lazy_quantized_llama.rs:
+        224-260).  Hyper-parameters come from the `{arch}.*` metadata; the
+        vocabulary size from token_embd.weight, which is also the output
+        matrix when output.weight is absent (tied).  f32 / f16 norm gains are
+        widened on the host; a quantized token_embd is dequantized on the
+        device (to_float).  Grouped-query attention (head_count_kv !=
+        head_count) is not supported by this decoder."""
+        from .gguf import GgufFile
+
+        g = GgufFile(path)
+        md = g.metadata
+        arch = md.get("general.architecture", "llama")
+
+        def meta(key, default=None):
+            v = md.get(f"{arch}.{key}", default)
+            if v is None:
+                raise ValueError(f"gguf: missing metadata {arch}.{key}")
+            return v
+
+        heads = int(meta("attention.head_count"))
+        if int(md.get(f"{arch}.attention.head_count_kv", heads)) != heads:
+            raise ValueError("gguf: grouped-query attention (head_count_kv != head_count) is not supported")
+        if "token_embd.weight" not in g.tensors:
+            raise ValueError("gguf: missing tensor \"token_embd.weight\"")
+        dim = int(meta("embedding_length"))
+        cfg = LlamaConfig(dim=dim, n_layers=int(meta("block_count")), n_heads=heads, head_dim=dim // heads,
+                          ffn=int(meta("feed_forward_length")), vocab=int(g.tensors["token_embd.weight"].dims[0]),
+                          eps=float(meta("attention.layer_norm_rms_epsilon", 1e-5)),
+                          rope_theta=float(meta("rope.freq_base", 10000.0)), max_ctx=max_ctx)
+
+        def info(name, rows, cols):
+            if name not in g.tensors:
+                raise ValueError(f"gguf: missing tensor \"{name}\"")
+            t = g.tensors[name]
+            if t.dims != (rows, cols):
+                raise ValueError(f"gguf: tensor {name} has dims {t.dims}, expected {(rows, cols)}")
+            if t.dtype not in (Q4K, Q6K, N.Q8_0):
+                raise ValueError(f"gguf: tensor {name} has dtype {t.dtype}; the mat-vec takes Q8_0 / Q4_K / Q6_K")
+            return t
+
+        def stacked(names, rows, cols):
+            infos = [info(n, rows, cols) for n in names]
+            if len({t.dtype for t in infos}) != 1:
+                raise ValueError(f"gguf: {names} must share one dtype to be stacked")
+            one = infos[0].nbytes
+            buf = _Buf(dev, one * len(names))
+            for i, n in enumerate(names):
+                g.copy_to_device(dev, n, buf.ptr + i * one)
+            return buf, infos[0].dtype
+
+        def vec(name, n):
+            if name not in g.tensors:
+                raise ValueError(f"gguf: missing tensor \"{name}\"")
+            t = g.tensors[name]
+            raw = g.tensor_bytes(name)
+            if t.dtype == N.F32:
+                a = raw.view(np.float32)
+            elif t.dtype == N.F16:
+                a = raw.view(np.float16).astype(np.float32)
+            else:
+                raise ValueError(f"gguf: norm tensor {name} has dtype {t.dtype} (f32 / f16 expected)")
+            if a.size != n:
+                raise ValueError(f"gguf: tensor {name} has {a.size} values, expected {n}")
+            return dev.from_numpy(a)
+
+        d, f = cfg.dim, cfg.ffn
+        layers, ag, fg = [], [], []
+        for li in range(cfg.n_layers):
+            nm = {k: f"blk.{li}.{v}.weight" for k, v in GGUF_NAMES.items()}
+            lw = {}
+            lw["wqk"], lw["dt_qk"] = stacked([nm["wq"], nm["wk"]], d, d)
+            lw["wv"], lw["dt_v"] = stacked([nm["wv"]], d, d)
+            lw["wo"], lw["dt_o"] = stacked([nm["wo"]], d, d)
+            lw["wgu"], lw["dt_gu"] = stacked([nm["wg"], nm["wu"]], f, d)
+            lw["wd"], lw["dt_down"] = stacked([nm["wd"]], d, f)
+            layers.append(lw)
+            ag.append(vec(f"blk.{li}.attn_norm.weight", d))
+            fg.append(vec(f"blk.{li}.ffn_norm.weight", d))
+        out_name = "output.weight" if "output.weight" in g.tensors else "token_embd.weight"
+        wout, dt_out = stacked([out_name], cfg.vocab, d)
+        et = g.tensors["token_embd.weight"]
+        if et.dtype in (N.F32, N.F16):
+            embed = vec("token_embd.weight", cfg.vocab * d)
+        else:
+            qs = g.load_quantized(dev, "token_embd.weight")
+            embed = qs.dequantize(cfg.vocab * d)
+            del qs
+        embed.shape = (cfg.vocab, d)  # rows of the table (the buffer is contiguous)
+        dec = cls(dev, cfg, _weights=(layers, wout, dt_out, embed, ag, fg, vec("output_norm.weight", d)))
+        g.close()
+        return dec
 
     # ---- weights ----
 
@@ -179,19 +283,19 @@ class LlamaDecoder:
             return out
 
         d, f = cfg.dim, cfg.ffn
-        tsz = {Q4K: 144, Q6K: 210}
 
         def mat(buf, dt, rows, cols, idx=0):  # (block bytes, (rows, blocks per row), dtype)
-            n = rows * (cols // 256) * tsz[dt]
-            return fetch(buf, idx * n, n), (rows, cols // 256), dt
+            bs = 32 if dt == N.Q8_0 else 256
+            n = rows * (cols // bs) * N_TYPE_SIZE[dt]
+            return fetch(buf, idx * n, n), (rows, cols // bs), dt
 
         out = {"embed": self.embed.numpy(), "final_gain": self.final_gain.numpy(), "layers": []}
-        out["out"] = mat(self.wout, Q6K, cfg.vocab, d)
+        out["out"] = mat(self.wout, self.dt_out, cfg.vocab, d)
         for li, lw in enumerate(self.layers):
             out["layers"].append({
-                "wq": mat(lw["wqk"], Q4K, d, d, 0), "wk": mat(lw["wqk"], Q4K, d, d, 1),
-                "wv": mat(lw["wv"], Q6K, d, d), "wo": mat(lw["wo"], Q4K, d, d),
-                "wg": mat(lw["wgu"], Q4K, f, d, 0), "wu": mat(lw["wgu"], Q4K, f, d, 1),
+                "wq": mat(lw["wqk"], lw["dt_qk"], d, d, 0), "wk": mat(lw["wqk"], lw["dt_qk"], d, d, 1),
+                "wv": mat(lw["wv"], lw["dt_v"], d, d), "wo": mat(lw["wo"], lw["dt_o"], d, d),
+                "wg": mat(lw["wgu"], lw["dt_gu"], f, d, 0), "wu": mat(lw["wgu"], lw["dt_gu"], f, d, 1),
                 "wd": mat(lw["wd"], lw["dt_down"], d, f),
                 "attn_gain": self.attn_gain[li].numpy(), "ffn_gain": self.ffn_gain[li].numpy(),
             })
@@ -236,24 +340,35 @@ class LlamaDecoder:
         x = vp(self.x.ptr)
         for li, lw in enumerate(self.layers):
             ag, fg = vp(self.attn_gain[li].ptr), vp(self.ffn_gain[li].ptr)
-            check(L.frq_qmatmul_fused_pair(h, 1, d, x, d, ag, eps, Q4K, 2 * d, vp(lw["wqk"].ptr), vp(self.qk.ptr),
-                                           Q6K, d, vp(lw["wv"].ptr), vp(self.v.ptr)))
+            if self._pair(lw):
+                check(L.frq_qmatmul_fused_pair(h, 1, d, x, d, ag, eps, lw["dt_qk"], 2 * d, vp(lw["wqk"].ptr),
+                                               vp(self.qk.ptr), lw["dt_v"], d, vp(lw["wv"].ptr), vp(self.v.ptr)))
+            else:
+                check(L.frq_qmatmul_fused(h, lw["dt_qk"], 1, 2 * d, d, vp(lw["wqk"].ptr), x, d, None, ag, eps, 0,
+                                          vp(self.qk.ptr), 2 * d))
+                check(L.frq_qmatmul_fused(h, lw["dt_v"], 1, d, d, vp(lw["wv"].ptr), x, d, None, ag, eps, 0,
+                                          vp(self.v.ptr), d))
             check(L.frq_attention_decode(h, cfg.n_heads, cfg.head_dim, cfg.max_ctx, vp(self.qk.ptr), vp(self.v.ptr),
                                          vp(self.rcos.ptr), vp(self.rsin.ptr), vp(self.kc[li].ptr),
                                          vp(self.vc[li].ptr), vp(self.pos.ptr), self.scale, vp(self.work.ptr),
                                          self.work_bytes, vp(self.att.ptr)))
-            check(L.frq_qmatmul_fused(h, Q4K, 1, d, d, vp(lw["wo"].ptr), vp(self.att.ptr), d, None, None, 0.0, 1, x, d))
-            check(L.frq_qmatmul_fused(h, Q4K, 1, 2 * f, d, vp(lw["wgu"].ptr), x, d, None, fg, eps, 0,
+            check(L.frq_qmatmul_fused(h, lw["dt_o"], 1, d, d, vp(lw["wo"].ptr), vp(self.att.ptr), d, None, None, 0.0,
+                                      1, x, d))
+            check(L.frq_qmatmul_fused(h, lw["dt_gu"], 1, 2 * f, d, vp(lw["wgu"].ptr), x, d, None, fg, eps, 0,
                                       vp(self.gu.ptr), 2 * f))
             check(L.frq_qmatmul_fused(h, lw["dt_down"], 1, d, f, vp(lw["wd"].ptr), vp(self.gu.ptr), f,
                                       vp(self.gu.ptr + 4 * f), None, 0.0, 1, x, d))
-        check(L.frq_qmatmul_fused(h, Q6K, 1, cfg.vocab, d, vp(self.wout.ptr), x, d, None, vp(self.final_gain.ptr),
-                                  eps, 0, vp(self.logits.ptr), cfg.vocab))
+        check(L.frq_qmatmul_fused(h, self.dt_out, 1, cfg.vocab, d, vp(self.wout.ptr), x, d, None,
+                                  vp(self.final_gain.ptr), eps, 0, vp(self.logits.ptr), cfg.vocab))
         check(L.frq_argmax_embed(h, vp(self.logits.ptr), cfg.vocab, vp(self.embed.ptr), d, vp(self.tokens.ptr),
                                  cfg.max_ctx, self.prompt_len, vp(self.pos.ptr), x))
 
+    def _pair(self, lw) -> bool:
+        kq = (Q4K, Q6K)
+        return lw["dt_qk"] in kq and lw["dt_v"] in kq and self.cfg.dim <= 16384
+
     def launches_per_step(self) -> int:
-        return 6 * self.cfg.n_layers + 2
+        return sum(6 if self._pair(lw) else 7 for lw in self.layers) + 2
 
     def tokens_host(self) -> np.ndarray:
         return self.tokens.numpy()

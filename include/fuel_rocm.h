@@ -236,6 +236,56 @@ int frq_fill_random_bits(frq_device *dev, uint32_t *y_dev, size_t n, uint64_t st
 int frq_fill_normal(frq_device *dev, float *y_dev, size_t n, uint64_t seed, uint32_t stream, float mean,
                     float std);
 
+/* ---- GGUF files (host-side reader + upload) ----
+ * frq_gguf_open maps the file read-only and parses its header exactly as
+ * fuel_formats::gguf::Content::read (fuel-formats/src/gguf.rs:378-461) over
+ * fuel-core's mmap (fuel-core/src/quantized/gguf_mmap.rs:44-79): magic
+ * "GGUF" (either byte order), versions 1-3 (u32 counts and lengths in v1, u64
+ * after), metadata values of types 0-12 (nested arrays included; strings lose
+ * trailing NULs and invalid UTF-8 becomes U+FFFD), tensor infos with their
+ * dims reversed (outermost first, as fuel's Shape), GgmlDType codes of
+ * GgmlDType::from_u32, and tensor_data_offset = position rounded up to
+ * general.alignment (u8/u16/u32 or non-negative i8/i16/i32; else 32).  A
+ * repeated metadata key or tensor name keeps its first position and the last
+ * value.  Errors (FRQ_INVALID) carry the reference's messages ("unknown magic
+ * ...", "unrecognized value-type ...", "unexpected bool value ...", "unknown
+ * dtype for tensor ...").  The handle owns the mapping until frq_gguf_close. */
+typedef struct frq_gguf frq_gguf;
+typedef struct frq_gguf_value frq_gguf_value;
+int frq_gguf_open(const char *path, frq_gguf **out);
+int frq_gguf_close(frq_gguf *g);
+int frq_gguf_version(const frq_gguf *g);
+uint64_t frq_gguf_tensor_data_offset(const frq_gguf *g);
+size_t frq_gguf_tensor_count(const frq_gguf *g);
+/* Tensor `index` (file order): name, GgmlDType code, dims (outermost first,
+ * at most dims_cap written), offset relative to tensor_data_offset, and its
+ * byte length elem_count / block_size * type_size (the slice the lazy loaders
+ * take, fuel-core/src/lazy_quantized_llama.rs:251-260). */
+int frq_gguf_tensor_info(const frq_gguf *g, size_t index, const char **name, int *ggml_dtype, size_t *n_dims,
+                         uint64_t *dims, size_t dims_cap, uint64_t *offset, uint64_t *nbytes);
+int frq_gguf_find_tensor(const frq_gguf *g, const char *name, size_t *index);
+/* Host view of a tensor's bytes inside the mapping (bounds-checked). */
+int frq_gguf_tensor_data(const frq_gguf *g, size_t index, const void **host, uint64_t *nbytes);
+/* QuantizedDeviceKernels::load_quantized(dtype, bytes) of one tensor: its
+ * blocks uploaded verbatim ([out, in] block order) into a new storage
+ * (Q8_0 / Q4_K / Q6_K / Q8_K tensors). */
+int frq_gguf_load_quantized(frq_device *dev, const frq_gguf *g, size_t index, frq_qstorage **out);
+/* Metadata in file order and by key; values are read through the accessors
+ * below (the Value enum, gguf.rs:164-375): value_type is the format's code,
+ * value_scalar yields the raw payload of a scalar (unsigned types and bool in
+ * u, signed in i, f32/f64 in f), value_u64 follows Value::to_u64 (u64, or u8 /
+ * u16 / u32 / bool upcast), arrays are walked with value_array /
+ * value_array_at. */
+size_t frq_gguf_meta_count(const frq_gguf *g);
+int frq_gguf_meta_at(const frq_gguf *g, size_t index, const char **key, const frq_gguf_value **value);
+int frq_gguf_meta_find(const frq_gguf *g, const char *key, const frq_gguf_value **value);
+int frq_gguf_value_type(const frq_gguf_value *v);
+int frq_gguf_value_scalar(const frq_gguf_value *v, uint64_t *u, int64_t *i, double *f);
+int frq_gguf_value_u64(const frq_gguf_value *v, uint64_t *out);
+int frq_gguf_value_string(const frq_gguf_value *v, const char **s, size_t *len);
+int frq_gguf_value_array(const frq_gguf_value *v, size_t *len);
+int frq_gguf_value_array_at(const frq_gguf_value *v, size_t j, const frq_gguf_value **elem);
+
 #ifdef __cplusplus
 }
 #endif

@@ -288,3 +288,87 @@ def test_decoder_greedy_graph_replay(dev, small_decoder):
             assert gap <= DEC_TOL, (p, chosen, best, gap)
             exact += chosen == best
     assert exact >= (n_steps - len(prompt) + 1) // 2
+
+
+# ---- the decoder from a GGUF file ----
+
+def write_gguf(path, dec, tied=False):
+    """The decoder's weights as a GGUF file in llama.cpp's LLaMA layout."""
+    from oracle import gguf as G
+
+    cfg, wh = dec.cfg, dec.weights_host()
+    md = [("general.architecture", G.Value(G.VT_STRING, "llama")),
+          ("general.alignment", G.Value(G.VT_U32, 32)),
+          ("llama.embedding_length", G.Value(G.VT_U32, cfg.dim)),
+          ("llama.block_count", G.Value(G.VT_U32, cfg.n_layers)),
+          ("llama.attention.head_count", G.Value(G.VT_U32, cfg.n_heads)),
+          ("llama.attention.head_count_kv", G.Value(G.VT_U32, cfg.n_heads)),
+          ("llama.feed_forward_length", G.Value(G.VT_U32, cfg.ffn)),
+          ("llama.attention.layer_norm_rms_epsilon", G.Value(G.VT_F32, cfg.eps)),
+          ("llama.rope.freq_base", G.Value(G.VT_F32, cfg.rope_theta))]
+    d, f = cfg.dim, cfg.ffn
+
+    def q(t, rows, cols):
+        raw, _, dt = t
+        return dt, (rows, cols), raw.tobytes()
+
+    out_dt, _, out_raw = q(wh["out"], cfg.vocab, d)
+    tens = []
+    if tied:
+        tens.append(("token_embd.weight", out_dt, (cfg.vocab, d), out_raw))
+    else:
+        tens.append(("token_embd.weight", 0, (cfg.vocab, d), wh["embed"].astype(np.float32).tobytes()))
+        tens.append(("output.weight", out_dt, (cfg.vocab, d), out_raw))
+    tens.append(("output_norm.weight", 0, (d,), wh["final_gain"].tobytes()))
+    names = {"wq": "attn_q", "wk": "attn_k", "wv": "attn_v", "wo": "attn_output", "wg": "ffn_gate",
+             "wu": "ffn_up", "wd": "ffn_down"}
+    shape = {"wq": (d, d), "wk": (d, d), "wv": (d, d), "wo": (d, d), "wg": (f, d), "wu": (f, d), "wd": (d, f)}
+    for li, lw in enumerate(wh["layers"]):
+        for m, nm in names.items():
+            dt, dims, raw = q(lw[m], *shape[m])
+            tens.append((f"blk.{li}.{nm}.weight", dt, dims, raw))
+        tens.append((f"blk.{li}.attn_norm.weight", 0, (d,), lw["attn_gain"].tobytes()))
+        tens.append((f"blk.{li}.ffn_norm.weight", 1, (d,), lw["ffn_gain"].astype(np.float16).tobytes()))
+    path.write_bytes(G.write(md, tens))
+
+
+def test_decoder_from_gguf_matches(dev, small_decoder, tmp_path):
+    """The same model read back from a GGUF file decodes bit-identically."""
+    say("decoder from gguf")
+    dec = small_decoder
+    p = tmp_path / "small.gguf"
+    write_gguf(p, dec)
+    dec2 = LlamaDecoder.from_gguf(dev, str(p), max_ctx=dec.cfg.max_ctx)
+    assert (dec2.cfg.dim, dec2.cfg.n_layers, dec2.cfg.n_heads, dec2.cfg.ffn, dec2.cfg.vocab) == \
+        (dec.cfg.dim, dec.cfg.n_layers, dec.cfg.n_heads, dec.cfg.ffn, dec.cfg.vocab)
+    prompt = [3, 141, 59, 26]
+    runs = []
+    for dd in (dec, dec2):
+        dd.start(prompt)
+        lg = []
+        for _ in range(10):
+            dd.enqueue_step()
+            lg.append(dd.logits.numpy())
+        runs.append((dd.tokens_host()[:11].copy(), np.stack(lg)))
+    np.testing.assert_array_equal(runs[0][0], runs[1][0])
+    assert np.array_equal(runs[0][1].view(np.uint32), runs[1][1].view(np.uint32))
+
+
+def test_decoder_from_gguf_tied_output_and_errors(dev, small_decoder, tmp_path):
+    """Without output.weight the quantized token_embd is the output matrix and
+    the embedding table is its device dequantization (to_float)."""
+    say("decoder from gguf, tied")
+    dec = small_decoder
+    p = tmp_path / "tied.gguf"
+    write_gguf(p, dec, tied=True)
+    dec3 = LlamaDecoder.from_gguf(dev, str(p), max_ctx=16)
+    raw, shape, dt = dec.weights_host()["out"]
+    blocks = np.frombuffer(raw.tobytes(), dtype=O.BLOCK_DTYPE[dt]).reshape(shape)
+    np.testing.assert_array_equal(dec3.embed.numpy().view(np.uint32),
+                                  O.dequantize(dt, blocks).reshape(dec.cfg.vocab, dec.cfg.dim).view(np.uint32))
+    assert dec3.weights_host()["out"][0].tobytes() == raw.tobytes()
+    from oracle import gguf as G
+    bad = tmp_path / "bad.gguf"
+    bad.write_bytes(G.write([("general.architecture", G.Value(G.VT_STRING, "llama"))], []))
+    with pytest.raises(ValueError, match="missing metadata|missing tensor"):
+        LlamaDecoder.from_gguf(dev, str(bad))
