@@ -410,11 +410,22 @@ hipError_t launch_cfg(const uint8_t* w, ActView act, float* y, float* part, size
     using T = MmqTile<F, RT, CT, WM, WN>;
     const int mt = (M + T::BM - 1) / T::BM, nt = (N + T::BN - 1) / T::BN;
     const int KB = K / QK_K;
-    // split K when the tile grid cannot fill two workgroups per CU, keeping >= 2 superblocks per split
+    // Split K when the tile grid leaves resident workgroup slots empty, as
+    // far as one round of the grid still fits them (a partial second round
+    // costs more than the split saves), keeping >= 2 superblocks per split.
+    static int occ = -1;  // resident workgroups per CU of this instantiation
+    if (occ < 0) {
+        int o = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, mmq_kernel<F, RT, CT, WM, WN, false>, T::NT, 0) !=
+                hipSuccess ||
+            o < 1)
+            o = 1;
+        occ = o;
+    }
     int ks = 1;
-    const int tiles = mt * nt;
-    if (part && tiles < 2 * num_cus) {
-        ks = (2 * num_cus + tiles - 1) / tiles;
+    const int tiles = mt * nt, cap = occ * num_cus;
+    if (part && tiles < cap) {
+        ks = cap / tiles;
         const int kmax = KB / 2 > 1 ? KB / 2 : 1;
         if (ks > kmax) ks = kmax;
         while (ks > 1 && (size_t)ks * M * N > part_elems) ks--;
@@ -450,7 +461,7 @@ hipError_t launch_grouped_fmt(const uint8_t* w, ActView act, float* y, int bm, i
 template <class F>
 hipError_t launch_fmt(const uint8_t* w, ActView act, float* y, float* part, size_t part_elems, int M, int N, int K,
                       int ldy, int num_cus, hipStream_t s, bool yh) {
-    if (M >= 128) return launch_cfg<F, 4, 2, 2, 2>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s, yh);  // 128 x 64
+    if (M >= 128) return launch_cfg<F, 4, 1, 2, 4>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s, yh);  // 128 x 64, 8 waves
     if (M >= 64) return launch_cfg<F, 2, 2, 2, 2>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s, yh);   // 64 x 64
     return launch_cfg<F, 2, 1, 1, 4>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s, yh);                // 32 x 64
 }
@@ -470,8 +481,9 @@ hipError_t launch_mmq_grouped(int dtype, const uint8_t* w, ActView act, float* y
 bool mmq_supported(int dtype) { return dtype == GGML_Q4K || dtype == GGML_Q6K; }
 
 size_t mmq_partial_elems(int M, int N, int num_cus) {
-    // enough split partials for the widest split launch_cfg picks (2 x CUs tiles)
-    return (size_t)M * N * (size_t)(2 * num_cus > 64 ? 64 : 2 * num_cus);
+    // split partials for up to 16 K splits (launch_cfg steps its split down to what fits)
+    (void)num_cus;
+    return (size_t)M * N * 16;
 }
 
 hipError_t launch_mmq(int dtype, const uint8_t* w, ActView act, float* y, float* part, size_t part_elems, int M,
