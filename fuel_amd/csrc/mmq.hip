@@ -31,6 +31,8 @@
 // flight while the current one is multiplied, and one barrier per superblock
 // separates the two buffers' roles.  Lanes build their B fragments in
 // registers from the raw blocks.
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -392,6 +394,209 @@ __global__ __launch_bounds__(64 * WM * WN) void mmq_kernel(const uint8_t* __rest
         }
 }
 
+// ---- Q4_K with the staging through LDS DMA ----
+// The same tile computation, but every superblock's activation rows, weight
+// blocks and activation scales go global -> LDS with global_load_lds (each
+// lane's 16 or 4 bytes land at the instruction's LDS base + lane * size), into
+// a ring of three LDS buffers: superblock b+2 is in flight while b is
+// multiplied, with no staging registers and no LDS stores.  The waits are
+// explicit: before superblock b is read, each wavefront lets only b+1's loads
+// stay outstanding (s_waitcnt vmcnt), then one barrier per superblock.  The
+// three buffers are distinct LDS objects and the loop is unrolled by three,
+// so the compiler sees which buffer each load writes and adds no waits of its
+// own.  Activation rows are stored 256 bytes apart with chunk j of row r at
+// position j ^ (r & 15): the 16 rows an MFMA fragment read touches fall in
+// different banks.  Needs 16-byte aligned weight blocks (Q4_K: 144 bytes).
+
+#define FRQ_VMCNT(n) ((((n) & 0xF) | (((n) >> 4) << 14) | (7 << 4) | (0xF << 8)))
+
+template <class F, int RT, int CT, int WM, int WN>
+struct DmaTile {
+    static constexpr int NW = WM * WN, NT = 64 * NW;
+    static constexpr int BM = 16 * RT * WM, BN = 16 * CT * WN;
+    static constexpr int A_INST = BM / 4;  // 16 chunks per row, 64 per instruction
+    static_assert(A_INST % NW == 0, "activation tile must split evenly over the wavefronts");
+    static constexpr int A_PW = A_INST / NW;
+    static constexpr int W_CH = BN * F::CH;
+    static constexpr int W_INST = (W_CH + 63) / 64;
+    static constexpr int W_PW = (W_INST + NW - 1) / NW;
+    static constexpr int D_PW = ((BM + 63) / 64 + NW - 1) / NW;
+    static constexpr int NI = A_PW + W_PW + D_PW;  // load instructions per wavefront and superblock
+    static_assert(NI <= 63, "vmcnt range");
+    static constexpr int LA = A_PW * NW * 1024, LW = W_PW * NW * 1024, LD = D_PW * NW * 64;
+};
+
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
+
+// (kept in device functions: the builtin may not appear in a kernel body the
+// host pass instantiates)
+__device__ __forceinline__ void lds_dma16(const uint8_t* g, uint8_t* l) { __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0); }
+__device__ __forceinline__ void lds_dma4(const uint8_t* g, uint8_t* l) { __builtin_amdgcn_global_load_lds(g, l, 4, 0, 0); }
+
+template <class F, int RT, int CT, int WM, int WN, bool GROUPED>
+__global__ __launch_bounds__(64 * WM * WN) void mmq_dma_kernel(const uint8_t* __restrict__ W, ActView act,
+                                                               float* __restrict__ y, int M, int N, int K, int ldy,
+                                                               int mt, int nt, int nsplit, int y_half, MmqGroup g) {
+    using T = DmaTile<F, RT, CT, WM, WN>;
+    constexpr int BM = T::BM, BN = T::BN, NW = T::NW;
+    __shared__ __align__(16) uint8_t sA0[T::LA], sA1[T::LA], sA2[T::LA];
+    __shared__ __align__(16) uint8_t sW0[T::LW], sW1[T::LW], sW2[T::LW];
+    __shared__ __align__(16) float sD0[T::LD], sD1[T::LD], sD2[T::LD];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+    const int KB = K / QK_K;
+    const uint32_t row_bytes = (uint32_t)KB * F::BYTES;
+    const int l16 = lane & 15, kb = lane >> 4;
+
+    int mtile, ntile, split;
+    if constexpr (GROUPED) {
+        mtile = blockIdx.x;
+        ntile = blockIdx.y;
+        split = 0;
+    } else {
+        const int total = mt * nt * nsplit, L = blockIdx.x;
+        const int x = L & 7, slot = L >> 3, q = total >> 3, r = total & 7;
+        const int t = x * q + (x < r ? x : r) + slot;  // XCD x's contiguous range of tiles
+        mtile = t % mt;
+        ntile = (t / mt) % nt;
+        split = t / (mt * nt);
+    }
+    const int b0 = (int)((long long)KB * split / nsplit), b1 = (int)((long long)KB * (split + 1) / nsplit);
+    const int n0 = ntile * BN;
+    int m0 = mtile * BM, mend = M, n_split = N;
+    const uint8_t* W1 = W;
+    const uint8_t* W2 = W;
+    const int* x_row = nullptr;
+    if constexpr (GROUPED) {
+        if (mtile >= *g.ntiles) return;  // uniform: the tile table is shorter than the grid bound
+        const int e = g.tile_expert[mtile];
+        m0 = g.tile_row0[mtile];
+        mend = g.expert_offsets[e + 1];
+        W1 = W + (size_t)e * g.expert_bytes;
+        W2 = g.w2 ? g.w2 + (size_t)e * g.expert_bytes : W1;
+        if (g.w2) n_split = g.n_split;
+        x_row = g.x_row;
+    }
+    const bool second = n0 >= n_split;  // the workgroup's columns lie on one side of n_split
+    const uint8_t* wbase = second ? W2 : W1;
+    const uint8_t* dbase = reinterpret_cast<const uint8_t*>(act.d);
+    const uint8_t* qbase = reinterpret_cast<const uint8_t*>(act.qs);
+
+    // per-lane source byte offsets of superblock 0 (padding slots read offset 0,
+    // a valid address; their LDS bytes are never used)
+    uint32_t asrc[T::A_PW], wsrc[T::W_PW], dsrc[T::D_PW];
+#pragma unroll
+    for (int j = 0; j < T::A_PW; j++) {
+        const int q = 64 * (j * NW + wave) + lane, r = q >> 4, m = m0 + r;
+        const int row = m < mend ? (x_row ? x_row[m] : m) : 0;
+        asrc[j] = (uint32_t)row * (uint32_t)K + 16u * (uint32_t)((q & 15) ^ (r & 15));
+    }
+#pragma unroll
+    for (int j = 0; j < T::W_PW; j++) {
+        const int q = 64 * (j * NW + wave) + lane;
+        int n = n0 + q / F::CH;
+        n = n < N ? n : N - 1;  // tail columns re-read a valid block; their outputs are dropped
+        wsrc[j] = q < T::W_CH ? (uint32_t)(second ? n - n_split : n) * row_bytes + F::src(q % F::CH) : 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < T::D_PW; j++) {
+        const int q = 64 * (j * NW + wave) + lane, m = m0 + q;
+        dsrc[j] = q < BM && m < mend ? 4u * (uint32_t)((x_row ? x_row[m] : m) * KB) : 0u;
+    }
+
+    auto issue = [&](int b, uint8_t* A, uint8_t* Wd, float* D) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < T::A_PW; j++) lds_dma16(qbase + (asrc[j] + (uint32_t)b * QK_K), A + 1024 * (j * NW + wave));
+#pragma unroll
+        for (int j = 0; j < T::W_PW; j++)
+            lds_dma16(wbase + (wsrc[j] + (uint32_t)b * F::BYTES), Wd + 1024 * (j * NW + wave));
+#pragma unroll
+        for (int j = 0; j < T::D_PW; j++)
+            lds_dma4(dbase + (dsrc[j] + 4u * (uint32_t)b), reinterpret_cast<uint8_t*>(D) + 256 * (j * NW + wave));
+    };
+
+    float facc[RT][CT][4];
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int c = 0; c < CT; c++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) facc[r][c][i] = 0.0f;
+
+    if (b0 < b1) issue(b0, sA0, sW0, sD0);
+    if (b0 + 1 < b1) issue(b0 + 1, sA1, sW1, sD1);
+
+    auto iter = [&](auto kr, int b) __attribute__((always_inline)) {
+        constexpr int KR = decltype(kr)::value;
+        uint8_t* A = KR == 0 ? sA0 : KR == 1 ? sA1 : sA2;
+        uint8_t* Wd = KR == 0 ? sW0 : KR == 1 ? sW1 : sW2;
+        float* D = KR == 0 ? sD0 : KR == 1 ? sD1 : sD2;
+        // superblock b landed (only b+1's loads may stay in flight), in every wavefront
+        if (b + 1 < b1) __builtin_amdgcn_s_waitcnt(FRQ_VMCNT(T::NI));
+        else __builtin_amdgcn_s_waitcnt(FRQ_VMCNT(0));
+        compiler_fence();
+        __builtin_amdgcn_s_barrier();
+        compiler_fence();
+        // the buffer of b+2 was last read in iteration b-1, which every wavefront has left
+        if (b + 2 < b1) {
+            constexpr int KN = (KR + 2) % 3;
+            issue(b + 2, KN == 0 ? sA0 : KN == 1 ? sA1 : sA2, KN == 0 ? sW0 : KN == 1 ? sW1 : sW2,
+                  KN == 0 ? sD0 : KN == 1 ? sD1 : sD2);
+        }
+        v4i acc[RT][CT][F::NACC];  // set by the first K step (zero accumulator input)
+        typename F::Hdr hdr[CT];
+#pragma unroll
+        for (int c = 0; c < CT; c++) F::header(Wd + (wn * CT * 16 + c * 16 + l16) * F::STRIDE, hdr[c]);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            v4i afr[RT];
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                const int row = wm * RT * 16 + r * 16 + l16;  // row & 15 == l16
+                afr[r] = *reinterpret_cast<const v4i*>(A + row * QK_K + 16 * ((4 * t + kb) ^ l16));
+            }
+#pragma unroll
+            for (int c = 0; c < CT; c++)
+                F::template step<RT, CT>(t, kb, c, Wd + (wn * CT * 16 + c * 16 + l16) * F::STRIDE, hdr[c], afr, acc);
+        }
+#pragma unroll
+        for (int r = 0; r < RT; r++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float dx = D[wm * RT * 16 + r * 16 + 4 * kb + i];
+#pragma unroll
+                for (int c = 0; c < CT; c++) facc[r][c][i] = fmaf(dx, F::finish(acc[r][c], i, hdr[c]), facc[r][c][i]);
+            }
+    };
+    for (int b = b0; b < b1; b += 3) {
+        iter(std::integral_constant<int, 0>{}, b);
+        if (b + 1 < b1) iter(std::integral_constant<int, 1>{}, b + 1);
+        if (b + 2 < b1) iter(std::integral_constant<int, 2>{}, b + 2);
+    }
+
+    float* out = nsplit > 1 ? y + (size_t)split * M * N : y;  // split partials: [z][M][N]
+    const int ld = nsplit > 1 ? N : ldy;
+    const bool half_out = y_half && nsplit == 1;
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int c = 0; c < CT; c++) {
+            const int n = n0 + wn * CT * 16 + c * 16 + l16;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = m0 + wm * RT * 16 + r * 16 + 4 * kb + i;
+                if (m < mend && n < N) {
+                    if (half_out)
+                        reinterpret_cast<uint16_t*>(out)[(size_t)m * ld + n] = f32_to_f16_rne(facc[r][c][i]);
+                    else
+                        out[(size_t)m * ld + n] = facc[r][c][i];
+                }
+            }
+        }
+}
+
 // y[m][n] = sum over splits z (in order) of part[z][m][n]
 __global__ void mmq_reduce_kernel(const float* __restrict__ part, float* __restrict__ y, int M, int N, int ldy,
                                   int nsplit, int y_half) {
@@ -441,6 +646,39 @@ hipError_t launch_cfg(const uint8_t* w, ActView act, float* y, float* part, size
 }
 
 template <class F, int RT, int CT, int WM, int WN>
+hipError_t launch_dma_cfg(const uint8_t* w, ActView act, float* y, float* part, size_t part_elems, int M, int N,
+                          int K, int ldy, int num_cus, hipStream_t s, bool y_half) {
+    using T = DmaTile<F, RT, CT, WM, WN>;
+    const int mt = (M + T::BM - 1) / T::BM, nt = (N + T::BN - 1) / T::BN;
+    const int KB = K / QK_K;
+    static int occ = -1;  // resident workgroups per CU of this instantiation
+    if (occ < 0) {
+        int o = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, mmq_dma_kernel<F, RT, CT, WM, WN, false>, T::NT, 0) !=
+                hipSuccess ||
+            o < 1)
+            o = 1;
+        occ = o;
+    }
+    int ks = 1;
+    const int tiles = mt * nt, cap = occ * num_cus;
+    if (part && tiles < cap) {  // K split as in launch_cfg
+        ks = cap / tiles;
+        const int kmax = KB / 2 > 1 ? KB / 2 : 1;
+        if (ks > kmax) ks = kmax;
+        while (ks > 1 && (size_t)ks * M * N > part_elems) ks--;
+    }
+    hipLaunchKernelGGL((mmq_dma_kernel<F, RT, CT, WM, WN, false>), dim3(mt * nt * ks), dim3(T::NT), 0, s, w, act,
+                       ks > 1 ? part : y, M, N, K, ldy, mt, nt, ks, (int)y_half, MmqGroup{});
+    if (ks > 1) {
+        const size_t total = (size_t)M * N;
+        hipLaunchKernelGGL(mmq_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, y, M, N,
+                           ldy, ks, (int)y_half);
+    }
+    return hipGetLastError();
+}
+
+template <class F, int RT, int CT, int WM, int WN>
 hipError_t launch_grouped_cfg(const uint8_t* w, ActView act, float* y, int max_tiles, int N, int K, int ldy,
                               const MmqGroup& g, hipStream_t s) {
     using T = MmqTile<F, RT, CT, WM, WN>;
@@ -474,6 +712,8 @@ hipError_t launch_mmq_grouped(int dtype, const uint8_t* w, ActView act, float* y
                               int ldy, const MmqGroup& g, hipStream_t s) {
     if (!mmq_supported(dtype) || max_tiles <= 0) return max_tiles == 0 ? hipSuccess : hipErrorInvalidValue;
     if (g.w2 && g.n_split % 64) return hipErrorInvalidValue;  // a column tile must not straddle W | W2
+    // (the register-staged kernel: the LDS DMA one measured 4-10% slower on the
+    // MoE layer's short K loops)
     if (dtype == GGML_Q4K) return launch_grouped_fmt<MmqQ4K>(w, act, y, bm, max_tiles, N, K, ldy, g, s);
     return launch_grouped_fmt<MmqQ6K>(w, act, y, bm, max_tiles, N, K, ldy, g, s);
 }
@@ -488,7 +728,15 @@ size_t mmq_partial_elems(int M, int N, int num_cus) {
 
 hipError_t launch_mmq(int dtype, const uint8_t* w, ActView act, float* y, float* part, size_t part_elems, int M,
                       int N, int K, int ldy, int num_cus, hipStream_t s, bool y_half) {
-    if (dtype == GGML_Q4K) return launch_fmt<MmqQ4K>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s, y_half);
+    if (dtype == GGML_Q4K) {
+        // 144-byte blocks allow the LDS DMA staging; it wins from M = 64 on
+        // (M = 512: 4-7%), the register-staged kernel at M < 64
+        if (M >= 128)
+            return launch_dma_cfg<MmqQ4K, 4, 1, 2, 4>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s, y_half);
+        if (M >= 64)
+            return launch_dma_cfg<MmqQ4K, 2, 2, 2, 2>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s, y_half);
+        return launch_fmt<MmqQ4K>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s, y_half);
+    }
     if (dtype == GGML_Q6K) return launch_fmt<MmqQ6K>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s, y_half);
     return hipErrorInvalidValue;
 }
