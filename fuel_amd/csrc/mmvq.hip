@@ -39,6 +39,9 @@ constexpr int qmv_wg_big() {
     return raw <= 36 ? 1024 : raw <= 48 ? 512 : qmv_wg<F, SPL>();
 }
 
+// The loads are unconditional (a slot past the row's last block re-reads that
+// block; qmv_row skips it): with no branch around them the in-order vmcnt
+// counter can wait for one row while the next row's loads stay in flight.
 template <class F, int SPL>
 __device__ __forceinline__ void qmv_load_row(const uint8_t* __restrict__ wr, int gi, int c, int KB,
                                              typename F::Raw (&r)[SPL]) {
@@ -46,7 +49,7 @@ __device__ __forceinline__ void qmv_load_row(const uint8_t* __restrict__ wr, int
 #pragma unroll
     for (int s = 0; s < SPL; s++) {
         const int b = gi + BPW * s;
-        if (b < KB) F::load(wr + (size_t)b * F::BYTES, c, r[s]);
+        F::load(wr + (size_t)(b < KB ? b : KB - 1) * F::BYTES, c, r[s]);
     }
 }
 
