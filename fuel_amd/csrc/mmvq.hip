@@ -99,7 +99,7 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
                                          int gxn, uint8_t* smem, float* s_red) {
     constexpr int NW = WG / 64;
     const int m = blockIdx.y;
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int gi = lane / F::LPB, c = lane % F::LPB;
     const int KB = K / F::ELEMS;
     const size_t row_bytes = (size_t)KB * F::BYTES;
@@ -154,13 +154,15 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
         act_row_load_swiglu<F::ACT, NW, MAXQ>(xr, xr2, K, w, lane, pre);
     else
         act_row_load<F::ACT, NW, MAXQ>(xr, K, w, lane, pre);
+    __builtin_amdgcn_sched_barrier(0);  // the activation loads go out ahead of the weight loads
     // rows >= n_split live in the second matrix (row - n_split)
     auto wrow = [&](int r) { return r < n_split ? W + (size_t)r * row_bytes : W2 + (size_t)(r - n_split) * row_bytes; };
     typename F::Raw ra[SPL], rb[SPL];
     float resa = 0.0f, resb = 0.0f;  // residual values, loaded ahead of their row's weights
-    if (row < N) {
-        if (acc_out && lane == 63) resa = yr[row];
-        qmv_load_row<F, SPL>(wrow(row), gi, c, KB, ra);
+    {  // (every lane, unconditionally: a wavefront without rows loads the last row and never uses it)
+        const int r0 = row < N ? row : N - 1;
+        if (acc_out) resa = yr[r0];
+        qmv_load_row<F, SPL>(wrow(r0), gi, c, KB, ra);
     }
     if (MODE == QMV_FUSED && ix.rms_gain) {
         // rms_norm_last_dim (sum of squares over the whole row, spread over the
@@ -177,7 +179,7 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
     while (row < N) {
         int nrow = row + nw;
         int lrow = nrow < N ? nrow : row;
-        if (acc_out && lane == 63) resb = yr[lrow];
+        if (acc_out) resb = yr[lrow];
         qmv_load_row<F, SPL>(wrow(lrow), gi, c, KB, rb);
         float t = qmv_row<F, SPL>(ra, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
         if (lane == 63) store(row, acc_out ? resa + t : t);
@@ -185,7 +187,7 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
         if (row >= N) break;
         nrow = row + nw;
         lrow = nrow < N ? nrow : row;
-        if (acc_out && lane == 63) resa = yr[lrow];
+        if (acc_out) resa = yr[lrow];
         qmv_load_row<F, SPL>(wrow(lrow), gi, c, KB, ra);
         t = qmv_row<F, SPL>(rb, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
         if (lane == 63) store(row, acc_out ? resb + t : t);

@@ -136,18 +136,39 @@ struct ActRowPre {
     float4 v[MAXQ];
 };
 
+// Lane `lane`'s four elements of chunk w + NW*i: live unless the chunk is past
+// the row (or, for Q8_0 rows that end on a 32-element block, the lane is past
+// K).  Every load is issued, from a clamped in-row offset, and nothing reads
+// the registers before the quantize step: a load under a lane condition would
+// make the compiler wait for it at once (to merge the zero and the loaded
+// value), before the first weight rows are even requested.  Values of dead
+// slots are never used unmasked.
+template <int ACT>
+__device__ __forceinline__ bool act_live(int ch, int nchunks, int K, int lane) {
+    return ch < nchunks && (ACT == GGML_Q8K || ch * QK_K + 4 * lane < K);
+}
+__device__ __forceinline__ int act_elem(int ch, int nchunks, int K, int lane) {
+    const int e = (ch < nchunks ? ch : nchunks - 1) * QK_K + 4 * lane;
+    return e < K - 4 ? e : K - 4;
+}
+
+// A relaxed (workgroup-scope) atomic load is an ordinary global load on this
+// target, but the compiler keeps it where it is written instead of sinking it
+// to its first use, so the row's loads go out ahead of the weight loads.
+__device__ __forceinline__ float4 load_f4_early(const float* p) {
+    const unsigned long long* q = reinterpret_cast<const unsigned long long*>(p);
+    const unsigned long long a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    const unsigned long long b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    return make_float4(__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32)),
+                       __uint_as_float((uint32_t)b), __uint_as_float((uint32_t)(b >> 32)));
+}
+
 template <int ACT, int NW, int MAXQ>
 __device__ __forceinline__ void act_row_load(const float* __restrict__ x, int K, int w, int lane,
                                              ActRowPre<MAXQ>& p) {
     const int nchunks = (K + QK_K - 1) / QK_K;
 #pragma unroll
-    for (int i = 0; i < MAXQ; i++) {
-        const int ch = w + NW * i;
-        p.v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        // Q8_0 rows end on a 32-element block that may leave the last chunk short
-        const bool live = ch < nchunks && (ACT == GGML_Q8K || ch * QK_K + 4 * lane < K);
-        if (live) p.v[i] = reinterpret_cast<const float4*>(x + (size_t)ch * QK_K)[lane];
-    }
+    for (int i = 0; i < MAXQ; i++) p.v[i] = load_f4_early(x + act_elem(w + NW * i, nchunks, K, lane));
 }
 
 // f16 activation row (matmul_f16, k_quants.rs:2333-2374): each half is
@@ -156,17 +177,13 @@ template <int ACT, int NW, int MAXQ>
 __device__ __forceinline__ void act_row_load_h(const uint16_t* __restrict__ x, int K, int w, int lane,
                                                ActRowPre<MAXQ>& p) {
     const int nchunks = (K + QK_K - 1) / QK_K;
+    uint2 h[MAXQ];
 #pragma unroll
-    for (int i = 0; i < MAXQ; i++) {
-        const int ch = w + NW * i;
-        p.v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        const bool live = ch < nchunks && (ACT == GGML_Q8K || ch * QK_K + 4 * lane < K);
-        if (live) {
-            const uint2 h = reinterpret_cast<const uint2*>(x + (size_t)ch * QK_K)[lane];
-            p.v[i] = make_float4(f16_to_f32(h.x & 0xffffu), f16_to_f32(h.x >> 16), f16_to_f32(h.y & 0xffffu),
-                                 f16_to_f32(h.y >> 16));
-        }
-    }
+    for (int i = 0; i < MAXQ; i++) h[i] = *reinterpret_cast<const uint2*>(x + act_elem(w + NW * i, nchunks, K, lane));
+#pragma unroll
+    for (int i = 0; i < MAXQ; i++)
+        p.v[i] = make_float4(f16_to_f32(h[i].x & 0xffffu), f16_to_f32(h[i].x >> 16), f16_to_f32(h[i].y & 0xffffu),
+                             f16_to_f32(h[i].y >> 16));
 }
 
 // SwiGLU input: silu(g) * u = g / (1 + exp(-g)) * u, element by element in the
@@ -197,27 +214,26 @@ template <int ACT, int NW, int MAXQ, class BlockSum>
 __device__ __forceinline__ void act_row_rms_norm(ActRowPre<MAXQ>& p, const float* __restrict__ gain, float eps, int K,
                                                  int w, int lane, BlockSum block_sum) {
     const int nchunks = (K + QK_K - 1) / QK_K;
+    float4 g[MAXQ];  // gains, loaded unconditionally like the row
+#pragma unroll
+    for (int i = 0; i < MAXQ; i++) g[i] = *reinterpret_cast<const float4*>(gain + act_elem(w + NW * i, nchunks, K, lane));
     float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < MAXQ; i++) {  // dead lanes / chunks hold zeros
-        ss = fmaf(p.v[i].x, p.v[i].x, ss);
-        ss = fmaf(p.v[i].y, p.v[i].y, ss);
-        ss = fmaf(p.v[i].z, p.v[i].z, ss);
-        ss = fmaf(p.v[i].w, p.v[i].w, ss);
+    for (int i = 0; i < MAXQ; i++) {  // dead lanes / chunks count as zeros
+        const float4 v = act_live<ACT>(w + NW * i, nchunks, K, lane) ? p.v[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
     }
     const float total = block_sum(dpp_wave_sum(ss));
     const float rinv = 1.0f / sqrtf(total * (1.0f / (float)K) + eps);
 #pragma unroll
-    for (int i = 0; i < MAXQ; i++) {
-        const int ch = w + NW * i;
-        const bool live = ch < nchunks && (ACT == GGML_Q8K || ch * QK_K + 4 * lane < K);
-        if (live) {
-            const float4 g = reinterpret_cast<const float4*>(gain + (size_t)ch * QK_K)[lane];
-            p.v[i].x = (p.v[i].x * rinv) * g.x;
-            p.v[i].y = (p.v[i].y * rinv) * g.y;
-            p.v[i].z = (p.v[i].z * rinv) * g.z;
-            p.v[i].w = (p.v[i].w * rinv) * g.w;
-        }
+    for (int i = 0; i < MAXQ; i++) {  // (dead slots are scaled too; they are never stored)
+        p.v[i].x = (p.v[i].x * rinv) * g[i].x;
+        p.v[i].y = (p.v[i].y * rinv) * g[i].y;
+        p.v[i].z = (p.v[i].z * rinv) * g[i].z;
+        p.v[i].w = (p.v[i].w * rinv) * g[i].w;
     }
 }
 
