@@ -25,12 +25,22 @@ namespace {
 constexpr int HD = ATTN_HEAD_DIM;
 constexpr int ATT_WG = 256;
 constexpr int GROUPS = ATT_WG / 16;  // positions in flight per workgroup (16 lanes each)
+static_assert(HD == 128 && ATT_WG == 2 * HD, "the rope / append stage maps HD/2 elements to a wave");
+constexpr int CMB_CHUNK = 8;        // splits whose partials one combine step loads together
 
 // Sum over 16-lane groups (lanes l and l^8, l^4, l^2, l^1).
 __device__ __forceinline__ float group16_sum(float v) {
 #pragma unroll
     for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off);
     return v;
+}
+
+// A relaxed workgroup-scope atomic load is a plain global load here; the
+// compiler keeps it where it is written (ahead of the pos check) instead of
+// sinking it to its use.
+__device__ __forceinline__ float load_early(const float* p) {
+    return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_WORKGROUP));
 }
 
 // Raw f16 x 8 chunk (one 16-byte load) to floats.
@@ -61,6 +71,13 @@ __global__ __launch_bounds__(ATT_WG) void attn_split_kernel(const float* __restr
     const int h = blockIdx.x, sp = blockIdx.y, H = gridDim.x, nsplit = gridDim.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = tid >> 4, l16 = tid & 15;
+    // 1. the new row's inputs, issued before pos is known: wave 0 rotates q,
+    // wave 1 rotates k (elements lane and lane + HD/2), waves 2 and 3 take
+    // v's two halves (one element each; hi repeats lo's address there).
+    const int w = __builtin_amdgcn_readfirstlane(wave);
+    const float* xs = w == 0 ? qk + (size_t)h * HD
+                             : (w == 1 ? qk + (size_t)(H + h) * HD : vn + (size_t)h * HD + (HD / 2) * (w - 2));
+    const float x_lo = load_early(xs + lane), x_hi = load_early(xs + (w < 2 ? lane + HD / 2 : lane));
     const int pos = *pos_p;
     if (pos < 0 || pos >= max_ctx) return;  // the combine writes NaN
     const int n = pos + 1;
@@ -68,46 +85,46 @@ __global__ __launch_bounds__(ATT_WG) void attn_split_kernel(const float* __restr
     const int p0 = min(n, sp * chunk), p1 = min(n, p0 + chunk);
     const bool owner = p0 < p1 && p1 == n;  // this split holds the new position
     const size_t cbase = (size_t)h * max_ctx * HD;
+    const float* cs = rcos + (size_t)pos * HD;
+    const float* sn = rsin + (size_t)pos * HD;
+    const float c_lo = cs[lane], c_hi = cs[lane + HD / 2], s_lo = sn[lane], s_hi = sn[lane + HD / 2];
+    __builtin_amdgcn_sched_barrier(0);
 
-    // 1. all K / V loads of the range (row pos is stale in memory; replaced below)
+    // 2. every K / V load of the range, from positions clamped into it (p1 >= 1
+    // always: an empty range is [n, n)); slots past p1 are masked at use.  Row
+    // pos is stale in memory and is replaced below.
     uint4 kr[ATTN_NIT], vr[ATTN_NIT];
 #pragma unroll
     for (int it = 0; it < ATTN_NIT; it++) {
-        const int j = p0 + g + GROUPS * it;
-        kr[it] = uint4{0u, 0u, 0u, 0u};
-        vr[it] = uint4{0u, 0u, 0u, 0u};
-        if (j < p1) {
-            kr[it] = *reinterpret_cast<const uint4*>(kc + cbase + (size_t)j * HD + 8 * l16);
-            vr[it] = *reinterpret_cast<const uint4*>(vc + cbase + (size_t)j * HD + 8 * l16);
-        }
+        const int j = min(p0 + g + GROUPS * it, p1 - 1);
+        kr[it] = *reinterpret_cast<const uint4*>(kc + cbase + (size_t)j * HD + 8 * l16);
+        vr[it] = *reinterpret_cast<const uint4*>(vc + cbase + (size_t)j * HD + 8 * l16);
     }
-    // 2. rope(q); in the owner split rope(k) and v, rounded to f16 and appended
-    const float* cs = rcos + (size_t)pos * HD;
-    const float* sn = rsin + (size_t)pos * HD;
-    if (tid < HD / 2) {  // out[i] = x[i] cos[i] - x[i+h] sin[i], out[i+h] = x[i+h] cos[i+h] + x[i] sin[i+h]
-        const float* q = qk + (size_t)h * HD;
-        const float lo = q[tid], hi = q[tid + HD / 2];
-        s_q[tid] = lo * cs[tid] - hi * sn[tid];
-        s_q[tid + HD / 2] = hi * cs[tid + HD / 2] + lo * sn[tid + HD / 2];
-    } else if (tid < HD && owner) {
-        const int i = tid - HD / 2;
-        const float* k = qk + (size_t)(H + h) * HD;
-        const float lo = k[i], hi = k[i + HD / 2];
-        const __half a = __float2half(lo * cs[i] - hi * sn[i]);
-        const __half b = __float2half(hi * cs[i + HD / 2] + lo * sn[i + HD / 2]);
-        kc[cbase + (size_t)pos * HD + i] = a;
-        kc[cbase + (size_t)pos * HD + i + HD / 2] = b;
-        s_kn[i] = __half2float(a);
-        s_kn[i + HD / 2] = __half2float(b);
-    } else if (tid >= HD && owner) {
-        const int i = tid - HD;
-        const __half a = __float2half(vn[(size_t)h * HD + i]);
-        vc[cbase + (size_t)pos * HD + i] = a;
-        s_vn[i] = __half2float(a);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 3. rope(q); in the owner split rope(k) and v, rounded to f16 and appended.
+    // out[i] = x[i] cos[i] - x[i+h] sin[i], out[i+h] = x[i+h] cos[i+h] + x[i] sin[i+h]
+    if (w == 0) {
+        s_q[lane] = x_lo * c_lo - x_hi * s_lo;
+        s_q[lane + HD / 2] = x_hi * c_hi + x_lo * s_hi;
+    } else if (owner) {
+        if (w == 1) {
+            const __half a = __float2half(x_lo * c_lo - x_hi * s_lo);
+            const __half b = __float2half(x_hi * c_hi + x_lo * s_hi);
+            kc[cbase + (size_t)pos * HD + lane] = a;
+            kc[cbase + (size_t)pos * HD + lane + HD / 2] = b;
+            s_kn[lane] = __half2float(a);
+            s_kn[lane + HD / 2] = __half2float(b);
+        } else {
+            const int i = lane + (HD / 2) * (w - 2);
+            const __half a = __float2half(x_lo);
+            vc[cbase + (size_t)pos * HD + i] = a;
+            s_vn[i] = __half2float(a);
+        }
     }
     __syncthreads();
 
-    // 3. scores (all 16 lanes of a group end with their position's score)
+    // 4. scores (all 16 lanes of a group end with their position's score)
     float q8[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) q8[e] = s_q[8 * l16 + e];
@@ -129,7 +146,7 @@ __global__ __launch_bounds__(ATT_WG) void attn_split_kernel(const float* __restr
         sc[it] = j < p1 ? d : -__builtin_inff();
         mx = fmaxf(mx, sc[it]);
     }
-    // 4. softmax statistics of the range, weighted values
+    // 5. softmax statistics of the range, weighted values
 #pragma unroll
     for (int off = 32; off >= 16; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
     if (lane == 0) s_red[wave] = mx;
@@ -147,6 +164,10 @@ __global__ __launch_bounds__(ATT_WG) void attn_split_kernel(const float* __restr
         l += p;
         float vv[8];
         h8_to_f(vr[it], vv);
+        if (j >= p1) {  // a clamped slot (p is 0 there): keep stale rows out of the sum
+#pragma unroll
+            for (int e = 0; e < 8; e++) vv[e] = 0.0f;
+        }
         if (owner && j == pos) {
 #pragma unroll
             for (int e = 0; e < 8; e++) vv[e] = s_vn[8 * l16 + e];
@@ -154,7 +175,7 @@ __global__ __launch_bounds__(ATT_WG) void attn_split_kernel(const float* __restr
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[e] = fmaf(p, vv[e], acc[e]);
     }
-    // 5. sum over the 16 groups: in-wave across the 4 groups, then over waves
+    // 6. sum over the 16 groups: in-wave across the 4 groups, then over waves
 #pragma unroll
     for (int off = 32; off >= 16; off >>= 1) {
         l += __shfl_xor(l, off);
@@ -184,24 +205,46 @@ __global__ __launch_bounds__(ATT_WG) void attn_split_kernel(const float* __restr
 }
 
 // out[h] = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M) over the splits.
+// The partials of CMB_CHUNK splits are loaded together (clamped split index,
+// masked at use) so that a step is one memory round trip; M and the running
+// sums are rescaled between steps (one step, hence the plain formula above,
+// for nsplit <= CMB_CHUNK).  Split 0 is never empty, so M is finite after the
+// first step.  pos is loaded first and checked by a select at the end: the
+// partial loads do not wait for it.
 __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restrict__ part, int nsplit, int max_ctx,
                                                          const int* __restrict__ pos_p, float* __restrict__ out) {
     const int h = blockIdx.x, tid = threadIdx.x;
-    const int pos = *pos_p;
-    if (pos < 0 || pos >= max_ctx) {
-        out[(size_t)h * HD + tid] = __builtin_nanf("");
-        return;
-    }
+    const int pos = __float_as_int(load_early(reinterpret_cast<const float*>(pos_p)));
     const float* ph = part + (size_t)h * nsplit * (HD + 2);
-    float M = -__builtin_inff();
-    for (int s = 0; s < nsplit; s++) M = fmaxf(M, ph[s * (HD + 2) + HD]);
-    float L = 0.0f, O = 0.0f;
-    for (int s = 0; s < nsplit; s++) {
-        const float f = expf(ph[s * (HD + 2) + HD] - M);  // an empty range has max -inf: factor 0
-        L = fmaf(ph[s * (HD + 2) + HD + 1], f, L);
-        O = fmaf(ph[s * (HD + 2) + tid], f, O);
+    float M = -__builtin_inff(), L = 0.0f, O = 0.0f;
+    for (int s0 = 0; s0 < nsplit; s0 += CMB_CHUNK) {
+        float m[CMB_CHUNK], l[CMB_CHUNK], o[CMB_CHUNK];
+#pragma unroll
+        for (int c = 0; c < CMB_CHUNK; c++) o[c] = load_early(ph + (size_t)min(s0 + c, nsplit - 1) * (HD + 2) + tid);
+#pragma unroll
+        for (int c = 0; c < CMB_CHUNK; c++) {
+            const float* q = ph + (size_t)min(s0 + c, nsplit - 1) * (HD + 2);
+            m[c] = q[HD];
+            l[c] = q[HD + 1];
+        }
+        float Mn = M;
+#pragma unroll
+        for (int c = 0; c < CMB_CHUNK; c++) Mn = fmaxf(Mn, s0 + c < nsplit ? m[c] : -__builtin_inff());
+        if (Mn != M) {  // M = -inf only before the first step, where L = O = 0
+            const float r = expf(M - Mn);
+            L *= r;
+            O *= r;
+            M = Mn;
+        }
+#pragma unroll
+        for (int c = 0; c < CMB_CHUNK; c++) {
+            // an empty range has max -inf: factor 0; a clamped (repeated) split: factor 0
+            const float f = s0 + c < nsplit ? expf(m[c] - M) : 0.0f;
+            L = fmaf(l[c], f, L);
+            O = fmaf(o[c], f, O);
+        }
     }
-    out[(size_t)h * HD + tid] = O / L;
+    out[(size_t)h * HD + tid] = (pos < 0 || pos >= max_ctx) ? __builtin_nanf("") : O / L;
 }
 
 constexpr int AM_WG = 1024;

@@ -148,6 +148,10 @@ def test_attention_decode(dev, H, max_ctx, pos):
     rng = np.random.default_rng(pos + H)
     kc = rng.standard_normal((H, max_ctx, 128)).astype(np.float16)
     vc = rng.standard_normal((H, max_ctx, 128)).astype(np.float16)
+    # rows pos.. are not attended (row pos is replaced by the append): NaN there
+    # must not reach the output
+    kc[:, pos:] = np.float16(np.nan)
+    vc[:, pos:] = np.float16(np.nan)
     a.kc.copy_from(kc.view(np.uint16))
     a.vc.copy_from(vc.view(np.uint16))
     qk = O.normal((2 * H * 128,), seed=pos, stream=1, std=2.0)
@@ -160,6 +164,8 @@ def test_attention_decode(dev, H, max_ctx, pos):
     vc[:, pos] = v.reshape(H, 128).astype(np.float16)
     np.testing.assert_array_equal(a.kc.numpy()[:, pos], kc[:, pos].view(np.uint16))
     np.testing.assert_array_equal(a.vc.numpy()[:, pos], vc[:, pos].view(np.uint16))
+    kc[:, pos + 1:] = 0
+    vc[:, pos + 1:] = 0
     want = O.attention_decode(q, kc.astype(np.float32), vc.astype(np.float32), pos + 1,
                               float(np.float32(1 / np.sqrt(128.0))))
     assert rel_err(got, want) < 1e-5
