@@ -76,6 +76,8 @@ SIGNATURES = {
     "frq_attention_decode_workspace": (_sz, [_sz, _sz]),
     "frq_attention_decode": (_i32, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _sz,
                                     _vp]),
+    "frq_attention_decode_oproj": (_i32, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_float, _vp,
+                                          _sz, _i32, _vp, _sz, _vp]),
     "frq_argmax_embed": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _vp, _vp]),
     "frq_block_isums": (_i32, [_vp, _i32, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
     "frq_fill_random_bits": (_i32, [_vp, _vp, _sz, C.c_uint64, C.c_uint64, C.c_uint32, C.c_uint32]),

@@ -854,6 +854,52 @@ int frq_attention_decode(frq_device* dev, size_t n_heads, size_t head_dim, size_
     return FRQ_OK;
 }
 
+int frq_attention_decode_oproj(frq_device* dev, size_t n_heads, size_t head_dim, size_t max_ctx, const float* qk,
+                               const float* v, const float* rcos, const float* rsin, uint16_t* kc, uint16_t* vc,
+                               const int32_t* pos, float scale, void* work, size_t work_bytes, int o_dtype,
+                               const void* w_o, size_t n_out, float* y) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (head_dim != (size_t)ATTN_HEAD_DIM)
+        return fail(FRQ_UNSUPPORTED, "attention_decode_oproj: head_dim=%zu (supported: %d)", head_dim, ATTN_HEAD_DIM);
+    const size_t need = frq_attention_decode_workspace(n_heads, max_ctx);
+    if (need == 0) return fail(FRQ_INVALID, "attention_decode_oproj: n_heads=%zu max_ctx=%zu", n_heads, max_ctx);
+    if (!is_weight_type(o_dtype)) return fail(FRQ_UNSUPPORTED, "attention_decode_oproj: o dtype %d", o_dtype);
+    const size_t k = n_heads * head_dim;
+    if (k % QK_K || k > qmv_kmax(o_dtype))
+        return fail(FRQ_UNSUPPORTED, "attention_decode_oproj: n_heads * head_dim = %zu (needs a multiple of %d, <= %zu)",
+                    k, QK_K, qmv_kmax(o_dtype));
+    if (n_out == 0 || n_out > (size_t)0x7fffffff) return fail(FRQ_INVALID, "attention_decode_oproj: n_out=%zu", n_out);
+    if (!qk || !v || !rcos || !rsin || !kc || !vc || !pos || !work || !w_o || !y)
+        return fail(FRQ_INVALID, "attention_decode_oproj: null buffer");
+    if (work_bytes < need)
+        return fail(FRQ_WORKSPACE, "attention_decode_oproj: workspace %zu < %zu bytes", work_bytes, need);
+    if (!aligned16(kc) || !aligned16(vc) || !aligned16(work) || !aligned4(w_o) || !aligned4(y))
+        return fail(FRQ_MISALIGNED,
+                    "attention_decode_oproj: caches and work must be 16-byte aligned, w_o and y 4-byte aligned");
+    float* part = static_cast<float*>(work);
+    const int ns = attn_decode_splits((int)n_heads, (int)max_ctx);
+    QmvOpts o{};
+    o.accumulate = 1;
+    if (ns <= ATTN_MERGE_CHUNK) {  // the merge inside the mat-vec: two launches
+        HIP_TRY(launch_attn_split(qk, v, rcos, rsin, kc, vc, (int)n_heads, (int)max_ctx, pos, scale, part,
+                                  dev->stream));
+        o.attn_nsplit = ns;
+        o.attn_max_ctx = (int)max_ctx;
+        o.attn_pos = pos;
+        HIP_TRY(launch_qmv_attn(o_dtype, static_cast<const uint8_t*>(w_o), part, y, (int)n_out, (int)k, o,
+                                dev->stream, dev->num_cus));
+    } else {  // more splits than one merge step holds: the merge kernel into the workspace's tail
+        float* att = part + (size_t)n_heads * ns * ATTN_PSTRIDE;
+        HIP_TRY(launch_attn_decode(qk, v, rcos, rsin, kc, vc, (int)n_heads, (int)max_ctx, pos, scale, part, att,
+                                   dev->stream));
+        o.ldx = (int)k;
+        HIP_TRY(launch_qmv_fused(o_dtype, static_cast<const uint8_t*>(w_o), att, y, 1, (int)n_out, (int)k,
+                                 (int)n_out, o, dev->stream, dev->num_cus));
+    }
+    return FRQ_OK;
+}
+
 int frq_argmax_embed(frq_device* dev, const float* logits, size_t vocab, const float* table, size_t dim, int32_t* tokens,
                      size_t tokens_cap, size_t prompt_len, int32_t* pos, float* x) {
     int rc = use_device(dev);

@@ -6,7 +6,8 @@
 //   fuel-cpu-backend/src/byte_kernels.rs:1885-1964), append of k and v to an
 //   f16 KV cache, scores (q . k_j) * scale, softmax over j <= pos and the
 //   weighted sum of the values, per head.  The context is split over
-//   workgroups (flash-decoding) and a second kernel merges the splits.
+//   workgroups (flash-decoding); the splits are merged by a second kernel
+//   here, or inside the o-projection mat-vec (mmvq.hip, QMV_ATTN).
 //
 //   argmax + embedding: the next token (the prompt's while it lasts, else the
 //   first-index argmax of the logits, argmax_dim_f32 byte_kernels.rs:8246),
@@ -15,6 +16,7 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
+#include "attn.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -26,21 +28,12 @@ constexpr int HD = ATTN_HEAD_DIM;
 constexpr int ATT_WG = 256;
 constexpr int GROUPS = ATT_WG / 16;  // positions in flight per workgroup (16 lanes each)
 static_assert(HD == 128 && ATT_WG == 2 * HD, "the rope / append stage maps HD/2 elements to a wave");
-constexpr int CMB_CHUNK = 8;        // splits whose partials one combine step loads together
 
 // Sum over 16-lane groups (lanes l and l^8, l^4, l^2, l^1).
 __device__ __forceinline__ float group16_sum(float v) {
 #pragma unroll
     for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off);
     return v;
-}
-
-// A relaxed workgroup-scope atomic load is a plain global load here; the
-// compiler keeps it where it is written (ahead of the pos check) instead of
-// sinking it to its use.
-__device__ __forceinline__ float load_early(const float* p) {
-    return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_WORKGROUP));
 }
 
 // Raw f16 x 8 chunk (one 16-byte load) to floats.
@@ -77,7 +70,7 @@ __global__ __launch_bounds__(ATT_WG) void attn_split_kernel(const float* __restr
     const int w = __builtin_amdgcn_readfirstlane(wave);
     const float* xs = w == 0 ? qk + (size_t)h * HD
                              : (w == 1 ? qk + (size_t)(H + h) * HD : vn + (size_t)h * HD + (HD / 2) * (w - 2));
-    const float x_lo = load_early(xs + lane), x_hi = load_early(xs + (w < 2 ? lane + HD / 2 : lane));
+    const float x_lo = attn_load_early(xs + lane), x_hi = attn_load_early(xs + (w < 2 ? lane + HD / 2 : lane));
     const int pos = *pos_p;
     if (pos < 0 || pos >= max_ctx) return;  // the combine writes NaN
     const int n = pos + 1;
@@ -188,7 +181,7 @@ __global__ __launch_bounds__(ATT_WG) void attn_split_kernel(const float* __restr
     }
     if (lane == 0) s_red[wave] = l;
     __syncthreads();
-    float* pp = part + ((size_t)h * nsplit + sp) * (HD + 2);
+    float* pp = part + ((size_t)h * nsplit + sp) * ATTN_PSTRIDE;
     if (tid < HD) {
         float o = 0.0f;
 #pragma unroll
@@ -204,47 +197,31 @@ __global__ __launch_bounds__(ATT_WG) void attn_split_kernel(const float* __restr
     }
 }
 
-// out[h] = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M) over the splits.
-// The partials of CMB_CHUNK splits are loaded together (clamped split index,
-// masked at use) so that a step is one memory round trip; M and the running
-// sums are rescaled between steps (one step, hence the plain formula above,
-// for nsplit <= CMB_CHUNK).  Split 0 is never empty, so M is finite after the
-// first step.  pos is loaded first and checked by a select at the end: the
-// partial loads do not wait for it.
+// out[h] = the merge of the head's split partials (attn_merge_step, attn.hpp),
+// one element per thread.  The partials of ATTN_MERGE_CHUNK splits are loaded
+// together (clamped split index) so that a step is one memory round trip;
+// pos is loaded first and checked by a select at the end: the partial loads
+// do not wait for it.
 __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restrict__ part, int nsplit, int max_ctx,
                                                          const int* __restrict__ pos_p, float* __restrict__ out) {
     const int h = blockIdx.x, tid = threadIdx.x;
-    const int pos = __float_as_int(load_early(reinterpret_cast<const float*>(pos_p)));
-    const float* ph = part + (size_t)h * nsplit * (HD + 2);
-    float M = -__builtin_inff(), L = 0.0f, O = 0.0f;
-    for (int s0 = 0; s0 < nsplit; s0 += CMB_CHUNK) {
-        float m[CMB_CHUNK], l[CMB_CHUNK], o[CMB_CHUNK];
+    const int pos = __float_as_int(attn_load_early(reinterpret_cast<const float*>(pos_p)));
+    const float* ph = part + (size_t)h * nsplit * ATTN_PSTRIDE;
+    float M = -__builtin_inff(), L = 0.0f, O[1] = {0.0f};
+    for (int s0 = 0; s0 < nsplit; s0 += ATTN_MERGE_CHUNK) {
+        float m[ATTN_MERGE_CHUNK], l[ATTN_MERGE_CHUNK], o[ATTN_MERGE_CHUNK][1];
 #pragma unroll
-        for (int c = 0; c < CMB_CHUNK; c++) o[c] = load_early(ph + (size_t)min(s0 + c, nsplit - 1) * (HD + 2) + tid);
+        for (int c = 0; c < ATTN_MERGE_CHUNK; c++)
+            o[c][0] = attn_load_early(ph + (size_t)min(s0 + c, nsplit - 1) * ATTN_PSTRIDE + tid);
 #pragma unroll
-        for (int c = 0; c < CMB_CHUNK; c++) {
-            const float* q = ph + (size_t)min(s0 + c, nsplit - 1) * (HD + 2);
+        for (int c = 0; c < ATTN_MERGE_CHUNK; c++) {
+            const float* q = ph + (size_t)min(s0 + c, nsplit - 1) * ATTN_PSTRIDE;
             m[c] = q[HD];
             l[c] = q[HD + 1];
         }
-        float Mn = M;
-#pragma unroll
-        for (int c = 0; c < CMB_CHUNK; c++) Mn = fmaxf(Mn, s0 + c < nsplit ? m[c] : -__builtin_inff());
-        if (Mn != M) {  // M = -inf only before the first step, where L = O = 0
-            const float r = expf(M - Mn);
-            L *= r;
-            O *= r;
-            M = Mn;
-        }
-#pragma unroll
-        for (int c = 0; c < CMB_CHUNK; c++) {
-            // an empty range has max -inf: factor 0; a clamped (repeated) split: factor 0
-            const float f = s0 + c < nsplit ? expf(m[c] - M) : 0.0f;
-            L = fmaf(l[c], f, L);
-            O = fmaf(o[c], f, O);
-        }
+        attn_merge_step<1>(o, m, l, s0, nsplit, M, L, O);
     }
-    out[(size_t)h * HD + tid] = (pos < 0 || pos >= max_ctx) ? __builtin_nanf("") : O / L;
+    out[(size_t)h * HD + tid] = (pos < 0 || pos >= max_ctx) ? __builtin_nanf("") : O[0] / L;
 }
 
 constexpr int AM_WG = 1024;
@@ -304,16 +281,28 @@ int attn_decode_splits(int n_heads, int max_ctx) {
 }
 
 size_t attn_decode_work_bytes(int n_heads, int max_ctx) {
-    return (size_t)n_heads * attn_decode_splits(n_heads, max_ctx) * (HD + 2) * sizeof(float);
+    // the split partials, then room for the merged output (n_heads * HD) for
+    // callers that merge into scratch (frq_attention_decode_oproj with many splits)
+    return ((size_t)n_heads * attn_decode_splits(n_heads, max_ctx) * ATTN_PSTRIDE + (size_t)n_heads * HD) *
+           sizeof(float);
+}
+
+hipError_t launch_attn_split(const float* qk, const float* v, const float* rcos, const float* rsin, uint16_t* kc,
+                             uint16_t* vc, int n_heads, int max_ctx, const int* pos, float scale, float* part,
+                             hipStream_t s) {
+    const int ns = attn_decode_splits(n_heads, max_ctx);
+    hipLaunchKernelGGL(attn_split_kernel, dim3(n_heads, ns), dim3(ATT_WG), 0, s, qk, v, rcos, rsin,
+                       reinterpret_cast<__half*>(kc), reinterpret_cast<__half*>(vc), max_ctx, pos, scale, part);
+    return hipGetLastError();
 }
 
 hipError_t launch_attn_decode(const float* qk, const float* v, const float* rcos, const float* rsin, uint16_t* kc,
                               uint16_t* vc, int n_heads, int max_ctx, const int* pos, float scale, float* part,
                               float* out, hipStream_t s) {
-    const int ns = attn_decode_splits(n_heads, max_ctx);
-    hipLaunchKernelGGL(attn_split_kernel, dim3(n_heads, ns), dim3(ATT_WG), 0, s, qk, v, rcos, rsin,
-                       reinterpret_cast<__half*>(kc), reinterpret_cast<__half*>(vc), max_ctx, pos, scale, part);
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(HD), 0, s, part, ns, max_ctx, pos, out);
+    const hipError_t e = launch_attn_split(qk, v, rcos, rsin, kc, vc, n_heads, max_ctx, pos, scale, part, s);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(HD), 0, s, part, attn_decode_splits(n_heads, max_ctx),
+                       max_ctx, pos, out);
     return hipGetLastError();
 }
 

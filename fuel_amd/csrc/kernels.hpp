@@ -50,11 +50,21 @@ struct QmvOpts {
     const float* rms_gain;
     float rms_eps;
     int accumulate;
+    // attention-merging mode (launch_qmv_attn): x holds the decode-attention
+    // split partials, M = 1
+    int attn_nsplit;
+    int attn_max_ctx;
+    const int* attn_pos;
 };
 hipError_t launch_qmv_indexed(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
                               const QmvOpts& ix, hipStream_t s, int num_cus);
 hipError_t launch_qmv_fused(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
                             const QmvOpts& o, hipStream_t s, int num_cus);
+// y [N] (+)= W a where a [K = heads * ATTN_HEAD_DIM] is the merge of the
+// decode-attention partials in `part` (attn_decode_work layout, o.attn_*
+// set): the merge runs in each workgroup's activation stage.
+hipError_t launch_qmv_attn(int dtype, const uint8_t* w, const float* part, float* y, int N, int K, const QmvOpts& o,
+                           hipStream_t s, int num_cus);
 // Two fused mat-vecs of the same activation rows (ldx apart, optional RMS
 // norm from `o`) in one launch: y1 [M, n1] = W1 a(x), y2 [M, n2] = W2 a(x);
 // Q4K / Q6K weights, K <= 16384.
@@ -134,11 +144,18 @@ hipError_t launch_normal(float* y, size_t n, unsigned long long seed, uint32_t s
 constexpr int ATTN_HEAD_DIM = 128;
 constexpr int ATTN_NIT = 8;                     // positions per 16-lane group and split
 constexpr int ATTN_MAX_CHUNK = 16 * ATTN_NIT;   // positions per split (256-thread workgroups)
+constexpr int ATTN_PSTRIDE = ATTN_HEAD_DIM + 4; // floats per (head, split) partial: o, max, sum, 2 pad (16-byte rows)
+constexpr int ATTN_MERGE_CHUNK = 8;             // splits merged per step
 int attn_decode_splits(int n_heads, int max_ctx);
 size_t attn_decode_work_bytes(int n_heads, int max_ctx);
 hipError_t launch_attn_decode(const float* qk, const float* v, const float* rcos, const float* rsin, uint16_t* kc,
                               uint16_t* vc, int n_heads, int max_ctx, const int* pos, float scale, float* part,
                               float* out, hipStream_t s);
+// The split kernel alone (partials into `part`), for a consumer that merges
+// them itself (launch_qmv_attn).
+hipError_t launch_attn_split(const float* qk, const float* v, const float* rcos, const float* rsin, uint16_t* kc,
+                             uint16_t* vc, int n_heads, int max_ctx, const int* pos, float scale, float* part,
+                             hipStream_t s);
 hipError_t launch_argmax_embed(const float* logits, int vocab, const float* table, int dim, int* tokens,
                                int tokens_cap, int prompt_len, int* pos, float* x, hipStream_t s);
 

@@ -14,6 +14,7 @@
 //
 // The only rounding after the exact integer stage is the f32 combination
 // y += d_w*d_x*isum - dmin_w*d_x*msum.
+#include "attn.hpp"
 #include "common.hpp"
 #include "formats.hpp"
 #include "kernels.hpp"
@@ -81,7 +82,66 @@ __device__ __forceinline__ float qmv_row(const typename F::Raw (&r)[SPL], const 
 
 // QMV_HALF: f16 activations in (x holds halves), f16 outputs (y holds
 // halves, f16::from_f32 = round to nearest even of the f32 row sum).
-enum QmvMode { QMV_PLAIN = 0, QMV_INDEXED = 1, QMV_FUSED = 2, QMV_HALF = 3 };
+// QMV_ATTN: x holds decode-attention split partials; the activation row is
+// their merge (attn_merge_step), residual add as QMV_FUSED.
+enum QmvMode { QMV_PLAIN = 0, QMV_INDEXED = 1, QMV_FUSED = 2, QMV_HALF = 3, QMV_ATTN = 4 };
+
+// Activation stage of QMV_ATTN: lane `lane`'s four elements of chunk
+// w + NW*i are elements d..d+3 of head hd (HD = ATTN_HEAD_DIM per head).  The
+// partials of its (at most ATTN_MERGE_CHUNK) splits are loaded with the other
+// activation loads (attn_row_load) and merged once the first weight rows are
+// requested (attn_row_merge: one attn_merge_step).
+template <int MAXQ>
+struct AttnRowPre {
+    float4 o[MAXQ][ATTN_MERGE_CHUNK];
+    float2 ml[MAXQ][ATTN_MERGE_CHUNK];  // (max, sum)
+};
+
+__device__ __forceinline__ float2 load_f2_early(const float* p) {
+    const unsigned long long a = __hip_atomic_load(reinterpret_cast<const unsigned long long*>(p), __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+    return make_float2(__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32)));
+}
+
+template <int NW, int MAXQ>
+__device__ __forceinline__ void attn_row_load(const float* __restrict__ part, int nsplit, int K, int w, int lane,
+                                              AttnRowPre<MAXQ>& p) {
+    const int nchunks = K / QK_K;
+#pragma unroll
+    for (int i = 0; i < MAXQ; i++) {
+        const int e = act_elem(w + NW * i, nchunks, K, lane);
+        const float* ph = part + (size_t)(e / ATTN_HEAD_DIM) * nsplit * ATTN_PSTRIDE + e % ATTN_HEAD_DIM;
+        const float* pm = part + (size_t)(e / ATTN_HEAD_DIM) * nsplit * ATTN_PSTRIDE + ATTN_HEAD_DIM;
+#pragma unroll
+        for (int c = 0; c < ATTN_MERGE_CHUNK; c++) {
+            const size_t so = (size_t)(c < nsplit ? c : nsplit - 1) * ATTN_PSTRIDE;
+            p.o[i][c] = *reinterpret_cast<const float4*>(ph + so);
+            p.ml[i][c] = *reinterpret_cast<const float2*>(pm + so);
+        }
+    }
+}
+
+template <int NW, int MAXQ>
+__device__ __forceinline__ void attn_row_merge(const AttnRowPre<MAXQ>& p, int nsplit, bool pos_ok,
+                                               ActRowPre<MAXQ>& out) {
+#pragma unroll
+    for (int i = 0; i < MAXQ; i++) {
+        float M = -__builtin_inff(), L = 0.0f, O[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        float o[ATTN_MERGE_CHUNK][4], m[ATTN_MERGE_CHUNK], l[ATTN_MERGE_CHUNK];
+#pragma unroll
+        for (int c = 0; c < ATTN_MERGE_CHUNK; c++) {
+            o[c][0] = p.o[i][c].x;
+            o[c][1] = p.o[i][c].y;
+            o[c][2] = p.o[i][c].z;
+            o[c][3] = p.o[i][c].w;
+            m[c] = p.ml[i][c].x;
+            l[c] = p.ml[i][c].y;
+        }
+        attn_merge_step<4>(o, m, l, 0, nsplit, M, L, O);  // nsplit <= ATTN_MERGE_CHUNK (launch_qmv_attn)
+        const float nan = __builtin_nanf("");
+        out.v[i] = pos_ok ? make_float4(O[0] / L, O[1] / L, O[2] / L, O[3] / L) : make_float4(nan, nan, nan, nan);
+    }
+}
 
 // Sum over the workgroup of one float per wavefront (valid in lane 63 of each
 // wavefront), broadcast to every thread.
@@ -139,7 +199,7 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
     }
     float* yr = y + (size_t)m * ldy;
     uint16_t* yh = reinterpret_cast<uint16_t*>(y) + (size_t)m * ldy;  // QMV_HALF
-    const bool acc_out = MODE == QMV_FUSED && ix.accumulate;
+    const bool acc_out = (MODE == QMV_FUSED || MODE == QMV_ATTN) && ix.accumulate;
     auto store = [&](int r, float v) {
         if constexpr (MODE == QMV_HALF) yh[r] = f32_to_f16_rne(v);
         else yr[r] = v;
@@ -151,9 +211,14 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
     constexpr int CHUNKS = SPL * (64 / F::LPB) * F::ELEMS / QK_K;
     constexpr int MAXQ = (CHUNKS + NW - 1) / NW;
     ActRowPre<MAXQ> pre;
+    AttnRowPre<MODE == QMV_ATTN ? MAXQ : 1> apre;
+    int apos = 0;
     if constexpr (MODE == QMV_HALF)
         act_row_load_h<F::ACT, NW, MAXQ>(reinterpret_cast<const uint16_t*>(x) + (size_t)m * K, K, w, lane, pre);
-    else if (MODE != QMV_PLAIN && xr2)
+    else if constexpr (MODE == QMV_ATTN) {
+        apos = __float_as_int(attn_load_early(reinterpret_cast<const float*>(ix.attn_pos)));
+        attn_row_load<NW, MAXQ>(x, ix.attn_nsplit, K, w, lane, apre);
+    } else if (MODE != QMV_PLAIN && xr2)
         act_row_load_swiglu<F::ACT, NW, MAXQ>(xr, xr2, K, w, lane, pre);
     else
         act_row_load<F::ACT, NW, MAXQ>(xr, K, w, lane, pre);
@@ -166,6 +231,10 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
         const int r0 = row < N ? row : N - 1;
         if (acc_out) resa = yr[r0];
         qmv_load_row<F, SPL>(wrow(r0), gi, c, KB, ra);
+    }
+    if constexpr (MODE == QMV_ATTN) {
+        __builtin_amdgcn_sched_barrier(0);  // the merge's waits come after the first row's loads are out
+        attn_row_merge<NW, MAXQ>(apre, ix.attn_nsplit, apos >= 0 && apos < ix.attn_max_ctx, pre);
     }
     if (MODE == QMV_FUSED && ix.rms_gain) {
         // rms_norm_last_dim (sum of squares over the whole row, spread over the
@@ -419,6 +488,13 @@ hipError_t launch_block_isums(int dtype, const uint8_t* w, ActView act, int32_t*
 hipError_t launch_qmv_fused(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
                             const QmvOpts& o, hipStream_t s, int num_cus) {
     return launch_dtype<QMV_FUSED>(dtype, w, x, y, M, N, K, ldy, o, s, num_cus);
+}
+
+hipError_t launch_qmv_attn(int dtype, const uint8_t* w, const float* part, float* y, int N, int K, const QmvOpts& o,
+                           hipStream_t s, int num_cus) {
+    if (K % QK_K || K % ATTN_HEAD_DIM || o.attn_nsplit < 1 || o.attn_nsplit > ATTN_MERGE_CHUNK)
+        return hipErrorInvalidValue;
+    return launch_dtype<QMV_ATTN>(dtype, w, part, y, 1, N, K, N, o, s, num_cus);
 }
 
 }  // namespace frq

@@ -6,12 +6,14 @@ a KV cache, built from this library's C ABI:
     per layer:  [q|k] = QMatMul_Q4K(rms_norm(x) * attn_gain)        (one launch for both, Wq|Wk stacked)
                 v     = QMatMul_Q6K(rms_norm(x) * attn_gain)
                 a     = attention(rope(q), cache <- rope(k), v)      (RoPE + f16 cache append fused)
-                x    += QMatMul_Q4K(a)                               (residual fused)
+                x    += QMatMul_Q4K(a)                               (split merge + residual fused)
                 [g|u] = QMatMul_Q4K(rms_norm(x) * ffn_gain)         (Wg|Wu stacked)
                 x    += QMatMul_down(silu(g) * u)                    (SwiGLU + residual fused)
     logits = QMatMul_Q6K(rms_norm(x) * final_gain); next = argmax; x = embed[next]; pos += 1
 
-Six launches per layer (the attention is two), 194 per token.  The position lives in device memory,
+Five launches per layer (the attention's split kernel; its merge runs inside the
+o-projection mat-vec), 162 per token (fuse_oproj=False: the merge as its own
+kernel, six per layer, 194 per token; the same bits).  The position lives in device memory,
 so one captured HIP graph replays every step (prompt tokens are forced while
 they last).  Weights follow a Q4_K_M-style mix: Q4_K everywhere except attn_v,
 ffn_down of the even layers and the output matrix (Q6_K).  All weights are
@@ -106,10 +108,12 @@ GGUF_NAMES = {"wq": "attn_q", "wk": "attn_k", "wv": "attn_v", "wo": "attn_output
 
 
 class LlamaDecoder:
-    def __init__(self, dev: RocmDevice, cfg: LlamaConfig, seed: int = 1234, std: float = 0.02, _weights=None):
+    def __init__(self, dev: RocmDevice, cfg: LlamaConfig, seed: int = 1234, std: float = 0.02, _weights=None,
+                 fuse_oproj: bool = True):
         if cfg.head_dim != 128 or cfg.n_heads * cfg.head_dim != cfg.dim:
             raise ValueError("this decoder needs head_dim 128 and n_heads * head_dim == dim")
         self.dev, self.cfg, self.seed, self.std = dev, cfg, seed, std
+        self.fuse_oproj = fuse_oproj
         L = lib()
         self.L = L
         d, f, H, HD, Cx = cfg.dim, cfg.ffn, cfg.n_heads, cfg.head_dim, cfg.max_ctx
@@ -348,12 +352,19 @@ class LlamaDecoder:
                                           vp(self.qk.ptr), 2 * d))
                 check(L.frq_qmatmul_fused(h, lw["dt_v"], 1, d, d, vp(lw["wv"].ptr), x, d, None, ag, eps, 0,
                                           vp(self.v.ptr), d))
-            check(L.frq_attention_decode(h, cfg.n_heads, cfg.head_dim, cfg.max_ctx, vp(self.qk.ptr), vp(self.v.ptr),
-                                         vp(self.rcos.ptr), vp(self.rsin.ptr), vp(self.kc[li].ptr),
-                                         vp(self.vc[li].ptr), vp(self.pos.ptr), self.scale, vp(self.work.ptr),
-                                         self.work_bytes, vp(self.att.ptr)))
-            check(L.frq_qmatmul_fused(h, lw["dt_o"], 1, d, d, vp(lw["wo"].ptr), vp(self.att.ptr), d, None, None, 0.0,
-                                      1, x, d))
+            if self.fuse_oproj:
+                check(L.frq_attention_decode_oproj(h, cfg.n_heads, cfg.head_dim, cfg.max_ctx, vp(self.qk.ptr),
+                                                   vp(self.v.ptr), vp(self.rcos.ptr), vp(self.rsin.ptr),
+                                                   vp(self.kc[li].ptr), vp(self.vc[li].ptr), vp(self.pos.ptr),
+                                                   self.scale, vp(self.work.ptr), self.work_bytes, lw["dt_o"],
+                                                   vp(lw["wo"].ptr), d, x))
+            else:
+                check(L.frq_attention_decode(h, cfg.n_heads, cfg.head_dim, cfg.max_ctx, vp(self.qk.ptr),
+                                             vp(self.v.ptr), vp(self.rcos.ptr), vp(self.rsin.ptr),
+                                             vp(self.kc[li].ptr), vp(self.vc[li].ptr), vp(self.pos.ptr), self.scale,
+                                             vp(self.work.ptr), self.work_bytes, vp(self.att.ptr)))
+                check(L.frq_qmatmul_fused(h, lw["dt_o"], 1, d, d, vp(lw["wo"].ptr), vp(self.att.ptr), d, None, None,
+                                          0.0, 1, x, d))
             check(L.frq_qmatmul_fused(h, lw["dt_gu"], 1, 2 * f, d, vp(lw["wgu"].ptr), x, d, None, fg, eps, 0,
                                       vp(self.gu.ptr), 2 * f))
             check(L.frq_qmatmul_fused(h, lw["dt_down"], 1, d, f, vp(lw["wd"].ptr), vp(self.gu.ptr), f,
@@ -368,7 +379,8 @@ class LlamaDecoder:
         return lw["dt_qk"] in kq and lw["dt_v"] in kq and self.cfg.dim <= 16384
 
     def launches_per_step(self) -> int:
-        return sum(6 if self._pair(lw) else 7 for lw in self.layers) + 2
+        per_layer = 5 if self.fuse_oproj else 6
+        return sum(per_layer if self._pair(lw) else per_layer + 1 for lw in self.layers) + 2
 
     def tokens_host(self) -> np.ndarray:
         return self.tokens.numpy()

@@ -206,6 +206,25 @@ int frq_attention_decode(frq_device *dev, size_t n_heads, size_t head_dim, size_
                          const float *v_dev, const float *rope_cos_dev, const float *rope_sin_dev,
                          uint16_t *k_cache_dev, uint16_t *v_cache_dev, const int32_t *pos_dev, float scale,
                          void *work_dev, size_t work_bytes, float *out_dev);
+/* frq_attention_decode followed by the attention output projection with the
+ * residual add, y_dev[n_out] += W_o . attn (lazy.rs:7425-7440: o_proj then
+ * the residual).  When the context needs at most 8 splits (the split count
+ * is max(ceil(256 / n_heads), ceil(max_ctx / 128)): 32 heads up to
+ * max_ctx 1024) this is two launches instead of three: the per-split
+ * partials are merged inside the o-projection mat-vec (each workgroup merges
+ * its activation row while its first weight rows load) instead of by a
+ * separate kernel; otherwise the merge kernel writes into the workspace's
+ * tail first.  w_o_dev: [n_out, n_heads * head_dim] blocks of o_dtype (Q8_0, Q4_K,
+ * Q6_K); n_heads * head_dim must be a multiple of 256.  Same caches, appends
+ * and workspace as frq_attention_decode (work_dev 16-byte aligned here); the
+ * result is bit-identical to frq_attention_decode then frq_qmatmul_fused with
+ * accumulate = 1.  A pos outside [0, max_ctx) makes the attention NaN, as
+ * there. */
+int frq_attention_decode_oproj(frq_device *dev, size_t n_heads, size_t head_dim, size_t max_ctx,
+                               const float *qk_dev, const float *v_dev, const float *rope_cos_dev,
+                               const float *rope_sin_dev, uint16_t *k_cache_dev, uint16_t *v_cache_dev,
+                               const int32_t *pos_dev, float scale, void *work_dev, size_t work_bytes, int o_dtype,
+                               const void *w_o_dev, size_t n_out, float *y_dev);
 /* Greedy next token and its embedding: next = tokens[pos + 1] while
  * pos + 1 < prompt_len, else the first-index argmax of logits [vocab]
  * (argmax_dim_f32, byte_kernels.rs:8246-8261), stored at tokens[pos + 1]

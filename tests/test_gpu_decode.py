@@ -173,6 +173,71 @@ def test_attention_decode(dev, H, max_ctx, pos):
     np.testing.assert_array_equal(a.run(qk, v, pos), got)
 
 
+@pytest.mark.parametrize("H,max_ctx,pos,dt,n", [(32, 768, 700, O.Q4K, 4096), (32, 1024, 0, O.Q6K, 4096),
+                                                 (32, 768, 768, O.Q4K, 4096), (2, 64, 0, O.Q6K, 300),
+                                                 (2, 2048, 1500, O.Q8_0, 512), (4, 1024, 1023, O.Q4K, 1000),
+                                                 (2, 64, 64, O.Q4K, 256)])
+def test_attention_decode_oproj(dev, H, max_ctx, pos, dt, n):
+    """Attention + o-projection + residual equals frq_attention_decode then
+    the fused QMatMul with accumulate, bit for bit (same caches, appends and
+    outputs): 8 splits (32 heads: the merge inside the mat-vec, two
+    launches), 64 and 128 splits (the merge kernel into the workspace tail),
+    and an out-of-range pos (NaN attention, no append) on both paths."""
+    say("attention oproj", H, max_ctx, pos, dt, n)
+    k = H * 128
+    rng = np.random.default_rng(pos + H)
+    kc0 = rng.standard_normal((H, max_ctx, 128)).astype(np.float16)
+    vc0 = rng.standard_normal((H, max_ctx, 128)).astype(np.float16)
+    qk = O.normal((2 * k,), seed=pos, stream=1, std=2.0)
+    v = O.normal((k,), seed=pos, stream=2)
+    w = O.quantize(dt, O.normal((n, k), seed=n, stream=3, std=0.02))
+    y0 = O.normal((n,), seed=n, stream=4)
+    wd = dev.from_numpy(w.view(np.uint8))
+    scale = float(np.float32(1 / np.sqrt(128.0)))
+    outs = []
+    for fused_path in (False, True):
+        a = Attn(dev, H, max_ctx)
+        a.kc.copy_from(kc0.view(np.uint16))
+        a.vc.copy_from(vc0.view(np.uint16))
+        a.posd.copy_from(np.array([pos], np.int32))
+        qkd, vd, y = dev.from_numpy(qk), dev.from_numpy(v), dev.from_numpy(y0)
+        args = (dev.handle, H, 128, max_ctx, C.c_void_p(qkd.ptr), C.c_void_p(vd.ptr), C.c_void_p(a.cd.ptr),
+                C.c_void_p(a.sd.ptr), C.c_void_p(a.kc.ptr), C.c_void_p(a.vc.ptr), C.c_void_p(a.posd.ptr), scale,
+                C.c_void_p(a.work.ptr), a.wb)
+        if fused_path:
+            F._native.check(L().frq_attention_decode_oproj(*args, dt, C.c_void_p(wd.ptr), n, C.c_void_p(y.ptr)))
+        else:
+            F._native.check(L().frq_attention_decode(*args, C.c_void_p(a.out.ptr)))
+            fused(dev, dt, wd, a.out, n, k, acc=1, y=y)
+        outs.append((y.numpy(), a.kc.numpy(), a.vc.numpy()))
+    (y_ref, kc_ref, vc_ref), (y_got, kc_got, vc_got) = outs
+    np.testing.assert_array_equal(kc_got, kc_ref)
+    np.testing.assert_array_equal(vc_got, vc_ref)
+    np.testing.assert_array_equal(y_got, y_ref)  # (NaN == NaN here)
+    if pos < max_ctx:
+        assert np.isfinite(y_got).all()
+
+
+def test_attention_decode_oproj_errors(dev):
+    a = Attn(dev, 2, 64)
+    w = dev.alloc((256 * 144,), np.uint8)
+    y = dev.alloc((256,), np.float32)
+    base = (dev.handle, 2, 128, 64, C.c_void_p(y.ptr), C.c_void_p(y.ptr), C.c_void_p(a.cd.ptr), C.c_void_p(a.sd.ptr),
+            C.c_void_p(a.kc.ptr), C.c_void_p(a.vc.ptr), C.c_void_p(a.posd.ptr), 0.1)
+    with pytest.raises(F.FuelRocmError):  # workspace too small
+        F._native.check(L().frq_attention_decode_oproj(*base, C.c_void_p(a.work.ptr), a.wb - 4, O.Q4K,
+                                                       C.c_void_p(w.ptr), 256, C.c_void_p(y.ptr)))
+    with pytest.raises(F.FuelRocmError):  # workspace not 16-byte aligned
+        F._native.check(L().frq_attention_decode_oproj(*base, C.c_void_p(a.work.ptr + 4), a.wb, O.Q4K,
+                                                       C.c_void_p(w.ptr), 256, C.c_void_p(y.ptr)))
+    with pytest.raises(F.FuelRocmError):  # not a weight type
+        F._native.check(L().frq_attention_decode_oproj(*base, C.c_void_p(a.work.ptr), a.wb, 0,
+                                                       C.c_void_p(w.ptr), 256, C.c_void_p(y.ptr)))
+    with pytest.raises(F.FuelRocmError):  # n_heads * head_dim not a multiple of 256
+        F._native.check(L().frq_attention_decode_oproj(dev.handle, 1, 128, 64, *base[4:], C.c_void_p(a.work.ptr),
+                                                       a.wb, O.Q4K, C.c_void_p(w.ptr), 256, C.c_void_p(y.ptr)))
+
+
 def test_attention_decode_pos_out_of_range(dev):
     a = Attn(dev, 2, 16)
     a.kc.copy_from(np.zeros((2, 16, 128), np.uint16))
@@ -294,6 +359,25 @@ def test_decoder_greedy_graph_replay(dev, small_decoder):
             assert gap <= DEC_TOL, (p, chosen, best, gap)
             exact += chosen == best
     assert exact >= (n_steps - len(prompt) + 1) // 2
+
+
+def test_decoder_fused_oproj_matches_unfused(dev, small_decoder):
+    """The decoder's attention-merging o-projection (five launches per layer)
+    gives the same logits and tokens, bit for bit, as the separate merge
+    kernel (six)."""
+    say("decoder fused oproj")
+    dec = small_decoder
+    assert dec.fuse_oproj
+    ref = LlamaDecoder(dev, LlamaConfig(**SMALL), seed=99, std=0.05, fuse_oproj=False)
+    assert ref.launches_per_step() == dec.launches_per_step() + SMALL["n_layers"]
+    prompt = [3, 1, 4, 1, 5, 9, 2, 6]
+    dec.start(prompt)
+    ref.start(prompt)
+    for _ in range(16):
+        dec.enqueue_step()
+        ref.enqueue_step()
+        np.testing.assert_array_equal(dec.logits.numpy(), ref.logits.numpy())
+    np.testing.assert_array_equal(dec.tokens_host()[:17], ref.tokens_host()[:17])
 
 
 # ---- the decoder from a GGUF file ----
