@@ -73,6 +73,7 @@ SIGNATURES = {
     "frq_qmatmul_fused": (_i32, [_vp, _i32, _sz, _sz, _sz, _vp, _vp, _sz, _vp, _vp, C.c_float, _i32, _vp, _sz]),
     "frq_qmatmul_fused_pair": (_i32, [_vp, _sz, _sz, _vp, _sz, _vp, C.c_float, _i32, _sz, _vp, _vp, _i32, _sz, _vp,
                                       _vp]),
+    "frq_qmatmul_fused_glu": (_i32, [_vp, _i32, _sz, _sz, _sz, _vp, _vp, _vp, _sz, _vp, C.c_float, _vp, _sz]),
     "frq_attention_decode_workspace": (_sz, [_sz, _sz]),
     "frq_attention_decode": (_i32, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _sz,
                                     _vp]),

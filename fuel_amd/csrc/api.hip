@@ -854,6 +854,33 @@ int frq_attention_decode(frq_device* dev, size_t n_heads, size_t head_dim, size_
     return FRQ_OK;
 }
 
+int frq_qmatmul_fused_glu(frq_device* dev, int dt, size_t m, size_t n, size_t k, const void* w_gate, const void* w_up,
+                          const float* x, size_t ldx, const float* gain, float eps, float* y, size_t ldy) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (!is_weight_type(dt)) return fail(FRQ_UNSUPPORTED, "qmatmul_fused_glu: dtype %d", dt);
+    if (k == 0 || k % block_elems(dt))
+        return fail(FRQ_INVALID, "qmatmul_fused_glu: k=%zu must be a positive multiple of %zu", k, block_elems(dt));
+    if (k > qmv_kmax(dt)) return fail(FRQ_UNSUPPORTED, "qmatmul_fused_glu: k=%zu exceeds %zu", k, qmv_kmax(dt));
+    if (m > 65535 || n > (size_t)0x7fffffff) return fail(FRQ_UNSUPPORTED, "qmatmul_fused_glu: m=%zu n=%zu", m, n);
+    if (m == 0 || n == 0) return FRQ_OK;
+    if (!w_gate || !w_up || !x || !y) return fail(FRQ_INVALID, "qmatmul_fused_glu: null buffer");
+    if (m > 1 && (ldx < k || ldy < n))
+        return fail(FRQ_INVALID, "qmatmul_fused_glu: ldx=%zu < k or ldy=%zu < n", ldx, ldy);
+    if (ldx > (size_t)0x7fffffff || ldy > (size_t)0x7fffffff) return fail(FRQ_UNSUPPORTED, "qmatmul_fused_glu: strides");
+    if (!aligned16(x) || (gain && !aligned16(gain)) || ldx % 4)
+        return fail(FRQ_MISALIGNED, "qmatmul_fused_glu: x and gain must be 16-byte aligned and ldx %% 4 == 0");
+    if (!aligned4(y) || !aligned4(w_gate) || !aligned4(w_up))
+        return fail(FRQ_MISALIGNED, "qmatmul_fused_glu: weights / y not 4-byte aligned");
+    QmvOpts o{};
+    o.ldx = (int)ldx;
+    o.rms_gain = gain;
+    o.rms_eps = eps;
+    HIP_TRY(launch_qmv_glu(dt, static_cast<const uint8_t*>(w_gate), static_cast<const uint8_t*>(w_up), x, y, (int)m,
+                           (int)n, (int)k, (int)ldy, o, dev->stream, dev->num_cus));
+    return FRQ_OK;
+}
+
 int frq_attention_decode_oproj(frq_device* dev, size_t n_heads, size_t head_dim, size_t max_ctx, const float* qk,
                                const float* v, const float* rcos, const float* rsin, uint16_t* kc, uint16_t* vc,
                                const int32_t* pos, float scale, void* work, size_t work_bytes, int o_dtype,

@@ -60,6 +60,10 @@ hipError_t launch_qmv_indexed(int dtype, const uint8_t* w, const float* x, float
                               const QmvOpts& ix, hipStream_t s, int num_cus);
 hipError_t launch_qmv_fused(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
                             const QmvOpts& o, hipStream_t s, int num_cus);
+// y [M, N] = silu(Wg a(x)) * (Wu a(x)), a(x) as launch_qmv_fused (RMS norm
+// from o; no x2, no accumulate).
+hipError_t launch_qmv_glu(int dtype, const uint8_t* w_gate, const uint8_t* w_up, const float* x, float* y, int M, int N,
+                          int K, int ldy, const QmvOpts& o, hipStream_t s, int num_cus);
 // y [N] (+)= W a where a [K = heads * ATTN_HEAD_DIM] is the merge of the
 // decode-attention partials in `part` (attn_decode_work layout, o.attn_*
 // set): the merge runs in each workgroup's activation stage.

@@ -84,7 +84,9 @@ __device__ __forceinline__ float qmv_row(const typename F::Raw (&r)[SPL], const 
 // halves, f16::from_f32 = round to nearest even of the f32 row sum).
 // QMV_ATTN: x holds decode-attention split partials; the activation row is
 // their merge (attn_merge_step), residual add as QMV_FUSED.
-enum QmvMode { QMV_PLAIN = 0, QMV_INDEXED = 1, QMV_FUSED = 2, QMV_HALF = 3, QMV_ATTN = 4 };
+// QMV_GLU: activation as QMV_FUSED (RMS norm optional); output r is
+// silu(gate_r . a) * (up_r . a) with gate rows in W and up rows in ix.w2.
+enum QmvMode { QMV_PLAIN = 0, QMV_INDEXED = 1, QMV_FUSED = 2, QMV_HALF = 3, QMV_ATTN = 4, QMV_GLU = 5 };
 
 // Activation stage of QMV_ATTN: lane `lane`'s four elements of chunk
 // w + NW*i are elements d..d+3 of head hd (HD = ATTN_HEAD_DIM per head).  The
@@ -192,11 +194,12 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
             n_split = ix.n_split;
         }
     }
-    if constexpr (MODE == QMV_FUSED) {
+    if constexpr (MODE == QMV_FUSED || MODE == QMV_GLU) {
         const size_t xo = (size_t)m * ix.ldx;
         xr = x + xo;
         if (ix.x2) xr2 = ix.x2 + xo;
     }
+    if constexpr (MODE == QMV_GLU) W2 = ix.w2;  // (n_split stays N: wrow() reads gate rows)
     float* yr = y + (size_t)m * ldy;
     uint16_t* yh = reinterpret_cast<uint16_t*>(y) + (size_t)m * ldy;  // QMV_HALF
     const bool acc_out = (MODE == QMV_FUSED || MODE == QMV_ATTN) && ix.accumulate;
@@ -236,7 +239,7 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
         __builtin_amdgcn_sched_barrier(0);  // the merge's waits come after the first row's loads are out
         attn_row_merge<NW, MAXQ>(apre, ix.attn_nsplit, apos >= 0 && apos < ix.attn_max_ctx, pre);
     }
-    if (MODE == QMV_FUSED && ix.rms_gain) {
+    if ((MODE == QMV_FUSED || MODE == QMV_GLU) && ix.rms_gain) {
         // rms_norm_last_dim (sum of squares over the whole row, spread over the
         // wavefronts) and the affine gain, before quantization
         act_row_rms_norm<F::ACT, NW, MAXQ>(pre, ix.rms_gain, ix.rms_eps, K, w, lane,
@@ -245,6 +248,22 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
     act_row_quantize<F::ACT, NW, MAXQ>(pre, K, s_qs, lay.qstride, s_d, s_bs, w, lane);
     __syncthreads();
 
+    if constexpr (MODE == QMV_GLU) {
+        // The ring alternates gate row r (ra) and up row r (rb): the up row's
+        // loads are in flight while the gate row is reduced, the next gate
+        // row's while the up row is.
+        while (row < N) {
+            qmv_load_row<F, SPL>(W2 + (size_t)row * row_bytes, gi, c, KB, rb);
+            const float tg = qmv_row<F, SPL>(ra, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
+            const int nrow = row + nw;
+            const int lrow = nrow < N ? nrow : row;
+            qmv_load_row<F, SPL>(W + (size_t)lrow * row_bytes, gi, c, KB, ra);
+            const float tu = qmv_row<F, SPL>(rb, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
+            if (lane == 63) store(row, silu_mul(tg, tu));
+            row = nrow;
+        }
+        return;
+    }
     // Two-row ring: the next row's loads are in flight while a row is reduced.
     // Past the last row a wave re-issues its current row (cache-resident)
     // rather than branching around the loads.
@@ -488,6 +507,14 @@ hipError_t launch_block_isums(int dtype, const uint8_t* w, ActView act, int32_t*
 hipError_t launch_qmv_fused(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
                             const QmvOpts& o, hipStream_t s, int num_cus) {
     return launch_dtype<QMV_FUSED>(dtype, w, x, y, M, N, K, ldy, o, s, num_cus);
+}
+
+hipError_t launch_qmv_glu(int dtype, const uint8_t* w_gate, const uint8_t* w_up, const float* x, float* y, int M, int N,
+                          int K, int ldy, const QmvOpts& o, hipStream_t s, int num_cus) {
+    QmvOpts g = o;
+    g.w2 = w_up;
+    g.accumulate = 0;
+    return launch_dtype<QMV_GLU>(dtype, w_gate, x, y, M, N, K, ldy, g, s, num_cus);
 }
 
 hipError_t launch_qmv_attn(int dtype, const uint8_t* w, const float* part, float* y, int N, int K, const QmvOpts& o,

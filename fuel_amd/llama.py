@@ -7,13 +7,16 @@ a KV cache, built from this library's C ABI:
                 v     = QMatMul_Q6K(rms_norm(x) * attn_gain)
                 a     = attention(rope(q), cache <- rope(k), v)      (RoPE + f16 cache append fused)
                 x    += QMatMul_Q4K(a)                               (split merge + residual fused)
-                [g|u] = QMatMul_Q4K(rms_norm(x) * ffn_gain)         (Wg|Wu stacked)
-                x    += QMatMul_down(silu(g) * u)                    (SwiGLU + residual fused)
+                h     = silu(QMatMul_Q4K(a)) * QMatMul_Q4K(a),  a = rms_norm(x) * ffn_gain
+                                                                     (Wg|Wu stacked; one launch, h written)
+                x    += QMatMul_down(h)                              (residual fused)
     logits = QMatMul_Q6K(rms_norm(x) * final_gain); next = argmax; x = embed[next]; pos += 1
 
 Five launches per layer (the attention's split kernel; its merge runs inside the
 o-projection mat-vec), 162 per token (fuse_oproj=False: the merge as its own
-kernel, six per layer, 194 per token; the same bits).  The position lives in device memory,
+kernel, six per layer, 194 per token; fuse_glu=False: gate|up written and the
+SwiGLU product formed in the down projection's activation stage; the same
+bits either way).  The position lives in device memory,
 so one captured HIP graph replays every step (prompt tokens are forced while
 they last).  Weights follow a Q4_K_M-style mix: Q4_K everywhere except attn_v,
 ffn_down of the even layers and the output matrix (Q6_K).  All weights are
@@ -109,11 +112,11 @@ GGUF_NAMES = {"wq": "attn_q", "wk": "attn_k", "wv": "attn_v", "wo": "attn_output
 
 class LlamaDecoder:
     def __init__(self, dev: RocmDevice, cfg: LlamaConfig, seed: int = 1234, std: float = 0.02, _weights=None,
-                 fuse_oproj: bool = True):
+                 fuse_oproj: bool = True, fuse_glu: bool = True):
         if cfg.head_dim != 128 or cfg.n_heads * cfg.head_dim != cfg.dim:
             raise ValueError("this decoder needs head_dim 128 and n_heads * head_dim == dim")
         self.dev, self.cfg, self.seed, self.std = dev, cfg, seed, std
-        self.fuse_oproj = fuse_oproj
+        self.fuse_oproj, self.fuse_glu = fuse_oproj, fuse_glu
         L = lib()
         self.L = L
         d, f, H, HD, Cx = cfg.dim, cfg.ffn, cfg.n_heads, cfg.head_dim, cfg.max_ctx
@@ -365,10 +368,17 @@ class LlamaDecoder:
                                              vp(self.work.ptr), self.work_bytes, vp(self.att.ptr)))
                 check(L.frq_qmatmul_fused(h, lw["dt_o"], 1, d, d, vp(lw["wo"].ptr), vp(self.att.ptr), d, None, None,
                                           0.0, 1, x, d))
-            check(L.frq_qmatmul_fused(h, lw["dt_gu"], 1, 2 * f, d, vp(lw["wgu"].ptr), x, d, None, fg, eps, 0,
-                                      vp(self.gu.ptr), 2 * f))
-            check(L.frq_qmatmul_fused(h, lw["dt_down"], 1, d, f, vp(lw["wd"].ptr), vp(self.gu.ptr), f,
-                                      vp(self.gu.ptr + 4 * f), None, 0.0, 1, x, d))
+            if self.fuse_glu:
+                up = lw["wgu"].ptr + f * (d // (32 if lw["dt_gu"] == N.Q8_0 else 256)) * N_TYPE_SIZE[lw["dt_gu"]]
+                check(L.frq_qmatmul_fused_glu(h, lw["dt_gu"], 1, f, d, vp(lw["wgu"].ptr), vp(up), x, d, fg, eps,
+                                              vp(self.gu.ptr), f))
+                check(L.frq_qmatmul_fused(h, lw["dt_down"], 1, d, f, vp(lw["wd"].ptr), vp(self.gu.ptr), f, None,
+                                          None, 0.0, 1, x, d))
+            else:
+                check(L.frq_qmatmul_fused(h, lw["dt_gu"], 1, 2 * f, d, vp(lw["wgu"].ptr), x, d, None, fg, eps, 0,
+                                          vp(self.gu.ptr), 2 * f))
+                check(L.frq_qmatmul_fused(h, lw["dt_down"], 1, d, f, vp(lw["wd"].ptr), vp(self.gu.ptr), f,
+                                          vp(self.gu.ptr + 4 * f), None, 0.0, 1, x, d))
         check(L.frq_qmatmul_fused(h, self.dt_out, 1, cfg.vocab, d, vp(self.wout.ptr), x, d, None,
                                   vp(self.final_gain.ptr), eps, 0, vp(self.logits.ptr), cfg.vocab))
         check(L.frq_argmax_embed(h, vp(self.logits.ptr), cfg.vocab, vp(self.embed.ptr), d, vp(self.tokens.ptr),

@@ -189,6 +189,19 @@ int frq_qmatmul_fused(frq_device *dev, int ggml_dtype, size_t m, size_t n, size_
 int frq_qmatmul_fused_pair(frq_device *dev, size_t m, size_t k, const float *x_dev, size_t ldx,
                            const float *rms_gain_dev, float rms_eps, int dtype1, size_t n1, const void *w1_dev,
                            float *y1_dev, int dtype2, size_t n2, const void *w2_dev, float *y2_dev);
+/* The gated FFN input of LlamaModel::apply_layer (lazy.rs:7436-7442:
+ * gate = a.qmatmul(W_gate), up = a.qmatmul(W_up), silu(gate) * up with
+ * silu(g) = g / (1 + exp(-g)), byte_kernels.rs silu):
+ * y[m][n] = silu(W_gate . a_m) * (W_up . a_m), a_m = rms_norm(x_m) * rms_gain
+ * (or x_m when rms_gain_dev is NULL), both matrices [n, k] blocks of dtype.
+ * One launch; each output's gate and up rows are reduced by the same
+ * wavefront, so the product is formed where both sums are and only n
+ * values are written.  Bit-identical to the two outputs of
+ * frq_qmatmul_fused (or the pair form) followed by the SwiGLU input stage
+ * of frq_qmatmul_fused (x2). */
+int frq_qmatmul_fused_glu(frq_device *dev, int dtype, size_t m, size_t n, size_t k, const void *w_gate_dev,
+                          const void *w_up_dev, const float *x_dev, size_t ldx, const float *rms_gain_dev,
+                          float rms_eps, float *y_dev, size_t ldy);
 /* Decode attention of one token (lazy.rs:7391-7423 at seq = 1 with a KV
  * cache): q and k of qk_dev = [q | k] (n_heads * head_dim each) are rotated
  * (rope_f32 rotate-half, byte_kernels.rs:1885-1964, with the rows `pos` of
@@ -207,7 +220,7 @@ int frq_attention_decode(frq_device *dev, size_t n_heads, size_t head_dim, size_
                          uint16_t *k_cache_dev, uint16_t *v_cache_dev, const int32_t *pos_dev, float scale,
                          void *work_dev, size_t work_bytes, float *out_dev);
 /* frq_attention_decode followed by the attention output projection with the
- * residual add, y_dev[n_out] += W_o . attn (lazy.rs:7425-7440: o_proj then
+ * residual add, y_dev[n_out] += W_o . attn (lazy.rs:7427-7434: o_proj then
  * the residual).  When the context needs at most 8 splits (the split count
  * is max(ceil(256 / n_heads), ceil(max_ctx / 128)): 32 heads up to
  * max_ctx 1024) this is two launches instead of three: the per-split

@@ -75,6 +75,34 @@ def test_qmatmul_fused_swiglu_residual(dev, dt, n, ffn):
     assert rel_err(y.numpy(), want) < TOL
 
 
+@pytest.mark.parametrize("dt,n,k,m,rms", [(O.Q4K, 11008, 4096, 1, True), (O.Q6K, 1000, 2048, 2, True),
+                                          (O.Q8_0, 300, 1024, 3, False), (O.Q4K, 513, 4096, 1, False)])
+def test_qmatmul_fused_glu(dev, dt, n, k, m, rms):
+    """silu(gate . a) * (up . a) in one launch: the gate and up sums are the
+    fused mat-vec's own (bit-identical), the product is silu_mul's; and the
+    CPU path (QMatMul gate and up, SiLU·mul) within 1e-3 of its norm."""
+    say("fused glu", dt, n, k, m, rms)
+    wg = O.quantize(dt, O.normal((n, k), seed=n + k, stream=1, std=0.02))
+    wu = O.quantize(dt, O.normal((n, k), seed=n + k, stream=2, std=0.02))
+    x = O.normal((m, k), seed=n + k, stream=3, std=2.0)
+    g = 1 + O.normal((k,), seed=n + k, stream=4, std=0.2)
+    wgd, wud, xd, gd = (dev.from_numpy(a) for a in (wg.view(np.uint8), wu.view(np.uint8), x, g))
+    y = dev.alloc((m, n), np.float32)
+    F._native.check(L().frq_qmatmul_fused_glu(dev.handle, dt, m, n, k, C.c_void_p(wgd.ptr), C.c_void_p(wud.ptr),
+                                              C.c_void_p(xd.ptr), k, C.c_void_p(gd.ptr) if rms else None, 1e-5,
+                                              C.c_void_p(y.ptr), n))
+    got = y.numpy()
+    sg = fused(dev, dt, wgd, xd, n, k, m=m, gain=gd if rms else None).numpy()
+    su = fused(dev, dt, wud, xd, n, k, m=m, gain=gd if rms else None).numpy()
+    host = (sg / (np.float32(1) + np.exp(-sg)) * su).astype(np.float32)
+    np.testing.assert_allclose(got, host, rtol=2e-6, atol=0)  # (device expf vs numpy exp: an ulp or two)
+    xn = O.rms_norm(x, g, 1e-5) if rms else x
+    gw, uw = O.matmul(dt, xn, wg), O.matmul(dt, xn, wu)
+    want = (gw / (np.float32(1) + np.exp(-gw)) * uw).astype(np.float32)
+    for r in range(m):
+        assert rel_err(got[r], want[r]) < TOL, r
+
+
 @pytest.mark.parametrize("dt1,n1,dt2,n2,k,m", [(O.Q4K, 8192, O.Q6K, 4096, 4096, 1), (O.Q6K, 300, O.Q4K, 1000, 2048, 2),
                                                (O.Q4K, 512, O.Q4K, 768, 11008, 1)])
 def test_qmatmul_fused_pair(dev, dt1, n1, dt2, n2, k, m):
@@ -363,12 +391,13 @@ def test_decoder_greedy_graph_replay(dev, small_decoder):
 
 def test_decoder_fused_oproj_matches_unfused(dev, small_decoder):
     """The decoder's attention-merging o-projection (five launches per layer)
-    gives the same logits and tokens, bit for bit, as the separate merge
-    kernel (six)."""
-    say("decoder fused oproj")
+    and its one-launch SwiGLU product give the same logits and tokens, bit for
+    bit, as the separate merge kernel (six) and the SwiGLU product formed in
+    the down projection's activation stage."""
+    say("decoder fused oproj / glu")
     dec = small_decoder
-    assert dec.fuse_oproj
-    ref = LlamaDecoder(dev, LlamaConfig(**SMALL), seed=99, std=0.05, fuse_oproj=False)
+    assert dec.fuse_oproj and dec.fuse_glu
+    ref = LlamaDecoder(dev, LlamaConfig(**SMALL), seed=99, std=0.05, fuse_oproj=False, fuse_glu=False)
     assert ref.launches_per_step() == dec.launches_per_step() + SMALL["n_layers"]
     prompt = [3, 1, 4, 1, 5, 9, 2, 6]
     dec.start(prompt)
