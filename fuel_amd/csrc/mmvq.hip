@@ -86,7 +86,19 @@ __device__ __forceinline__ float qmv_row(const typename F::Raw (&r)[SPL], const 
 // their merge (attn_merge_step), residual add as QMV_FUSED.
 // QMV_GLU: activation as QMV_FUSED (RMS norm optional); output r is
 // silu(gate_r . a) * (up_r . a) with gate rows in W and up rows in ix.w2.
-enum QmvMode { QMV_PLAIN = 0, QMV_INDEXED = 1, QMV_FUSED = 2, QMV_HALF = 3, QMV_ATTN = 4, QMV_GLU = 5 };
+// QMV_FUSED_NOX: QMV_FUSED without x2 and RMS norm (its own instantiation:
+// with the run-time choice of activation loader compiled out, nothing merges
+// registers at a join, so the first weight rows are requested before the
+// activation row has arrived).
+enum QmvMode {
+    QMV_PLAIN = 0,
+    QMV_INDEXED = 1,
+    QMV_FUSED = 2,
+    QMV_HALF = 3,
+    QMV_ATTN = 4,
+    QMV_GLU = 5,
+    QMV_FUSED_NOX = 6
+};
 
 // Activation stage of QMV_ATTN: lane `lane`'s four elements of chunk
 // w + NW*i are elements d..d+3 of head hd (HD = ATTN_HEAD_DIM per head).  The
@@ -194,7 +206,7 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
             n_split = ix.n_split;
         }
     }
-    if constexpr (MODE == QMV_FUSED || MODE == QMV_GLU) {
+    if constexpr (MODE == QMV_FUSED || MODE == QMV_GLU || MODE == QMV_FUSED_NOX) {
         const size_t xo = (size_t)m * ix.ldx;
         xr = x + xo;
         if (ix.x2) xr2 = ix.x2 + xo;
@@ -202,7 +214,7 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
     if constexpr (MODE == QMV_GLU) W2 = ix.w2;  // (n_split stays N: wrow() reads gate rows)
     float* yr = y + (size_t)m * ldy;
     uint16_t* yh = reinterpret_cast<uint16_t*>(y) + (size_t)m * ldy;  // QMV_HALF
-    const bool acc_out = (MODE == QMV_FUSED || MODE == QMV_ATTN) && ix.accumulate;
+    const bool acc_out = (MODE == QMV_FUSED || MODE == QMV_ATTN || MODE == QMV_FUSED_NOX) && ix.accumulate;
     auto store = [&](int r, float v) {
         if constexpr (MODE == QMV_HALF) yh[r] = f32_to_f16_rne(v);
         else yr[r] = v;
@@ -221,7 +233,7 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
     else if constexpr (MODE == QMV_ATTN) {
         apos = __float_as_int(attn_load_early(reinterpret_cast<const float*>(ix.attn_pos)));
         attn_row_load<NW, MAXQ>(x, ix.attn_nsplit, K, w, lane, apre);
-    } else if (MODE != QMV_PLAIN && xr2)
+    } else if (MODE != QMV_PLAIN && MODE != QMV_FUSED_NOX && xr2)
         act_row_load_swiglu<F::ACT, NW, MAXQ>(xr, xr2, K, w, lane, pre);
     else
         act_row_load<F::ACT, NW, MAXQ>(xr, K, w, lane, pre);
@@ -506,6 +518,7 @@ hipError_t launch_block_isums(int dtype, const uint8_t* w, ActView act, int32_t*
 
 hipError_t launch_qmv_fused(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
                             const QmvOpts& o, hipStream_t s, int num_cus) {
+    if (!o.x2 && !o.rms_gain) return launch_dtype<QMV_FUSED_NOX>(dtype, w, x, y, M, N, K, ldy, o, s, num_cus);
     return launch_dtype<QMV_FUSED>(dtype, w, x, y, M, N, K, ldy, o, s, num_cus);
 }
 
