@@ -322,9 +322,11 @@ DECODE_NEW = 256
 def decode_leg(new_tokens: int = DECODE_NEW, prompt_len: int = DECODE_PROMPT):
     """random-init LLaMA-2-7B-shaped decoder (Q4_K_M-style
     mix), a 512-token uniform random prompt, greedy decode of `new_tokens`.
-    Every step is one replay of a captured HIP graph (194 launches); the
+    Every step is one replay of a captured HIP graph (162 launches); the
     prompt is run through the same step with its tokens forced.  Timed: the
-    `new_tokens` steps that each emit a generated token."""
+    `new_tokens` steps that each emit a generated token.  Also timed: the
+    prompt as one batch (`LlamaDecoder.prefill`, int8-MFMA projections), with
+    its last-position logits against the forced steps'."""
     import fuel_amd as F
     from fuel_amd.hiprt import HipRuntime
     from fuel_amd.llama import LlamaConfig, LlamaDecoder
@@ -339,10 +341,20 @@ def decode_leg(new_tokens: int = DECODE_NEW, prompt_len: int = DECODE_PROMPT):
     t_build = time.time() - t0
     bits = F.fill_random_bits(dev, prompt_len, 0, SEED, 0, 77).numpy()
     prompt = (bits % cfg.vocab).astype(np.int32)   # uniform ids in [0, vocab)
+    # the prompt as one batch (int8-MFMA projections), timed; the forced
+    # steps below then rebuild the caches and the decode runs from there
+    e0, e1 = hip.event_create(), hip.event_create()
+    dec.prefill(prompt)                            # (first call sizes the batch buffers and workspace)
+    hip.stream_sync(stream)
+    hip.event_record(e0, stream)
+    dec.prefill(prompt)
+    hip.event_record(e1, stream)
+    hip.event_sync(e1)
+    prefill_batched_ms = hip.elapsed_ms(e0, e1)
+    logits_prefill = dec.logits.numpy()
     dec.start(prompt)
     hip.stream_sync(stream)
     g = hip.capture(stream, dec.enqueue_step)
-    e0, e1 = hip.event_create(), hip.event_create()
     dec.start(prompt)
     hip.event_record(e0, stream)
     for _ in range(prompt_len - 1):              # forced steps: cache rows 0 .. prompt_len-2
@@ -375,6 +387,10 @@ def decode_leg(new_tokens: int = DECODE_NEW, prompt_len: int = DECODE_PROMPT):
         "tokens_per_s": round(new_tokens / (decode_ms * 1e-3), 1),
         "ms_per_token": round(ms_tok, 4),
         "prefill_ms_by_decode_steps": round(prefill_ms, 2),
+        "prefill_ms_batched": round(prefill_batched_ms, 2),
+        "prefill_tokens_per_s_batched": round(prompt_len / (prefill_batched_ms * 1e-3), 1),
+        # logits of the last prompt position, batched prefill vs the forced steps (max |d| / norm)
+        "prefill_logits_rel_err_vs_steps": float(np.abs(logits_prefill - logits0).max() / np.linalg.norm(logits0)),
         "weight_bytes_per_token": wbytes,
         "kv_bytes_per_token_mean": int(kv_bytes),
         "hbm_GB_s": round((wbytes + kv_bytes) / (ms_tok * 1e-3) / 1e9, 1),

@@ -80,6 +80,12 @@ SIGNATURES = {
     "frq_attention_decode_oproj": (_i32, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_float, _vp,
                                           _sz, _i32, _vp, _sz, _vp]),
     "frq_argmax_embed": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _vp, _vp]),
+    "frq_rms_norm_rows": (_i32, [_vp, _sz, _sz, _vp, _sz, _vp, C.c_float, _vp, _sz]),
+    "frq_rope_append_rows": (_i32, [_vp, _sz, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _vp, _sz, _vp, _vp]),
+    "frq_attention_prefill": (_i32, [_vp, _sz, _sz, _sz, _sz, _vp, _sz, _vp, _vp, _sz, C.c_float, _vp, _sz]),
+    "frq_swiglu_rows": (_i32, [_vp, _sz, _sz, _vp, _sz, _vp, _sz]),
+    "frq_add": (_i32, [_vp, _sz, _vp, _vp]),
+    "frq_gather_rows": (_i32, [_vp, _vp, _sz, _sz, _vp, _sz, _vp]),
     "frq_block_isums": (_i32, [_vp, _i32, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
     "frq_fill_random_bits": (_i32, [_vp, _vp, _sz, C.c_uint64, C.c_uint64, C.c_uint32, C.c_uint32]),
     "frq_fill_normal": (_i32, [_vp, _vp, _sz, C.c_uint64, C.c_uint32, C.c_float, C.c_float]),

@@ -927,6 +927,95 @@ int frq_attention_decode_oproj(frq_device* dev, size_t n_heads, size_t head_dim,
     return FRQ_OK;
 }
 
+// ---- prefill row kernels ----
+
+int frq_rms_norm_rows(frq_device* dev, size_t m, size_t k, const float* x, size_t ldx, const float* gain, float eps,
+                      float* y, size_t ldy) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (m > 0x7fffffff || k == 0 || k > 0x7fffffff || ldx < k || ldy < k || ldx > 0x7fffffff || ldy > 0x7fffffff)
+        return fail(FRQ_INVALID, "rms_norm_rows: m=%zu k=%zu ldx=%zu ldy=%zu", m, k, ldx, ldy);
+    if (m == 0) return FRQ_OK;
+    if (!x || !gain || !y) return fail(FRQ_INVALID, "rms_norm_rows: null buffer");
+    HIP_TRY(launch_rms_norm_rows(x, (int)ldx, gain, eps, (int)m, (int)k, y, (int)ldy, dev->stream));
+    return FRQ_OK;
+}
+
+int frq_rope_append_rows(frq_device* dev, size_t m, size_t n_heads, size_t head_dim, size_t max_ctx, float* qk,
+                         size_t ldqk, const float* v, size_t ldv, const float* rcos, const float* rsin, size_t pos0,
+                         uint16_t* kc, uint16_t* vc) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (head_dim != (size_t)ATTN_HEAD_DIM)
+        return fail(FRQ_UNSUPPORTED, "rope_append_rows: head_dim=%zu (supported: %d)", head_dim, ATTN_HEAD_DIM);
+    if (n_heads == 0 || n_heads > 65535 || max_ctx == 0 || max_ctx > (size_t)0x7fffffff / (n_heads * head_dim) ||
+        pos0 > max_ctx || m > max_ctx - pos0)
+        return fail(FRQ_INVALID, "rope_append_rows: m=%zu pos0=%zu n_heads=%zu max_ctx=%zu", m, pos0, n_heads,
+                    max_ctx);
+    if (ldqk < 2 * n_heads * head_dim || ldv < n_heads * head_dim || ldqk > 0x7fffffff || ldv > 0x7fffffff)
+        return fail(FRQ_INVALID, "rope_append_rows: ldqk=%zu ldv=%zu", ldqk, ldv);
+    if (m == 0) return FRQ_OK;
+    if (m > 65535) return fail(FRQ_UNSUPPORTED, "rope_append_rows: m=%zu > 65535", m);
+    if (!qk || !v || !rcos || !rsin || !kc || !vc) return fail(FRQ_INVALID, "rope_append_rows: null buffer");
+    HIP_TRY(launch_rope_append_rows(qk, (int)ldqk, v, (int)ldv, rcos, rsin, (int)m, (int)n_heads, (int)pos0,
+                                    (int)max_ctx, kc, vc, dev->stream));
+    return FRQ_OK;
+}
+
+int frq_attention_prefill(frq_device* dev, size_t m, size_t n_heads, size_t head_dim, size_t max_ctx, const float* q,
+                          size_t ldq, const uint16_t* kc, const uint16_t* vc, size_t pos0, float scale, float* out,
+                          size_t ldo) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (head_dim != (size_t)ATTN_HEAD_DIM)
+        return fail(FRQ_UNSUPPORTED, "attention_prefill: head_dim=%zu (supported: %d)", head_dim, ATTN_HEAD_DIM);
+    if (n_heads == 0 || n_heads > 65535 || max_ctx == 0 || max_ctx > (size_t)0x7fffffff / (n_heads * head_dim) ||
+        pos0 > max_ctx || m > max_ctx - pos0)
+        return fail(FRQ_INVALID, "attention_prefill: m=%zu pos0=%zu n_heads=%zu max_ctx=%zu", m, pos0, n_heads,
+                    max_ctx);
+    if (ldq < n_heads * head_dim || ldo < n_heads * head_dim || ldq > 0x7fffffff || ldo > 0x7fffffff)
+        return fail(FRQ_INVALID, "attention_prefill: ldq=%zu ldo=%zu", ldq, ldo);
+    if (m == 0) return FRQ_OK;
+    if (!q || !kc || !vc || !out) return fail(FRQ_INVALID, "attention_prefill: null buffer");
+    if (!aligned16(kc) || !aligned16(vc)) return fail(FRQ_MISALIGNED, "attention_prefill: caches not 16-byte aligned");
+    HIP_TRY(launch_attention_prefill(q, (int)ldq, kc, vc, (int)pos0, (int)m, (int)n_heads, (int)max_ctx, scale, out,
+                                     (int)ldo, dev->stream));
+    return FRQ_OK;
+}
+
+int frq_swiglu_rows(frq_device* dev, size_t m, size_t f, const float* gu, size_t ldgu, float* h, size_t ldh) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (m > 65535 || f == 0 || f > 0x7fffffff || ldgu < 2 * f || ldh < f || ldgu > 0x7fffffff || ldh > 0x7fffffff)
+        return fail(FRQ_INVALID, "swiglu_rows: m=%zu f=%zu ldgu=%zu ldh=%zu", m, f, ldgu, ldh);
+    if (m == 0) return FRQ_OK;
+    if (!gu || !h) return fail(FRQ_INVALID, "swiglu_rows: null buffer");
+    HIP_TRY(launch_swiglu_rows(gu, (int)ldgu, (int)m, (int)f, h, (int)ldh, dev->stream));
+    return FRQ_OK;
+}
+
+int frq_add(frq_device* dev, size_t n, const float* x, float* y) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (n == 0) return FRQ_OK;
+    if (!x || !y) return fail(FRQ_INVALID, "add: null buffer");
+    if (n / 256 >= 0x7fffffff) return fail(FRQ_UNSUPPORTED, "add: n=%zu", n);
+    HIP_TRY(launch_add_rows(x, y, n, dev->stream));
+    return FRQ_OK;
+}
+
+int frq_gather_rows(frq_device* dev, const float* table, size_t rows, size_t dim, const int32_t* ids, size_t m,
+                    float* out) {
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (rows == 0 || rows > 0x7fffffff || dim == 0 || dim > 0x7fffffff || m > 65535)
+        return fail(FRQ_INVALID, "gather_rows: rows=%zu dim=%zu m=%zu", rows, dim, m);
+    if (m == 0) return FRQ_OK;
+    if (!table || !ids || !out) return fail(FRQ_INVALID, "gather_rows: null buffer");
+    HIP_TRY(launch_gather_rows(table, (int)rows, (int)dim, ids, (int)m, out, dev->stream));
+    return FRQ_OK;
+}
+
 int frq_argmax_embed(frq_device* dev, const float* logits, size_t vocab, const float* table, size_t dim, int32_t* tokens,
                      size_t tokens_cap, size_t prompt_len, int32_t* pos, float* x) {
     int rc = use_device(dev);

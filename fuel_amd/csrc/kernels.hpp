@@ -163,4 +163,18 @@ hipError_t launch_attn_split(const float* qk, const float* v, const float* rcos,
 hipError_t launch_argmax_embed(const float* logits, int vocab, const float* table, int dim, int* tokens,
                                int tokens_cap, int prompt_len, int* pos, float* x, hipStream_t s);
 
+// prefill.hip: row kernels of a batched prompt pass (M tokens at positions
+// pos0 .. pos0 + M - 1) between the int8-MFMA projections.
+hipError_t launch_rms_norm_rows(const float* x, int ldx, const float* gain, float eps, int M, int K, float* y, int ldy,
+                                hipStream_t s);
+hipError_t launch_rope_append_rows(float* qk, int ldqk, const float* v, int ldv, const float* rcos, const float* rsin,
+                                   int M, int n_heads, int pos0, int max_ctx, uint16_t* kc, uint16_t* vc,
+                                   hipStream_t s);
+hipError_t launch_attention_prefill(const float* q, int ldq, const uint16_t* kc, const uint16_t* vc, int pos0, int M,
+                                    int n_heads, int max_ctx, float scale, float* out, int ldo, hipStream_t s);
+hipError_t launch_swiglu_rows(const float* gu, int ldgu, int M, int f, float* h, int ldh, hipStream_t s);
+hipError_t launch_add_rows(const float* x, float* y, size_t n, hipStream_t s);
+hipError_t launch_gather_rows(const float* table, int rows, int dim, const int* ids, int M, float* out,
+                              hipStream_t s);
+
 }  // namespace frq

@@ -384,6 +384,61 @@ class LlamaDecoder:
         check(L.frq_argmax_embed(h, vp(self.logits.ptr), cfg.vocab, vp(self.embed.ptr), d, vp(self.tokens.ptr),
                                  cfg.max_ctx, self.prompt_len, vp(self.pos.ptr), x))
 
+    def prefill(self, prompt) -> None:
+        """The prompt as one batch (lazy.rs:7363-7446 at seq = M): every layer
+        over all M prompt tokens with the int8-MFMA QMatMul (frq_qmatmul, MFMA
+        from M = 16 rows) and the prefill row kernels, instead of M decode
+        steps.  Leaves the decoder where M forced steps would: cache rows
+        0 .. M-1 filled, the logits of position M-1, tokens[M] their greedy
+        pick, x its embedding, pos = M (the next enqueue_step emits token
+        M+1).  The values differ from the step-by-step path only by summation
+        order (MFMA tiles, one attention pass per query row)."""
+        self.start(prompt)
+        M = self.prompt_len
+        cfg, L, h = self.cfg, self.L, self.dev.handle
+        d, f, H, HD, Cx, eps = cfg.dim, cfg.ffn, cfg.n_heads, cfg.head_dim, cfg.max_ctx, cfg.eps
+        vp = C.c_void_p
+        B = self._batch_buffers(M)
+        x, xn, qk, v, att, o, gu, hh = (B[k].ptr for k in ("x", "xn", "qk", "v", "att", "o", "gu", "h"))
+        check(L.frq_gather_rows(h, vp(self.embed.ptr), cfg.vocab, d, vp(self.tokens.ptr), M, vp(x)))
+        for li, lw in enumerate(self.layers):
+            check(L.frq_rms_norm_rows(h, M, d, vp(x), d, vp(self.attn_gain[li].ptr), eps, vp(xn), d))
+            self._mm(lw["dt_qk"], lw["wqk"], 2 * d, d, xn, qk, M)
+            self._mm(lw["dt_v"], lw["wv"], d, d, xn, v, M)
+            check(L.frq_rope_append_rows(h, M, H, HD, Cx, vp(qk), 2 * d, vp(v), d, vp(self.rcos.ptr),
+                                         vp(self.rsin.ptr), 0, vp(self.kc[li].ptr), vp(self.vc[li].ptr)))
+            check(L.frq_attention_prefill(h, M, H, HD, Cx, vp(qk), 2 * d, vp(self.kc[li].ptr), vp(self.vc[li].ptr),
+                                          0, self.scale, vp(att), d))
+            self._mm(lw["dt_o"], lw["wo"], d, d, att, o, M)
+            check(L.frq_add(h, M * d, vp(o), vp(x)))
+            check(L.frq_rms_norm_rows(h, M, d, vp(x), d, vp(self.ffn_gain[li].ptr), eps, vp(xn), d))
+            self._mm(lw["dt_gu"], lw["wgu"], 2 * f, d, xn, gu, M)
+            check(L.frq_swiglu_rows(h, M, f, vp(gu), 2 * f, vp(hh), f))
+            self._mm(lw["dt_down"], lw["wd"], d, f, hh, o, M)
+            check(L.frq_add(h, M * d, vp(o), vp(x)))
+        # the last prompt row: logits, greedy next token and its embedding, pos = M
+        check(L.frq_qmatmul_fused(h, self.dt_out, 1, cfg.vocab, d, vp(self.wout.ptr), vp(x + (M - 1) * d * 4), d,
+                                  None, vp(self.final_gain.ptr), eps, 0, vp(self.logits.ptr), cfg.vocab))
+        self.pos.copy_from(np.array([M - 1], np.int32))
+        check(L.frq_argmax_embed(h, vp(self.logits.ptr), cfg.vocab, vp(self.embed.ptr), d, vp(self.tokens.ptr),
+                                 cfg.max_ctx, self.prompt_len, vp(self.pos.ptr), vp(self.x.ptr)))
+
+    def _mm(self, dt, w, n, k, x_ptr, y_ptr, M) -> None:
+        """y [M, n] = x [M, k] . W^T through the QMatMul KernelRef seam."""
+        bs = 32 if dt == N.Q8_0 else 256
+        check(self.L.frq_qmatmul(self.dev.handle, dt, 1, M, n, k, C.c_void_p(x_ptr), M * k * 4, C.c_void_p(w.ptr),
+                                 n * (k // bs) * N_TYPE_SIZE[dt], C.c_void_p(y_ptr), M * n * 4))
+
+    def _batch_buffers(self, M: int) -> dict:
+        cap = getattr(self, "_batch_cap", 0)
+        if cap < M:
+            d, f = self.cfg.dim, self.cfg.ffn
+            self._batch = {k: self.dev.alloc((M, n), np.float32) for k, n in
+                           (("x", d), ("xn", d), ("qk", 2 * d), ("v", d), ("att", d), ("o", d), ("gu", 2 * f),
+                            ("h", f))}
+            self._batch_cap = M
+        return self._batch
+
     def _pair(self, lw) -> bool:
         kq = (Q4K, Q6K)
         return lw["dt_qk"] in kq and lw["dt_v"] in kq and self.cfg.dim <= 16384

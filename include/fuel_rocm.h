@@ -238,6 +238,41 @@ int frq_attention_decode_oproj(frq_device *dev, size_t n_heads, size_t head_dim,
                                const float *rope_sin_dev, uint16_t *k_cache_dev, uint16_t *v_cache_dev,
                                const int32_t *pos_dev, float scale, void *work_dev, size_t work_bytes, int o_dtype,
                                const void *w_o_dev, size_t n_out, float *y_dev);
+/* ---- prefill: row kernels of a batched prompt pass ----
+ * LlamaModel::apply_layer (lazy.rs:7363-7446) at seq = m: the projections
+ * are frq_qmatmul calls (int8 MFMA for m >= 16) and these kernels run
+ * between them.  Row-major buffers with leading dimensions in elements. */
+/* y[r] = (x[r] * (1 / sqrt(sum(x[r]^2) / k + eps))) * gain, per row
+ * (rms_norm_last_dim_f32, byte_kernels.rs:2339-2368, and the affine gain,
+ * lazy.rs:10330-10346; the sum of squares is a tree, sequential there). */
+int frq_rms_norm_rows(frq_device *dev, size_t m, size_t k, const float *x_dev, size_t ldx, const float *gain_dev,
+                      float eps, float *y_dev, size_t ldy);
+/* Row r of qk_dev = [q | k] (n_heads * head_dim each) and of v_dev, at
+ * position pos0 + r: q and k rotated (rope_f32 rotate-half,
+ * byte_kernels.rs:1885-1964, with rows of the [max_ctx, head_dim] tables), q
+ * written back in place, k and v rounded to f16 into cache row pos0 + r of
+ * every head ([n_heads, max_ctx, head_dim] caches, as frq_attention_decode
+ * appends).  head_dim = 128. */
+int frq_rope_append_rows(frq_device *dev, size_t m, size_t n_heads, size_t head_dim, size_t max_ctx, float *qk_dev,
+                         size_t ldqk, const float *v_dev, size_t ldv, const float *rope_cos_dev,
+                         const float *rope_sin_dev, size_t pos0, uint16_t *k_cache_dev, uint16_t *v_cache_dev);
+/* Causal attention of m query rows (rotated q, [m, n_heads * head_dim]) at
+ * positions pos0 .. pos0 + m - 1 over the f16 cache rows 0 .. each row's
+ * position (lazy.rs:7415-7425: scores * scale plus the strict-causal mask,
+ * softmax_last_dim, times V), one pass with a running maximum.  The rows
+ * pos0 .. pos0 + m - 1 must already be in the caches (frq_rope_append_rows). */
+int frq_attention_prefill(frq_device *dev, size_t m, size_t n_heads, size_t head_dim, size_t max_ctx,
+                          const float *q_dev, size_t ldq, const uint16_t *k_cache_dev, const uint16_t *v_cache_dev,
+                          size_t pos0, float scale, float *out_dev, size_t ldo);
+/* h[r][i] = silu(gu[r][i]) * gu[r][f + i], silu(g) = g / (1 + exp(-g))
+ * (lazy.rs:7442 on the [gate | up] output of one stacked projection). */
+int frq_swiglu_rows(frq_device *dev, size_t m, size_t f, const float *gu_dev, size_t ldgu, float *h_dev, size_t ldh);
+/* y[i] += x[i] for i < n (the residual adds, lazy.rs:7434, 7446). */
+int frq_add(frq_device *dev, size_t n, const float *x_dev, float *y_dev);
+/* out[r] = table[ids[r]] (rows of dim floats; an id outside [0, rows) reads
+ * row 0): the prompt's embedding rows. */
+int frq_gather_rows(frq_device *dev, const float *table_dev, size_t rows, size_t dim, const int32_t *ids_dev,
+                    size_t m, float *out_dev);
 /* Greedy next token and its embedding: next = tokens[pos + 1] while
  * pos + 1 < prompt_len, else the first-index argmax of logits [vocab]
  * (argmax_dim_f32, byte_kernels.rs:8246-8261), stored at tokens[pos + 1]

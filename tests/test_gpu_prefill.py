@@ -1,0 +1,170 @@
+"""GPU parity of the batched prompt pass (prefill): the row kernels against
+the CPU oracle, and the decoder's prefill against its own step-by-step path
+and the CPU decoder.
+
+Bit-exact: the rotated, f16-rounded cache rows (rope_f32 has no fused
+multiply-add; neither has the kernel), SwiGLU against the decode path's
+own product, the gathers and adds.  f32: the RMS norm within 1e-6 (a tree sum
+against the reference's sequential one), attention within 1e-5 (f32, no
+quantization).  Decoder: the logits after a prefill within 1e-2 of their norm
+of both the step-by-step path's and the CPU path's (the projections run on
+the int8 MFMA from 16 rows; a different f32 summation order flips single Q8K
+activation roundings, which the decode tests bound the same way).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import fuel_amd as F
+import oracle as O
+from blockref import rel_err
+from fuel_amd.llama import LlamaConfig, LlamaDecoder
+from test_gpu_decode import SMALL, DEC_TOL, oracle_model
+
+pytestmark = pytest.mark.gpu
+L = F.lib
+vp = C.c_void_p
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+@pytest.mark.parametrize("m,k", [(1, 256), (37, 4096), (512, 4096), (3, 11008)])
+def test_rms_norm_rows(dev, m, k):
+    say("rms_norm_rows", m, k)
+    x = O.normal((m, k), seed=k + m, stream=1, std=3.0)
+    g = 1 + O.normal((k,), seed=k + m, stream=2, std=0.2)
+    xd, gd, y = dev.from_numpy(x), dev.from_numpy(g), dev.alloc((m, k), np.float32)
+    F._native.check(L().frq_rms_norm_rows(dev.handle, m, k, vp(xd.ptr), k, vp(gd.ptr), 1e-5, vp(y.ptr), k))
+    want = O.rms_norm(x, g, 1e-5)
+    for r in range(m):
+        assert rel_err(y.numpy()[r], want[r]) < 1e-6, r
+
+
+@pytest.mark.parametrize("m,H,max_ctx,pos0", [(24, 2, 32, 0), (5, 4, 64, 40), (512, 32, 768, 0)])
+def test_rope_append_rows(dev, m, H, max_ctx, pos0):
+    say("rope_append_rows", m, H, max_ctx, pos0)
+    d = H * 128
+    qk = O.normal((m, 2 * d), seed=m + H, stream=1, std=2.0)
+    v = O.normal((m, d), seed=m + H, stream=2)
+    c, s = O.rope_tables(10000.0, 0, max_ctx, 128)
+    qkd, vd, cd, sd = (dev.from_numpy(a) for a in (qk, v, c, s))
+    kc = dev.from_numpy(np.full((H, max_ctx, 128), 0x7e00, np.uint16))  # NaN outside the written rows
+    vc = dev.from_numpy(np.full((H, max_ctx, 128), 0x7e00, np.uint16))
+    F._native.check(L().frq_rope_append_rows(dev.handle, m, H, 128, max_ctx, vp(qkd.ptr), 2 * d, vp(vd.ptr), d,
+                                             vp(cd.ptr), vp(sd.ptr), pos0, vp(kc.ptr), vp(vc.ptr)))
+    ct, st = c[pos0:pos0 + m], s[pos0:pos0 + m]
+    q = O.rope(qk[:, :d].reshape(m, H, 128).transpose(1, 0, 2), ct, st)        # [H, m, 128]
+    k = O.rope(qk[:, d:].reshape(m, H, 128).transpose(1, 0, 2), ct, st)
+    got = qkd.numpy()
+    np.testing.assert_array_equal(got[:, :d].reshape(m, H, 128).transpose(1, 0, 2), q)
+    np.testing.assert_array_equal(got[:, d:], qk[:, d:])  # k is not written back
+    kh, vh = kc.numpy(), vc.numpy()
+    np.testing.assert_array_equal(kh[:, pos0:pos0 + m], k.astype(np.float16).view(np.uint16))
+    np.testing.assert_array_equal(vh[:, pos0:pos0 + m],
+                                  v.reshape(m, H, 128).transpose(1, 0, 2).astype(np.float16).view(np.uint16))
+    assert (kh[:, :pos0] == 0x7e00).all() and (kh[:, pos0 + m:] == 0x7e00).all()
+
+
+@pytest.mark.parametrize("m,H,max_ctx,pos0", [(24, 2, 32, 0), (17, 3, 128, 50), (64, 32, 768, 0), (1, 2, 64, 0)])
+def test_attention_prefill(dev, m, H, max_ctx, pos0):
+    """Each query row attends to cache rows 0 .. its position: the CPU
+    path's single-token attention at that position, within 1e-5."""
+    say("attention_prefill", m, H, max_ctx, pos0)
+    rng = np.random.default_rng(m + H)
+    kc = rng.standard_normal((H, max_ctx, 128)).astype(np.float16)
+    vc = rng.standard_normal((H, max_ctx, 128)).astype(np.float16)
+    kc[:, pos0 + m:] = np.float16(np.nan)  # rows past the last position are never read
+    vc[:, pos0 + m:] = np.float16(np.nan)
+    q = O.normal((m, H * 128), seed=m, stream=3, std=2.0)
+    qd, kd, vd = dev.from_numpy(q), dev.from_numpy(kc.view(np.uint16)), dev.from_numpy(vc.view(np.uint16))
+    out = dev.alloc((m, H * 128), np.float32)
+    scale = float(np.float32(1 / np.sqrt(128.0)))
+    F._native.check(L().frq_attention_prefill(dev.handle, m, H, 128, max_ctx, vp(qd.ptr), H * 128, vp(kd.ptr),
+                                              vp(vd.ptr), pos0, scale, vp(out.ptr), H * 128))
+    got = out.numpy()
+    kf, vf = kc.astype(np.float32), vc.astype(np.float32)
+    for r in range(m):
+        want = O.attention_decode(q[r].reshape(H, 128), kf, vf, pos0 + r + 1, scale).reshape(-1)
+        assert rel_err(got[r], want) < 1e-5, r
+
+
+def test_swiglu_add_gather_rows(dev):
+    m, f = 7, 1000
+    gu = O.normal((m, 2 * f), seed=5, stream=1, std=2.0)
+    gud, h = dev.from_numpy(gu), dev.alloc((m, f), np.float32)
+    F._native.check(L().frq_swiglu_rows(dev.handle, m, f, vp(gud.ptr), 2 * f, vp(h.ptr), f))
+    g, u = gu[:, :f], gu[:, f:]
+    np.testing.assert_allclose(h.numpy(), (g / (np.float32(1) + np.exp(-g)) * u).astype(np.float32), rtol=2e-6)
+    x = O.normal((m * f,), seed=6, stream=1)
+    y0 = O.normal((m * f,), seed=6, stream=2)
+    xd, yd = dev.from_numpy(x), dev.from_numpy(y0)
+    F._native.check(L().frq_add(dev.handle, m * f, vp(xd.ptr), vp(yd.ptr)))
+    np.testing.assert_array_equal(yd.numpy(), y0 + x)
+    table = O.normal((50, 96), seed=7, stream=1)
+    ids = np.array([3, 0, 49, 7, 60, -1], np.int32)  # out-of-range ids read row 0
+    td, idd, out = dev.from_numpy(table), dev.from_numpy(ids), dev.alloc((6, 96), np.float32)
+    F._native.check(L().frq_gather_rows(dev.handle, vp(td.ptr), 50, 96, vp(idd.ptr), 6, vp(out.ptr)))
+    np.testing.assert_array_equal(out.numpy(), table[[3, 0, 49, 7, 0, 0]])
+
+
+def test_prefill_errors(dev):
+    x = dev.alloc((4096,), np.float32)
+    with pytest.raises(F.FuelRocmError):  # head_dim
+        F._native.check(L().frq_attention_prefill(dev.handle, 1, 2, 64, 32, vp(x.ptr), 256, vp(x.ptr), vp(x.ptr),
+                                                  0, 0.1, vp(x.ptr), 256))
+    with pytest.raises(F.FuelRocmError):  # rows past max_ctx
+        F._native.check(L().frq_rope_append_rows(dev.handle, 10, 2, 128, 32, vp(x.ptr), 512, vp(x.ptr), 256,
+                                                 vp(x.ptr), vp(x.ptr), 30, vp(x.ptr), vp(x.ptr)))
+    with pytest.raises(F.FuelRocmError):  # ldx < k
+        F._native.check(L().frq_rms_norm_rows(dev.handle, 2, 256, vp(x.ptr), 128, vp(x.ptr), 1e-5, vp(x.ptr), 256))
+
+
+@pytest.fixture(scope="module")
+def prefill_pair(dev):
+    """Two small decoders with the same weights: one prefills, one steps."""
+    return (LlamaDecoder(dev, LlamaConfig(**SMALL), seed=99, std=0.05),
+            LlamaDecoder(dev, LlamaConfig(**SMALL), seed=99, std=0.05))
+
+
+@pytest.mark.parametrize("plen", [24, 9])
+def test_decoder_prefill_matches_steps(dev, prefill_pair, plen):
+    """A prefill of the prompt (int8 MFMA from 16 rows) leaves the same state
+    as stepping through it: logits of the last prompt position within
+    DEC_TOL of the step path's and of the CPU decoder's, the caches' rows
+    likewise, and decoding continues from pos = len(prompt)."""
+    say("decoder prefill", plen)
+    pre, step = prefill_pair
+    rng = np.random.default_rng(plen)
+    prompt = rng.integers(0, SMALL["vocab"], plen).astype(np.int32)
+    pre.prefill(prompt)
+    assert pre.pos.numpy()[0] == plen
+    lp = pre.logits.numpy().copy()
+    step.start(prompt)
+    for _ in range(plen):
+        step.enqueue_step()
+    ls = step.logits.numpy().copy()
+    err = rel_err(lp, ls)
+    say("  logits vs steps", err)
+    assert err < DEC_TOL
+    ref = oracle_model(step)
+    for p in range(plen):
+        lo = ref.step(int(prompt[p]), p)
+    assert rel_err(lp, lo) < DEC_TOL
+    for li in range(SMALL["n_layers"]):
+        kp, vp_ = pre.kv_host(li)
+        ks, vs = step.kv_host(li)
+        assert rel_err(kp[:, :plen], ks[:, :plen]) < DEC_TOL and rel_err(vp_[:, :plen], vs[:, :plen]) < DEC_TOL
+    # the greedy pick of the last prompt position is the next token; x is its embedding
+    tok = pre.tokens_host()[plen]
+    assert tok == int(np.argmax(lp))
+    np.testing.assert_array_equal(pre.x.numpy(), pre.embed.numpy()[tok])
+    # decoding continues from pos = plen: one more step from both states (when
+    # both picked the same token; a near-tie may be broken either way)
+    assert step.pos.numpy()[0] == plen
+    if step.tokens_host()[plen] == tok:
+        step.enqueue_step()
+        pre.enqueue_step()
+        assert rel_err(pre.logits.numpy(), step.logits.numpy()) < DEC_TOL
