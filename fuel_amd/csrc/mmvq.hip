@@ -347,7 +347,10 @@ hipError_t launch_qmv_wg(const uint8_t* w, const float* x, float* y, int M, int 
 template <class F, int SPL, int MODE>
 hipError_t launch_qmv(const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy, const QmvOpts& ix,
                       hipStream_t s, int num_cus) {
-    constexpr int WGN = qmv_wg<F, SPL>(), WGB = qmv_wg_big<F, SPL>();
+    // (the GLU mode reduces two rows per output: at most 512 threads there)
+    constexpr int WGN0 = qmv_wg<F, SPL>(), WGB0 = qmv_wg_big<F, SPL>();
+    constexpr int WGN = MODE == QMV_GLU && WGN0 > 512 ? 512 : WGN0;
+    constexpr int WGB = MODE == QMV_GLU && WGB0 > 512 ? 512 : WGB0;
     if (WGB != WGN && (size_t)N * (size_t)M <= (size_t)num_cus * (WGB / 64) * 2)
         return launch_qmv_wg<F, SPL, WGB, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
     return launch_qmv_wg<F, SPL, WGN, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
@@ -386,8 +389,11 @@ hipError_t launch_dtype(int dtype, const uint8_t* w, const float* x, float* y, i
 template <class F1, class F2, int SPL>
 hipError_t launch_pair_spl(const uint8_t* w1, float* y1, int n1, const uint8_t* w2, float* y2, int n2, const float* x,
                            int M, int K, const QmvOpts& o, hipStream_t s, int num_cus) {
+    // (at most 512 threads: three such workgroups per CU keep more rows in
+    // flight than one of 1024; measured on the 7B decode's q|k + v pair +1%)
     constexpr int WG1 = qmv_wg_big<F1, SPL>(), WG2 = qmv_wg_big<F2, SPL>();
-    constexpr int WG = WG1 < WG2 ? WG1 : WG2;
+    constexpr int WG12 = WG1 < WG2 ? WG1 : WG2;
+    constexpr int WG = WG12 > 512 ? 512 : WG12;
     constexpr int NW = WG / 64;
     static int occ = -1;
     if (occ < 0) {
