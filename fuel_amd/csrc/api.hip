@@ -712,9 +712,16 @@ int frq_moe_ffn(frq_device* dev, int dt, size_t t, size_t d, size_t ffn, size_t 
     float* yd = reinterpret_cast<float*>(carve(ydb));
     void* ax = carve(axb);
     void* ah = carve(ahb);
-    if ((rc = route_and_batch(dev, logits, t, e, topk, ids, wts, offsets, sorted_token, nullptr, entry_expert,
-                              entry_pos, tiles)))
-        return rc;
+    // The grouped path needs the expert batches; the mat-vec path takes its
+    // launch rows in (token, slot) order straight from the routing, and the
+    // combine still sums each token's entries in ascending expert order.
+    if (grouped) {
+        if ((rc = route_and_batch(dev, logits, t, e, topk, ids, wts, offsets, sorted_token, nullptr, entry_expert,
+                                  entry_pos, tiles)))
+            return rc;
+    } else {
+        HIP_TRY(launch_moe_route(logits, (int)t, (int)e, (int)topk, ids, wts, dev->stream));
+    }
     const size_t gate_bytes = ffn * (d / bs) * type_size(dt);
     const size_t down_bytes = d * (ffn / bs) * type_size(dt);
     if (grouped) {
@@ -744,12 +751,12 @@ int frq_moe_ffn(frq_device* dev, int dt, size_t t, size_t d, size_t ffn, size_t 
         HIP_TRY(launch_moe_combine(yd, ids, wts, entry_pos, (int)t, (int)topk, (int)d, out, dev->stream));
         return FRQ_OK;
     }
-    // gate | up in one launch over the sorted entries: gu[p] = [gate(x) | up(x)]
+    // gate | up in one launch over the entries: gu[p] = [gate(x[p / topk]) | up(x[p / topk])]
     QmvOpts gi{};
-    gi.x_row = sorted_token;
-    gi.x_div = 1;
+    gi.x_row = nullptr;
+    gi.x_div = (int)topk;
     gi.ldx = (int)d;
-    gi.w_sel = entry_expert;
+    gi.w_sel = ids;
     gi.n_experts = (int)e;
     gi.expert_bytes = gate_bytes;
     gi.w2 = static_cast<const uint8_t*>(w_up);
@@ -762,13 +769,13 @@ int frq_moe_ffn(frq_device* dev, int dt, size_t t, size_t d, size_t ffn, size_t 
     di.x_row = nullptr;
     di.x_div = 1;
     di.ldx = (int)(2 * ffn);
-    di.w_sel = entry_expert;
+    di.w_sel = ids;
     di.n_experts = (int)e;
     di.expert_bytes = down_bytes;
     di.x2 = gu + ffn;
     if ((rc = run_indexed(dev, dt, static_cast<const uint8_t*>(w_down), gu, p, (int)d, (int)ffn, yd, (int)d, di)))
         return rc;
-    HIP_TRY(launch_moe_combine(yd, ids, wts, entry_pos, (int)t, (int)topk, (int)d, out, dev->stream));
+    HIP_TRY(launch_moe_combine(yd, ids, wts, nullptr, (int)t, (int)topk, (int)d, out, dev->stream));
     return FRQ_OK;
 }
 

@@ -30,13 +30,15 @@ __global__ __launch_bounds__(ROUTE_WG) void moe_route_kernel(const float* __rest
     const int t = blockIdx.x * (ROUTE_WG / 64) + (threadIdx.x >> 6);
     if (t >= T) return;  // whole wavefront
     const float* lr = logits + (size_t)t * E;
-    float v[EPL];  // element j = lane + 64 i
+    float v[EPL], orig[EPL];  // element j = lane + 64 i (orig: as loaded, for the softmax)
 #pragma unroll
     for (int i = 0; i < EPL; i++) {
         const int j = lane + 64 * i;
-        v[i] = j < E ? lr[j] : 0.0f;
+        orig[i] = lr[j < E ? j : E - 1];
+        v[i] = orig[i];
     }
-    int my_id = 0;  // lane s < topk keeps the s-th pick
+    int my_id = 0;       // lane s < topk keeps the s-th pick
+    float my_val = 0.0f; // and its original logit
     for (int s = 0; s < topk; s++) {
         float bv = -INFINITY;
         int bi = 0x7fffffff;
@@ -51,13 +53,22 @@ __global__ __launch_bounds__(ROUTE_WG) void moe_route_kernel(const float* __rest
             const int oi = __shfl_xor(bi, off);
             argmax_merge(bv, bi, ov, oi);
         }
-        if (lane == s) my_id = bi;
+        float pv = 0.0f;  // the pick's original logit, from its owner lane
+#pragma unroll
+        for (int i = 0; i < EPL; i++) {
+            const float o = __shfl(orig[i], bi & 63);
+            if ((bi >> 6) == i) pv = o;
+        }
+        if (lane == s) {
+            my_id = bi;
+            my_val = pv;
+        }
 #pragma unroll
         for (int i = 0; i < EPL; i++)
             if (lane + 64 * i == bi) v[i] += -1e30f;
     }
     // softmax over the picked (original) logits, in pick order
-    const float p = lane < topk ? lr[my_id] : 0.0f;
+    const float p = lane < topk ? my_val : 0.0f;
     float mx = __shfl(p, 0);
     for (int s = 1; s < topk; s++) {
         const float ps = __shfl(p, s);
@@ -187,7 +198,9 @@ __global__ __launch_bounds__(BATCH_WG) void moe_batches_kernel(const int* __rest
 constexpr int COMBINE_WG = 256;
 
 // out[t, :] = sum over the token's entries in ascending expert order (equal
-// experts in slot order) of yd[pos, :] * w; the sum starts from 0.
+// experts in slot order) of yd[pos, :] * w; the sum starts from 0.  pos is
+// the entry's row in yd: entry_pos[t * topk + slot] (expert-sorted rows), or
+// t * topk + slot when entry_pos is null (rows in routing order).
 __global__ __launch_bounds__(COMBINE_WG) void moe_combine_kernel(const float* __restrict__ yd,
                                                                 const int* __restrict__ ids,
                                                                 const float* __restrict__ wts,
@@ -201,7 +214,7 @@ __global__ __launch_bounds__(COMBINE_WG) void moe_combine_kernel(const float* __
         const int e = ti[tid];
         int rank = 0;
         for (int s = 0; s < topk; s++) rank += ti[s] < e || (ti[s] == e && s < tid);
-        opos[rank] = entry_pos[(size_t)t * topk + tid];
+        opos[rank] = entry_pos ? entry_pos[(size_t)t * topk + tid] : t * topk + tid;
         ow[rank] = wts[(size_t)t * topk + tid];
     }
     __syncthreads();
