@@ -11,7 +11,7 @@
 //   attention_prefill causal scaled-dot-product attention of each query row
 //                     over cache rows 0 .. its position (lazy.rs:7415-7425:
 //                     scores * scale + causal mask, softmax_last_dim, . V),
-//                     one pass with a running maximum (online softmax)
+//                     one pass with a running maximum, eight rows per step
 //   swiglu_rows       silu(g) * u (lazy.rs:7442)
 //   add_rows          the residual adds (lazy.rs:7434, 7446)
 //   gather_rows       embedding rows of the prompt tokens
@@ -80,6 +80,7 @@ __global__ __launch_bounds__(HD) void rope_append_rows_kernel(float* __restrict_
 
 constexpr int AP_WG = 256;
 constexpr int AP_Q = AP_WG / 16;  // query rows per workgroup (16 lanes each, 8 dims per lane)
+constexpr int AP_KB = 8;          // cache rows whose loads are in flight together
 
 __device__ __forceinline__ float group16_sum(float v) {
 #pragma unroll
@@ -98,10 +99,11 @@ __device__ __forceinline__ void h8_to_f(const uint4& u, float (&f)[8]) {
 
 // grid (heads, ceil(M / AP_Q)), AP_WG threads: 16-lane group g takes query row
 // m = AP_Q * blockIdx.y + g (position pos0 + m) and walks cache rows
-// 0 .. position with a running maximum: per row j the score s = (q . k_j) *
-// scale, M' = max(M, s), l = l e^(M - M') + e^(s - M'), o = o e^(M - M') +
-// e^(s - M') v_j; out = o / l.  Rows past a group's position (the wave runs
-// to its last group's) are skipped by a uniform-per-group select.
+// 0 .. position AP_KB at a time with a running maximum: the step's scores
+// s_j = (q . k_j) * scale, M' = max(M, s_j of the step), l = l e^(M - M') +
+// sum e^(s_j - M'), o = o e^(M - M') + sum e^(s_j - M') v_j; out = o / l.
+// Rows past a group's position (the wave runs to its last group's) are
+// dropped by selects.
 __global__ __launch_bounds__(AP_WG) void attention_prefill_kernel(const float* __restrict__ q, int ldq,
                                                                   const __half* __restrict__ kc,
                                                                   const __half* __restrict__ vc, int pos0, int M,
@@ -120,22 +122,47 @@ __global__ __launch_bounds__(AP_WG) void attention_prefill_kernel(const float* _
     for (int e = 0; e < 8; e++) q8[e] = qr[e];
     const size_t cbase = (size_t)h * max_ctx * HD + 8 * l16;
     float mx = -__builtin_inff(), l = 0.0f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int j = 0; j <= jend; j++) {
-        float kv[8], vv[8];
-        h8_to_f(*reinterpret_cast<const uint4*>(kc + cbase + (size_t)j * HD), kv);
-        h8_to_f(*reinterpret_cast<const uint4*>(vc + cbase + (size_t)j * HD), vv);
-        float d = 0.0f;
+    // AP_KB cache rows per step, all their loads issued before the first is
+    // used (rows past jend repeat row jend and are skipped like any row past a
+    // group's position), so a step costs one memory round trip, not AP_KB
+    for (int j0 = 0; j0 <= jend; j0 += AP_KB) {
+        uint4 kr[AP_KB], vr[AP_KB];
 #pragma unroll
-        for (int e = 0; e < 8; e++) d = fmaf(q8[e], kv[e], d);
-        const float s = group16_sum(d) * scale;
-        if (j <= pos) {  // (uniform over the 16-lane group)
-            const float mn = fmaxf(mx, s);
-            const float c = expf(mx - mn), p = expf(s - mn);
-            l = fmaf(l, c, p);
-#pragma unroll
-            for (int e = 0; e < 8; e++) o[e] = fmaf(o[e], c, p * vv[e]);
-            mx = mn;
+        for (int u = 0; u < AP_KB; u++) {
+            const size_t jr = (size_t)min(j0 + u, jend) * HD;
+            kr[u] = *reinterpret_cast<const uint4*>(kc + cbase + jr);
+            vr[u] = *reinterpret_cast<const uint4*>(vc + cbase + jr);
         }
+        // the step's scores (rows past the group's position: -inf), one
+        // rescale to the step's maximum, then the rows' weighted values
+        float sv[AP_KB];
+        float mn = mx;
+#pragma unroll
+        for (int u = 0; u < AP_KB; u++) {
+            float kv[8];
+            h8_to_f(kr[u], kv);
+            float d = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) d = fmaf(q8[e], kv[e], d);
+            const float sc = group16_sum(d) * scale;
+            sv[u] = j0 + u <= pos ? sc : -__builtin_inff();
+            mn = fmaxf(mn, sv[u]);
+        }
+        const float c = expf(mx - mn);  // (the first step: mx = -inf, l = o = 0; row 0 is always live)
+        l *= c;
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[e] *= c;
+#pragma unroll
+        for (int u = 0; u < AP_KB; u++) {
+            const bool live = j0 + u <= pos;
+            const float p = expf(sv[u] - mn);
+            float vv[8];
+            h8_to_f(vr[u], vv);
+            l = live ? l + p : l;
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[e] = live ? fmaf(p, vv[e], o[e]) : o[e];
+        }
+        mx = mn;
     }
     if (m < M) {
         float* orow = out + (size_t)m * ldo + (size_t)h * HD + 8 * l16;
