@@ -8,7 +8,11 @@ each pass also runs device copies of a known size, whose counter readings give
 the factor that converts FETCH_SIZE / WRITE_SIZE to bytes.  Writes a Markdown
 summary and a JSON file (traffic bytes per launch) into --out.
 
-Usage: python bench_profile.py [--shape 4096x32000] [--out gpurun_out/profiles]
+With --leg decode / batched / moe it instead runs one --kernel-trace --stats
+pass over that bench.py leg (config 4 decode + batched prompt, config 3
+M = 32/128/512 matmuls, config 5 MoE layer) and writes the per-kernel summary.
+
+Usage: python bench_profile.py [--shape 4096x32000] [--leg matvec|decode|batched|moe] [--out gpurun_out/profiles]
 """
 from __future__ import annotations
 
@@ -36,15 +40,53 @@ def rows(d: str, name: str):
         yield from csv.DictReader(open(f))
 
 
+# one kernel-trace pass per leg: (bench.py arguments, summary file name, title)
+LEGS = {
+    "decode": (["--decode-only", "--no-cpu"], "decode_7b_q4km",
+               "Config 4: 7B Q4_K_M decode (512-token batched prompt, 512 forced steps, 256 greedy tokens)"),
+    "batched": (["--shape", "4096x4096", "--steps", "5", "--warmup", "1", "--no-cpu", "--no-decode", "--no-moe"],
+                "mmq_batched_m32_m128_m512",
+                "Config 3: Q4_K / Q6_K QMatMul at M = 32, 128, 512 (int8 MFMA), 7B layer shapes"),
+    "moe": (["--shape", "4096x4096", "--steps", "5", "--warmup", "1", "--no-cpu", "--no-decode", "--no-batched",
+             "--no-q6k"], "moe_qwen3_layer", "Config 5: Qwen3-MoE layer (route, gate|up, down, combine) at T = 1/16/512"),
+}
+
+
+def trace_leg(leg: str, out: str, summarize_only: bool) -> int:
+    bargs, name, title = LEGS[leg]
+    cmd = ["rocprofv3", "--kernel-trace", "--stats", "--output-format", "csv", "-d", f"{out}/{name}", "-o", "run",
+           "--", "python3", "bench.py"] + bargs
+    if not summarize_only:
+        run(cmd, f"{out}/{name}.log", 600)
+    stats = list(rows(f"{out}/{name}", "run_kernel_stats.csv"))
+    total_ns = sum(float(r["TotalDurationNs"]) for r in stats)
+    with open(os.path.join(ROOT, out, f"{name}.md"), "w") as f:
+        f.write(f"# {title}\n\n")
+        f.write(f"Made by `python3 bench_profile.py --leg {leg}` (repository root, one MI355X), which runs:\n\n")
+        f.write(f"`{' '.join(cmd)}`\n\n")
+        f.write(f"rocprofv3 --stats kernel summary: {len(stats)} kernels, {total_ns / 1e6:.2f} ms of kernel time "
+                "in the whole run (warm-up and checks included).\n\n")
+        f.write("| kernel | calls | avg us | min us | max us | total ms | % |\n|---|---|---|---|---|---|---|\n")
+        for r in sorted(stats, key=lambda r: -float(r["TotalDurationNs"]))[:24]:
+            f.write(f"| `{r['Name'][:110]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                    f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | "
+                    f"{float(r['TotalDurationNs']) / 1e6:.3f} | {float(r['Percentage']):.1f} |\n")
+    print(f"wrote {out}/{name}.md", flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--shape", default="4096x32000")
+    ap.add_argument("--leg", default="matvec", choices=["matvec"] + sorted(LEGS))
     ap.add_argument("--out", default="gpurun_out/profiles")
     ap.add_argument("--summarize-only", action="store_true", help="re-read existing pass outputs")
     args = ap.parse_args()
     os.makedirs(os.path.join(ROOT, args.out), exist_ok=True)
     out = args.out  # relative to the repository root, where every pass runs
     os.environ.setdefault("TMPDIR", "/tmp")
+    if args.leg != "matvec":
+        return trace_leg(args.leg, out, args.summarize_only)
     bench = ["python3", "bench.py", "--shape", args.shape, "--steps", "50", "--warmup", "5", "--no-cpu",
              "--no-decode", "--no-batched", "--no-moe", "--no-q6k", "--copy-bytes", str(COPY_BYTES)]
     cmds = {
