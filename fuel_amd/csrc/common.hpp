@@ -113,6 +113,23 @@ __device__ __forceinline__ float dpp_wave_sum(float v) {
     return v;
 }
 
+// Sum over each 64/RPW-lane segment of the wavefront (RPW = 2 or 4), in the
+// order dpp_wave_sum adds those lanes; valid in the segment's last lane.
+template <int RPW>
+__device__ __forceinline__ float dpp_seg_sum(float v) {
+    static_assert(RPW == 2 || RPW == 4, "segments of 32 or 16 lanes");
+#define FRQ_DPP_ADD(ctrl, rmask)                                                                         \
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, rmask, \
+                                                               0xF, false))
+    FRQ_DPP_ADD(0xB1, 0xF);
+    FRQ_DPP_ADD(0x4E, 0xF);
+    FRQ_DPP_ADD(0x141, 0xF);
+    FRQ_DPP_ADD(0x140, 0xF);  // each 16-lane row holds its sum
+    if constexpr (RPW == 2) FRQ_DPP_ADD(0x142, 0xA);  // rows 1, 3 add rows 0, 2
+#undef FRQ_DPP_ADD
+    return v;
+}
+
 __device__ __forceinline__ int wave_sum_i(int v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);

@@ -58,8 +58,9 @@ __device__ __forceinline__ void qmv_load_row(const uint8_t* __restrict__ wr, int
 }
 
 // Row dot product of one weight row (raw registers) with the LDS activation;
-// the f32 total is valid in lane 63.
-template <class F, int SPL>
+// the f32 total is valid in lane 63 (RPW > 1: each 64/RPW-lane segment holds
+// its own row, total in the segment's last lane).
+template <class F, int SPL, int RPW = 1>
 __device__ __forceinline__ float qmv_row(const typename F::Raw (&r)[SPL], const int8_t* s_qs, int qstride,
                                          const float* s_d, const int16_t* s_bs, int gi, int c, int KB) {
     constexpr int BPW = 64 / F::LPB;
@@ -77,7 +78,8 @@ __device__ __forceinline__ float qmv_row(const typename F::Raw (&r)[SPL], const 
             acc = fmaf(-(dmw * xa.d), (float)msum, acc);
         }
     }
-    return dpp_wave_sum(acc);
+    if constexpr (RPW == 1) return dpp_wave_sum(acc);
+    else return dpp_seg_sum<RPW>(acc);
 }
 
 // QMV_HALF: f16 activations in (x holds halves), f16 outputs (y holds
@@ -170,7 +172,10 @@ __device__ __forceinline__ float block_sum_waves(float v, float* s_red, int w, i
 }
 
 // The mat-vec of one workgroup: block bx of gxn walking the rows of W.
-template <class F, int SPL, int WG, int MODE>
+// RPW > 1 (rows of at most 16/RPW superblocks, SPL == 1): a wavefront step
+// covers RPW consecutive rows, 16/RPW block slots each, instead of one row
+// with most slots past its end; `row` then counts groups of RPW rows.
+template <class F, int SPL, int WG, int MODE, int RPW = 1>
 __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const float* __restrict__ x,
                                          float* __restrict__ y, int N, int K, int ldy, const QmvOpts& ix, int bx,
                                          int gxn, uint8_t* smem, float* s_red) {
@@ -242,10 +247,15 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
     auto wrow = [&](int r) { return r < n_split ? W + (size_t)r * row_bytes : W2 + (size_t)(r - n_split) * row_bytes; };
     typename F::Raw ra[SPL], rb[SPL];
     float resa = 0.0f, resb = 0.0f;  // residual values, loaded ahead of their row's weights
+    static_assert(RPW == 1 || (SPL == 1 && 64 / F::LPB == 16), "row groups: one slot set of 16 blocks");
+    constexpr int SB = (64 / F::LPB) / RPW;              // block slots per row of a group
+    const int rsub = RPW > 1 ? gi / SB : 0;              // this lane's row within the group
+    const int gb = RPW > 1 ? gi % SB : gi;               // and its first block slot
     {  // (every lane, unconditionally: a wavefront without rows loads the last row and never uses it)
-        const int r0 = row < N ? row : N - 1;
+        const int rr = RPW > 1 ? row * RPW + rsub : row;
+        const int r0 = rr < N ? rr : N - 1;
         if (acc_out) resa = yr[r0];
-        qmv_load_row<F, SPL>(wrow(r0), gi, c, KB, ra);
+        qmv_load_row<F, SPL>(wrow(r0), gb, c, KB, ra);
     }
     if constexpr (MODE == QMV_ATTN) {
         __builtin_amdgcn_sched_barrier(0);  // the merge's waits come after the first row's loads are out
@@ -276,6 +286,34 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
         }
         return;
     }
+    if constexpr (RPW > 1) {
+        // the two-row ring below over groups of RPW rows; the segment's last
+        // lane stores its row
+        const int ng = (N + RPW - 1) / RPW;
+        const bool seg_last = (lane & (64 / RPW - 1)) == 64 / RPW - 1;
+        while (row < ng) {
+            int ngrp = row + nw;
+            int lg = ngrp < ng ? ngrp : row;
+            int lr = lg * RPW + rsub < N ? lg * RPW + rsub : N - 1;
+            if (acc_out) resb = yr[lr];
+            qmv_load_row<F, SPL>(wrow(lr), gb, c, KB, rb);
+            float t = qmv_row<F, SPL, RPW>(ra, s_qs, lay.qstride, s_d, s_bs, gb, c, KB);
+            int my = row * RPW + rsub;
+            if (seg_last && my < N) store(my, acc_out ? resa + t : t);
+            row = ngrp;
+            if (row >= ng) break;
+            ngrp = row + nw;
+            lg = ngrp < ng ? ngrp : row;
+            lr = lg * RPW + rsub < N ? lg * RPW + rsub : N - 1;
+            if (acc_out) resa = yr[lr];
+            qmv_load_row<F, SPL>(wrow(lr), gb, c, KB, ra);
+            t = qmv_row<F, SPL, RPW>(rb, s_qs, lay.qstride, s_d, s_bs, gb, c, KB);
+            my = row * RPW + rsub;
+            if (seg_last && my < N) store(my, acc_out ? resb + t : t);
+            row = ngrp;
+        }
+        return;
+    }
     // Two-row ring: the next row's loads are in flight while a row is reduced.
     // Past the last row a wave re-issues its current row (cache-resident)
     // rather than branching around the loads.
@@ -298,12 +336,12 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
     }
 }
 
-template <class F, int SPL, int WG, int MODE>
+template <class F, int SPL, int WG, int MODE, int RPW = 1>
 __global__ __launch_bounds__(WG) void qmv_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
                                                  float* __restrict__ y, int N, int K, int ldy, QmvOpts ix) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float s_red[WG / 64];
-    qmv_body<F, SPL, WG, MODE>(W, x, y, N, K, ldy, ix, blockIdx.x, gridDim.x, smem, s_red);
+    qmv_body<F, SPL, WG, MODE, RPW>(W, x, y, N, K, ldy, ix, blockIdx.x, gridDim.x, smem, s_red);
 }
 
 // Two matrices of the same activation rows in one launch: workgroups
@@ -322,25 +360,27 @@ __global__ __launch_bounds__(WG) void qmv_pair_kernel(const uint8_t* __restrict_
 
 namespace {
 
-template <class F, int SPL, int WG, int MODE>
+template <class F, int SPL, int WG, int MODE, int RPW = 1>
 hipError_t launch_qmv_wg(const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy, const QmvOpts& ix,
                          hipStream_t s, int num_cus) {
     constexpr int NW = WG / 64;
     static int occ = -1;  // resident workgroups per CU for this instantiation
     if (occ < 0) {
         int o = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, qmv_kernel<F, SPL, WG, MODE>, WG, 16384) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, qmv_kernel<F, SPL, WG, MODE, RPW>, WG, 16384) !=
+                hipSuccess ||
             o < 1)
             o = 1;
         occ = o;
     }
     const size_t lds = (size_t)act_lds_layout(F::ACT, K).bytes;
     if (lds > 65536) return hipErrorInvalidValue;
-    const int need = (N + NW - 1) / NW;
+    const int groups = (N + RPW - 1) / RPW;  // (rows, or groups of RPW rows)
+    const int need = (groups + NW - 1) / NW;
     int cap = num_cus * occ / (M > 0 ? M : 1);
     if (cap < 1) cap = 1;
     const int gx = need < cap ? need : cap;
-    hipLaunchKernelGGL((qmv_kernel<F, SPL, WG, MODE>), dim3(gx, M), dim3(WG), lds, s, w, x, y, N, K, ldy, ix);
+    hipLaunchKernelGGL((qmv_kernel<F, SPL, WG, MODE, RPW>), dim3(gx, M), dim3(WG), lds, s, w, x, y, N, K, ldy, ix);
     return hipGetLastError();
 }
 
@@ -351,6 +391,12 @@ hipError_t launch_qmv(const uint8_t* w, const float* x, float* y, int M, int N, 
     constexpr int WGN0 = qmv_wg<F, SPL>(), WGB0 = qmv_wg_big<F, SPL>();
     constexpr int WGN = MODE == QMV_GLU && WGN0 > 512 ? 512 : WGN0;
     constexpr int WGB = MODE == QMV_GLU && WGB0 > 512 ? 512 : WGB0;
+    // short rows (at most 8 of a wavefront step's 16 block slots): 2 or 4 rows per step
+    if constexpr (SPL == 1 && 64 / F::LPB == 16 && MODE != QMV_GLU && MODE != QMV_ATTN) {
+        const int KB = K / F::ELEMS;
+        if (KB <= 4) return launch_qmv_wg<F, 1, WGN, MODE, 4>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        if (KB <= 8) return launch_qmv_wg<F, 1, WGN, MODE, 2>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+    }
     if (WGB != WGN && (size_t)N * (size_t)M <= (size_t)num_cus * (WGB / 64) * 2)
         return launch_qmv_wg<F, SPL, WGB, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
     return launch_qmv_wg<F, SPL, WGN, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
