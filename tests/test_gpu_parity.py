@@ -126,6 +126,27 @@ def test_qmatmul_q8_0_config1(dev):
     assert rel_err(out.numpy(), want) <= TOL
 
 
+@pytest.mark.parametrize("dt", [O.Q4K, O.Q6K])
+@pytest.mark.parametrize("m,n,k", [(1, 1, 512), (1, 2, 256), (1, 6, 768), (2, 5, 1024), (1, 7, 1536), (3, 6, 1792),
+                                   (1, 9, 2048), (4, 2049, 512)])
+def test_qmatmul_short_rows(dev, dt, m, n, k):
+    # rows of at most 8 superblocks go two or four to a wavefront step: row
+    # counts that leave a group part-filled, groups past the last row; the
+    # output starts as NaN so an unwritten row fails (n * k/256 even: the
+    # weights go in as u32 words, and a Q6_K block is 210 bytes)
+    say("qmatmul short rows", dt, m, n, k)
+    wq = weights(dt, n, k)
+    x = acts(m, k)
+    want = O.matmul(dt, x, wq)
+    out = dev.from_numpy(np.full((m, n), np.nan, np.float32))
+    F.qmatmul_f32_rocm_wrapper([dev.from_numpy(x), dev.from_numpy(as_u32(wq))], [out],
+                               F.QMatMulParams(dt, 1, m, n, k))
+    got = out.numpy()
+    assert np.isfinite(got).all()
+    for r in range(m):
+        assert rel_err(got[r], want[r]) <= TOL, r
+
+
 @pytest.mark.parametrize("dt", [O.Q4K, O.Q6K, O.Q8_0])
 def test_qmatmul_batched_small(dev, dt):
     batch, m, n, k = 2, 3, 40, 512
