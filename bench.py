@@ -308,7 +308,7 @@ def moe_leg():
         nbytes = distinct * per_expert + 2 * T * D * 4
         res[f"T{T}"] = {"us_per_layer": round(us, 2), "distinct_experts_mean": distinct,
                         "algorithmic_bytes": int(nbytes), "GB_s": round(nbytes / us / 1e3, 1),
-                        "path": "grouped int8-MFMA" if T * TOPK >= E else "indexed mat-vec"}
+                        "path": "grouped int8-MFMA" if T * TOPK > E else "indexed mat-vec"}
         x.free()
         out.free()
     dev.close()
