@@ -114,7 +114,8 @@ __device__ __forceinline__ float dpp_wave_sum(float v) {
 }
 
 // Sum over each 64/RPW-lane segment of the wavefront (RPW = 2 or 4), in the
-// order dpp_wave_sum adds those lanes; valid in the segment's last lane.
+// order dpp_wave_sum adds those lanes; valid in the segment's last lane (with
+// RPW = 4 in every lane of the 16-lane segment).
 template <int RPW>
 __device__ __forceinline__ float dpp_seg_sum(float v) {
     static_assert(RPW == 2 || RPW == 4, "segments of 32 or 16 lanes");

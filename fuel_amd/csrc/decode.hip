@@ -29,12 +29,11 @@ constexpr int ATT_WG = 256;
 constexpr int GROUPS = ATT_WG / 16;  // positions in flight per workgroup (16 lanes each)
 static_assert(HD == 128 && ATT_WG == 2 * HD, "the rope / append stage maps HD/2 elements to a wave");
 
-// Sum over 16-lane groups (lanes l and l^8, l^4, l^2, l^1).
-__device__ __forceinline__ float group16_sum(float v) {
-#pragma unroll
-    for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-    return v;
-}
+// Sum over 16-lane groups, every lane of a group ending with it: the DPP
+// row steps of dpp_seg_sum (plain VALU operations; measured against four
+// __shfl_xor steps through the LDS crossbar: decode +1%; the prefill
+// attention kernel keeps the shuffles, which measured faster there).
+__device__ __forceinline__ float group16_sum(float v) { return dpp_seg_sum<4>(v); }
 
 // Raw f16 x 8 chunk (one 16-byte load) to floats.
 __device__ __forceinline__ void h8_to_f(const uint4& u, float (&f)[8]) {
