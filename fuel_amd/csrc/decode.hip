@@ -25,9 +25,9 @@ namespace frq {
 namespace {
 
 constexpr int HD = ATTN_HEAD_DIM;
-constexpr int ATT_WG = 256;
+constexpr int ATT_WG = 512;
 constexpr int GROUPS = ATT_WG / 16;  // positions in flight per workgroup (16 lanes each)
-static_assert(HD == 128 && ATT_WG == 2 * HD, "the rope / append stage maps HD/2 elements to a wave");
+static_assert(HD == 128 && ATT_WG >= 2 * HD && ATT_WG % 64 == 0, "the rope / append stage maps HD/2 elements to each of waves 0..3");
 
 // Sum over 16-lane groups, every lane of a group ending with it: the DPP
 // row steps of dpp_seg_sum (plain VALU operations; measured against four
@@ -45,9 +45,11 @@ __device__ __forceinline__ void h8_to_f(const uint4& u, float (&f)[8]) {
     }
 }
 
-// grid = (heads, nsplit), 256 threads.  qk = [q | k] unrotated (heads * HD
-// each), vn = v; caches are [heads][max_ctx][HD] f16.  Split sp of a head
-// takes a contiguous range of at most 16 * ATTN_NIT positions: 16 lanes per
+// grid = (heads, nsplit), ATT_WG = 512 threads (two wavefronts per SIMD at one
+// workgroup per CU; against 256 threads and twice the iterations: decode
+// +0.8%).  qk = [q | k] unrotated (heads * HD each), vn = v; caches are
+// [heads][max_ctx][HD] f16.  Split sp of a head
+// takes a contiguous range of at most 32 * ATTN_NIT positions: 16 lanes per
 // position (8 dims per lane), every K and V load of the range issued before
 // any arithmetic (one memory round trip).  It writes its unnormalized output,
 // max and sum to part[head][sp]; attn_combine_kernel merges the splits (a
@@ -65,10 +67,11 @@ __global__ __launch_bounds__(ATT_WG) void attn_split_kernel(const float* __restr
     const int g = tid >> 4, l16 = tid & 15;
     // 1. the new row's inputs, issued before pos is known: wave 0 rotates q,
     // wave 1 rotates k (elements lane and lane + HD/2), waves 2 and 3 take
-    // v's two halves (one element each; hi repeats lo's address there).
+    // v's two halves (one element each; hi repeats lo's address there);
+    // waves 4.. load wave 2's addresses and append nothing.
     const int w = __builtin_amdgcn_readfirstlane(wave);
     const float* xs = w == 0 ? qk + (size_t)h * HD
-                             : (w == 1 ? qk + (size_t)(H + h) * HD : vn + (size_t)h * HD + (HD / 2) * (w - 2));
+                             : (w == 1 ? qk + (size_t)(H + h) * HD : vn + (size_t)h * HD + (HD / 2) * (w == 3));
     const float x_lo = attn_load_early(xs + lane), x_hi = attn_load_early(xs + (w < 2 ? lane + HD / 2 : lane));
     const int pos = *pos_p;
     if (pos < 0 || pos >= max_ctx) return;  // the combine writes NaN
@@ -99,7 +102,7 @@ __global__ __launch_bounds__(ATT_WG) void attn_split_kernel(const float* __restr
     if (w == 0) {
         s_q[lane] = x_lo * c_lo - x_hi * s_lo;
         s_q[lane + HD / 2] = x_hi * c_hi + x_lo * s_hi;
-    } else if (owner) {
+    } else if (owner && w < 4) {  // (waves 4.. take no part in the append)
         if (w == 1) {
             const __half a = __float2half(x_lo * c_lo - x_hi * s_lo);
             const __half b = __float2half(x_hi * c_hi + x_lo * s_hi);

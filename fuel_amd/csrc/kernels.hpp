@@ -146,8 +146,8 @@ hipError_t launch_normal(float* y, size_t n, unsigned long long seed, uint32_t s
 // (attn_decode_work_bytes), then a combine kernel; and the greedy next-token
 // + embedding step.
 constexpr int ATTN_HEAD_DIM = 128;
-constexpr int ATTN_NIT = 8;                     // positions per 16-lane group and split
-constexpr int ATTN_MAX_CHUNK = 16 * ATTN_NIT;   // positions per split (256-thread workgroups)
+constexpr int ATTN_NIT = 4;                     // positions per 16-lane group and split
+constexpr int ATTN_MAX_CHUNK = 32 * ATTN_NIT;   // positions per split (512-thread workgroups)
 constexpr int ATTN_PSTRIDE = ATTN_HEAD_DIM + 4; // floats per (head, split) partial: o, max, sum, 2 pad (16-byte rows)
 constexpr int ATTN_MERGE_CHUNK = 8;             // splits merged per step
 int attn_decode_splits(int n_heads, int max_ctx);
