@@ -12,7 +12,7 @@ With --leg decode / batched / moe it instead runs one --kernel-trace --stats
 pass over that bench.py leg (config 4 decode + batched prompt, config 3
 M = 32/128/512 matmuls, config 5 MoE layer) and writes the per-kernel summary.
 
-Usage: python bench_profile.py [--shape 4096x32000] [--leg matvec|decode|batched|moe] [--out gpurun_out/profiles]
+Usage: python bench_profile.py [--shape 4096x32000] [--leg matvec|decode|batched|moe] [--out DIR]
 """
 from __future__ import annotations
 
