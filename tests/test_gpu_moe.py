@@ -151,7 +151,9 @@ def device_experts(dev, dt, e, rows, cols, seed, stream):
 
 @pytest.mark.parametrize("t,d,ffn,e,k,dt", [
     (1, 2048, 768, 128, 8, O.Q4K),        # Qwen3-MoE-style expert layer, decode
-    (16, 2048, 768, 128, 8, O.Q4K),
+    (16, 2048, 768, 128, 8, O.Q4K),       # one routed entry per expert: the indexed mat-vec
+    (17, 2048, 768, 128, 8, O.Q4K),       # just above it: the grouped int8-MFMA tiles
+    (3, 256, 512, 6, 2, O.Q4K),           # entries == experts on a small layer
     (512, 2048, 768, 128, 8, O.Q4K),
     (5, 256, 512, 6, 2, O.Q4K),
     (9, 512, 256, 10, 3, O.Q6K),
