@@ -284,6 +284,22 @@ def test_device_quantize_bit_exact(dev, dt):
     assert got.tobytes() == want.tobytes(), f"first differing blocks {np.unique(bad[0])[:8]}"
 
 
+def test_device_quantize_known_answers(dev):
+    """The hand-derived known-answer blocks of weight_kat.py (grid-exact
+    sub-blocks, clamps, ties, saturation, zero blocks) through the device
+    from_float, byte for byte against the hand results."""
+    from weight_kat import CASES
+
+    for dt in (O.Q4K, O.Q6K):
+        names = [n for n in sorted(CASES) if CASES[n][0] == dt]
+        say("device from_float known answers", names)
+        xs, ws = zip(*(CASES[n][1]() for n in names))
+        x = np.concatenate(xs)[None]
+        q = dev.qzeros(x.size, dt)
+        q.quantize(dev.from_numpy(x))
+        assert q.data() == np.concatenate(ws).tobytes()
+
+
 def test_random_bits_bit_exact(dev):
     seed, base, stream = 0xDEADBEEF12345678, 3, 9
     got = F.fill_random_bits(dev, 1001, 7, seed, base, stream).numpy()

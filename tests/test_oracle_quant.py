@@ -8,10 +8,8 @@ known values (to_float), the two scale-unpack routines agreeing on random
 bytes, the all-ones Q6K case of fuel-dispatch/src/pipelined.rs:10073-10139
 worked out by hand, and from_float -> to_float error bounds.
 
-Parity unpinned: the exact bytes BlockQ4K::from_float / BlockQ6K::from_float
-produce for general inputs (iterative float searches in utils.rs
-make_qkx1_quants / make_qx_quants) have no golden vector in the reference and
-the Rust cannot be built here; only the invariants below hold them.
+The exact bytes of BlockQ4K::from_float / BlockQ6K::from_float are pinned
+by the hand-derived known-answer blocks of test_oracle_quant_kat.py.
 """
 import numpy as np
 
