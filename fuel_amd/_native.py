@@ -45,6 +45,7 @@ SIGNATURES = {
     "frq_device_set_stream": (_i32, [_vp, _vp]),
     "frq_sync": (_i32, [_vp]),
     "frq_device_cu_count": (_i32, [_vp, C.POINTER(C.c_int)]),
+    "frq_device_workspace_bytes": (_i32, [_vp, C.POINTER(_sz)]),
     "frq_malloc": (_i32, [_vp, _sz, C.POINTER(_vp)]),
     "frq_free": (_i32, [_vp, _vp]),
     "frq_memcpy_htod": (_i32, [_vp, _vp, _vp, _sz]),
@@ -79,7 +80,7 @@ SIGNATURES = {
                                     _vp]),
     "frq_attention_decode_oproj": (_i32, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_float, _vp,
                                           _sz, _i32, _vp, _sz, _vp]),
-    "frq_argmax_embed": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _vp, _vp]),
+    "frq_argmax_embed": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _vp, _vp]),
     "frq_rms_norm_rows": (_i32, [_vp, _sz, _sz, _vp, _sz, _vp, C.c_float, _vp, _sz]),
     "frq_rope_append_rows": (_i32, [_vp, _sz, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _vp, _sz, _vp, _vp]),
     "frq_attention_prefill": (_i32, [_vp, _sz, _sz, _sz, _sz, _vp, _sz, _vp, _vp, _sz, C.c_float, _vp, _sz]),

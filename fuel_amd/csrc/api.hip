@@ -172,16 +172,16 @@ int run_qmatmul(frq_device* dev, int t, const uint8_t* w, const float* x, size_t
     const bool w32 = n * (k / block_elems(t)) * type_size(t) <= 0xffffffffull;
     if (rows >= MMQ_MIN_ROWS && mmq_supported(t) && w32) {
         // many activation rows: quantize them once, then the int8-MFMA GEMM
-        // workspace: quantized rows, then the split-K partial sums
+        // workspace: quantized rows, then the split-K partial sums the plan needs
+        const MmqPlan plan = mmq_plan(t, w, (int)rows, (int)n, (int)k, dev->num_cus);
         const size_t abytes = align256(act_bytes(vec_dot_type(t), rows, k));
-        const size_t pelems = mmq_partial_elems((int)rows, (int)n, dev->num_cus);
-        int rc = ensure_ws(dev, abytes + pelems * sizeof(float));
+        int rc = ensure_ws(dev, abytes + plan.part_elems * sizeof(float));
         if (rc) return rc;
         ActView act;
         rc = quantize_rows(dev, vec_dot_type(t), x, rows, k, nullptr, &act);
         if (rc) return rc;
-        float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(dev->ws) + abytes);
-        HIP_TRY(launch_mmq(t, w, act, y, part, pelems, (int)rows, (int)n, (int)k, (int)n, dev->num_cus, dev->stream));
+        float* part = plan.part_elems ? reinterpret_cast<float*>(static_cast<uint8_t*>(dev->ws) + abytes) : nullptr;
+        HIP_TRY(launch_mmq(plan, t, w, act, y, part, (int)rows, (int)n, (int)k, (int)n, dev->stream));
         return FRQ_OK;
     }
     HIP_TRY(launch_qmv(t, w, x, y, (int)rows, (int)n, (int)k, (int)n, dev->stream, dev->num_cus));
@@ -200,15 +200,15 @@ int run_qmatmul_f16(frq_device* dev, int t, const uint8_t* w, const uint16_t* x,
     if (k > kmax) return fail(FRQ_UNSUPPORTED, "qmatmul_f16: k=%zu exceeds %zu for dtype %d", k, kmax, t);
     const bool w32 = n * (k / block_elems(t)) * type_size(t) <= 0xffffffffull;
     if (rows >= MMQ_MIN_ROWS && mmq_supported(t) && w32) {
+        const MmqPlan plan = mmq_plan(t, w, (int)rows, (int)n, (int)k, dev->num_cus);
         const size_t abytes = align256(act_bytes(GGML_Q8K, rows, k));
-        const size_t pelems = mmq_partial_elems((int)rows, (int)n, dev->num_cus);
-        int rc = ensure_ws(dev, abytes + pelems * sizeof(float));
+        int rc = ensure_ws(dev, abytes + plan.part_elems * sizeof(float));
         if (rc) return rc;
         const ActView act = act_view(dev->ws, GGML_Q8K, rows, k);
         HIP_TRY(launch_quantize_q8k_h(x, (int)rows, (int)k, act, dev->stream));
-        float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(dev->ws) + abytes);
-        HIP_TRY(launch_mmq(t, w, act, reinterpret_cast<float*>(y), part, pelems, (int)rows, (int)n, (int)k, (int)n,
-                           dev->num_cus, dev->stream, true));
+        float* part = plan.part_elems ? reinterpret_cast<float*>(static_cast<uint8_t*>(dev->ws) + abytes) : nullptr;
+        HIP_TRY(launch_mmq(plan, t, w, act, reinterpret_cast<float*>(y), part, (int)rows, (int)n, (int)k, (int)n,
+                           dev->stream, true));
         return FRQ_OK;
     }
     HIP_TRY(launch_qmv_half(t, w, x, y, (int)rows, (int)n, (int)k, (int)n, dev->stream, dev->num_cus));
@@ -341,6 +341,12 @@ int frq_sync(frq_device* dev) {
 int frq_device_cu_count(const frq_device* dev, int* cus) {
     if (!dev || !cus) return fail(FRQ_INVALID, "null argument");
     *cus = dev->num_cus;
+    return FRQ_OK;
+}
+
+int frq_device_workspace_bytes(const frq_device* dev, size_t* bytes) {
+    if (!dev || !bytes) return fail(FRQ_INVALID, "null argument");
+    *bytes = dev->ws_bytes;
     return FRQ_OK;
 }
 
@@ -1026,15 +1032,15 @@ int frq_gather_rows(frq_device* dev, const float* table, size_t rows, size_t dim
 }
 
 int frq_argmax_embed(frq_device* dev, const float* logits, size_t vocab, const float* table, size_t dim, int32_t* tokens,
-                     size_t tokens_cap, size_t prompt_len, int32_t* pos, float* x) {
+                     size_t tokens_cap, const int32_t* prompt_len, int32_t* pos, float* x) {
     int rc = use_device(dev);
     if (rc) return rc;
     if (vocab == 0 || vocab > (size_t)0x7fffffff || dim == 0 || dim % 4 || tokens_cap > (size_t)0x7fffffff)
         return fail(FRQ_INVALID, "argmax_embed: vocab=%zu dim=%zu", vocab, dim);
-    if (!logits || !table || !tokens || !pos || !x) return fail(FRQ_INVALID, "argmax_embed: null buffer");
+    if (!logits || !table || !tokens || !prompt_len || !pos || !x) return fail(FRQ_INVALID, "argmax_embed: null buffer");
     if (!aligned16(table) || !aligned16(x)) return fail(FRQ_MISALIGNED, "argmax_embed: table / x not 16-byte aligned");
-    const int pl = prompt_len > tokens_cap ? (int)tokens_cap : (int)prompt_len;
-    HIP_TRY(launch_argmax_embed(logits, (int)vocab, table, (int)dim, tokens, (int)tokens_cap, pl, pos, x, dev->stream));
+    HIP_TRY(launch_argmax_embed(logits, (int)vocab, table, (int)dim, tokens, (int)tokens_cap, prompt_len, pos, x,
+                                dev->stream));
     return FRQ_OK;
 }
 

@@ -230,7 +230,7 @@ constexpr int AM_WG = 1024;
 
 __global__ __launch_bounds__(AM_WG) void argmax_embed_kernel(const float* __restrict__ logits, int vocab,
                                                             const float* __restrict__ table, int dim, int* tokens,
-                                                            int tokens_cap, int prompt_len, int* pos_p,
+                                                            int tokens_cap, const int* prompt_len_p, int* pos_p,
                                                             float* __restrict__ x) {
     __shared__ float s_v[AM_WG / 64];
     __shared__ int s_i[AM_WG / 64];
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(AM_WG) void argmax_embed_kernel(const float* __rest
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pos = *pos_p;
     const int nxt = pos + 1;
-    const bool forced = nxt < prompt_len && nxt < tokens_cap;
+    const bool forced = nxt < *prompt_len_p && nxt < tokens_cap;
     int tok;
     if (forced) {
         tok = tokens[nxt];
@@ -309,7 +309,7 @@ hipError_t launch_attn_decode(const float* qk, const float* v, const float* rcos
 }
 
 hipError_t launch_argmax_embed(const float* logits, int vocab, const float* table, int dim, int* tokens,
-                               int tokens_cap, int prompt_len, int* pos, float* x, hipStream_t s) {
+                               int tokens_cap, const int* prompt_len, int* pos, float* x, hipStream_t s) {
     hipLaunchKernelGGL(argmax_embed_kernel, dim3(1), dim3(AM_WG), 0, s, logits, vocab, table, dim, tokens, tokens_cap,
                        prompt_len, pos, x);
     return hipGetLastError();

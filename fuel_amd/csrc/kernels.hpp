@@ -100,12 +100,19 @@ hipError_t launch_moe_combine(const float* yd, const int* ids, const float* w, c
                               int d, float* out, hipStream_t s);
 // mmq.hip: int8-MFMA matmul for M >= 16 over activations already quantized
 // into the workspace (quantize_q8k), y [M, N] with row stride ldy.
-// `part` (part_elems floats, may be null) holds split-K partial sums.  With
-// y_half set, y holds f16 outputs (round to nearest even of the f32 sums).
+// mmq_plan picks the kernel (tile shape; the LDS-DMA staging only for 16-byte
+// aligned Q4_K blocks) and the K split on the host; part_elems is the number
+// of f32 split-K partial sums launch_mmq needs in `part` (0 without a split).
+// With y_half set, y holds f16 outputs (round to nearest even of the f32 sums).
 bool mmq_supported(int dtype);
-size_t mmq_partial_elems(int M, int N, int num_cus);
-hipError_t launch_mmq(int dtype, const uint8_t* w, ActView act, float* y, float* part, size_t part_elems, int M,
-                      int N, int K, int ldy, int num_cus, hipStream_t s, bool y_half = false);
+struct MmqPlan {
+    int kind;           // kernel instantiation
+    int ks;             // K splits (1: none)
+    size_t part_elems;  // split partial sums: ks * M * N, or 0
+};
+MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus);
+hipError_t launch_mmq(const MmqPlan& plan, int dtype, const uint8_t* w, ActView act, float* y, float* part, int M,
+                      int N, int K, int ldy, hipStream_t s, bool y_half = false);
 
 // Grouped (MoE) int8-MFMA matmul: workgroup x takes tile x of the tile table
 // (rows [tile_row0, expert end) of one expert, up to bm of them); its weights
@@ -161,7 +168,7 @@ hipError_t launch_attn_split(const float* qk, const float* v, const float* rcos,
                              uint16_t* vc, int n_heads, int max_ctx, const int* pos, float scale, float* part,
                              hipStream_t s);
 hipError_t launch_argmax_embed(const float* logits, int vocab, const float* table, int dim, int* tokens,
-                               int tokens_cap, int prompt_len, int* pos, float* x, hipStream_t s);
+                               int tokens_cap, const int* prompt_len, int* pos, float* x, hipStream_t s);
 
 // prefill.hip: row kernels of a batched prompt pass (M tokens at positions
 // pos0 .. pos0 + M - 1) between the int8-MFMA projections.

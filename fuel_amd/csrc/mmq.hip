@@ -609,67 +609,56 @@ __global__ void mmq_reduce_kernel(const float* __restrict__ part, float* __restr
     else y[o] = s;
 }
 
-template <class F, int RT, int CT, int WM, int WN>
-hipError_t launch_cfg(const uint8_t* w, ActView act, float* y, float* part, size_t part_elems, int M, int N, int K,
-                      int ldy, int num_cus, hipStream_t s, bool y_half) {
-    using T = MmqTile<F, RT, CT, WM, WN>;
-    const int mt = (M + T::BM - 1) / T::BM, nt = (N + T::BN - 1) / T::BN;
-    const int KB = K / QK_K;
-    // Split K when the tile grid leaves resident workgroup slots empty, as
-    // far as one round of the grid still fits them (a partial second round
-    // costs more than the split saves), keeping >= 2 superblocks per split.
-    static int occ = -1;  // resident workgroups per CU of this instantiation
+// Resident workgroups per CU of a kernel instantiation (cached per instantiation).
+template <class Kern>
+int kernel_occupancy(Kern kern, int threads) {
+    static int occ = -1;
     if (occ < 0) {
         int o = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, mmq_kernel<F, RT, CT, WM, WN, false>, T::NT, 0) !=
-                hipSuccess ||
-            o < 1)
-            o = 1;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, kern, threads, 0) != hipSuccess || o < 1) o = 1;
         occ = o;
     }
-    int ks = 1;
-    const int tiles = mt * nt, cap = occ * num_cus;
-    if (part && tiles < cap) {
-        ks = cap / tiles;
-        const int kmax = KB / 2 > 1 ? KB / 2 : 1;
-        if (ks > kmax) ks = kmax;
-        while (ks > 1 && (size_t)ks * M * N > part_elems) ks--;
-    }
-    hipLaunchKernelGGL((mmq_kernel<F, RT, CT, WM, WN, false>), dim3(mt * nt * ks), dim3(T::NT), 0, s, w, act,
-                       ks > 1 ? part : y, M, N, K, ldy, mt, nt, ks, (int)y_half, MmqGroup{});
-    if (ks > 1) {
-        const size_t total = (size_t)M * N;
-        hipLaunchKernelGGL(mmq_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, y, M, N,
-                           ldy, ks, (int)y_half);
-    }
-    return hipGetLastError();
+    return occ;
 }
 
-template <class F, int RT, int CT, int WM, int WN>
-hipError_t launch_dma_cfg(const uint8_t* w, ActView act, float* y, float* part, size_t part_elems, int M, int N,
-                          int K, int ldy, int num_cus, hipStream_t s, bool y_half) {
-    using T = DmaTile<F, RT, CT, WM, WN>;
-    const int mt = (M + T::BM - 1) / T::BM, nt = (N + T::BN - 1) / T::BN;
-    const int KB = K / QK_K;
-    static int occ = -1;  // resident workgroups per CU of this instantiation
-    if (occ < 0) {
-        int o = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, mmq_dma_kernel<F, RT, CT, WM, WN, false>, T::NT, 0) !=
-                hipSuccess ||
-            o < 1)
-            o = 1;
-        occ = o;
-    }
-    int ks = 1;
-    const int tiles = mt * nt, cap = occ * num_cus;
-    if (part && tiles < cap) {  // K split as in launch_cfg
-        ks = cap / tiles;
-        const int kmax = KB / 2 > 1 ? KB / 2 : 1;
-        if (ks > kmax) ks = kmax;
-        while (ks > 1 && (size_t)ks * M * N > part_elems) ks--;
-    }
-    hipLaunchKernelGGL((mmq_dma_kernel<F, RT, CT, WM, WN, false>), dim3(mt * nt * ks), dim3(T::NT), 0, s, w, act,
-                       ks > 1 ? part : y, M, N, K, ldy, mt, nt, ks, (int)y_half, MmqGroup{});
+// K splits for a grid of `tiles` workgroups: split when the tiles leave
+// resident workgroup slots empty, as far as one round of the grid still fits
+// them (a partial second round costs more than the split saves), keeping >= 2
+// superblocks per split and at most 16 splits.
+int mmq_ksplit(int tiles, int occ, int num_cus, int KB) {
+    const int cap = occ * num_cus;
+    if (tiles >= cap) return 1;
+    int ks = cap / tiles;
+    const int kmax = KB / 2 > 1 ? KB / 2 : 1;
+    if (ks > kmax) ks = kmax;
+    return ks > 16 ? 16 : ks;
+}
+
+template <class F, int RT, int CT, int WM, int WN, bool DMA>
+void plan_cfg(int M, int N, int K, int num_cus, MmqPlan& p) {
+    constexpr int NT = 64 * WM * WN, BM = 16 * RT * WM, BN = 16 * CT * WN;
+    const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
+    int occ;
+    if constexpr (DMA) occ = kernel_occupancy(mmq_dma_kernel<F, RT, CT, WM, WN, false>, NT);
+    else occ = kernel_occupancy(mmq_kernel<F, RT, CT, WM, WN, false>, NT);
+    p.ks = mmq_ksplit(mt * nt, occ, num_cus, K / QK_K);
+    p.part_elems = p.ks > 1 ? (size_t)p.ks * M * N : 0;
+}
+
+template <class F, int RT, int CT, int WM, int WN, bool DMA>
+hipError_t launch_cfg(const MmqPlan& p, const uint8_t* w, ActView act, float* y, float* part, int M, int N, int K,
+                      int ldy, hipStream_t s, bool y_half) {
+    constexpr int NT = 64 * WM * WN, BM = 16 * RT * WM, BN = 16 * CT * WN;
+    const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
+    const int ks = p.ks;
+    if (ks > 1 && !part) return hipErrorInvalidValue;
+    float* out = ks > 1 ? part : y;
+    if constexpr (DMA)
+        hipLaunchKernelGGL((mmq_dma_kernel<F, RT, CT, WM, WN, false>), dim3(mt * nt * ks), dim3(NT), 0, s, w, act, out,
+                           M, N, K, ldy, mt, nt, ks, (int)y_half, MmqGroup{});
+    else
+        hipLaunchKernelGGL((mmq_kernel<F, RT, CT, WM, WN, false>), dim3(mt * nt * ks), dim3(NT), 0, s, w, act, out, M,
+                           N, K, ldy, mt, nt, ks, (int)y_half, MmqGroup{});
     if (ks > 1) {
         const size_t total = (size_t)M * N;
         hipLaunchKernelGGL(mmq_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, y, M, N,
@@ -696,15 +685,62 @@ hipError_t launch_grouped_fmt(const uint8_t* w, ActView act, float* y, int bm, i
     return hipErrorInvalidValue;
 }
 
-template <class F>
-hipError_t launch_fmt(const uint8_t* w, ActView act, float* y, float* part, size_t part_elems, int M, int N, int K,
-                      int ldy, int num_cus, hipStream_t s, bool yh) {
-    if (M >= 128) return launch_cfg<F, 4, 1, 2, 4>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s, yh);  // 128 x 64, 8 waves
-    if (M >= 64) return launch_cfg<F, 2, 2, 2, 2>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s, yh);   // 64 x 64
-    return launch_cfg<F, 2, 1, 1, 4>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s, yh);                // 32 x 64
-}
+// Kernel instantiations, by MmqPlan::kind.
+enum MmqKind {
+    MMQ_Q4K_32 = 0,   // register-staged 32 x 64
+    MMQ_Q4K_64,       // register-staged 64 x 64
+    MMQ_Q4K_128,      // register-staged 128 x 64, 8 waves
+    MMQ_Q4K_DMA_64,   // LDS-DMA 64 x 64 (16-byte aligned blocks)
+    MMQ_Q4K_DMA_128,  // LDS-DMA 128 x 64
+    MMQ_Q6K_32,
+    MMQ_Q6K_64,
+    MMQ_Q6K_128,
+};
+
+#define FRQ_MMQ_KINDS(X)                          \
+    X(MMQ_Q4K_32, MmqQ4K, 2, 1, 1, 4, false)      \
+    X(MMQ_Q4K_64, MmqQ4K, 2, 2, 2, 2, false)      \
+    X(MMQ_Q4K_128, MmqQ4K, 4, 1, 2, 4, false)     \
+    X(MMQ_Q4K_DMA_64, MmqQ4K, 2, 2, 2, 2, true)   \
+    X(MMQ_Q4K_DMA_128, MmqQ4K, 4, 1, 2, 4, true)  \
+    X(MMQ_Q6K_32, MmqQ6K, 2, 1, 1, 4, false)      \
+    X(MMQ_Q6K_64, MmqQ6K, 2, 2, 2, 2, false)      \
+    X(MMQ_Q6K_128, MmqQ6K, 4, 1, 2, 4, false)
 
 }  // namespace
+
+bool mmq_supported(int dtype) { return dtype == GGML_Q4K || dtype == GGML_Q6K; }
+
+MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus) {
+    MmqPlan p{};
+    // 144-byte Q4_K blocks at a 16-byte aligned base allow the LDS DMA staging
+    // (16-byte global_load_lds); it wins from M = 64 on (M = 512: 4-7%), the
+    // register-staged kernel below that
+    const bool dma = dtype == GGML_Q4K && ((uintptr_t)w & 15u) == 0;
+    const int base = dtype == GGML_Q4K ? MMQ_Q4K_32 : MMQ_Q6K_32;
+    p.kind = M >= 128 ? base + 2 : M >= 64 ? base + 1 : base;
+    if (dma && M >= 64) p.kind = M >= 128 ? MMQ_Q4K_DMA_128 : MMQ_Q4K_DMA_64;
+    switch (p.kind) {
+#define FRQ_PLAN(kind, F, RT, CT, WM, WN, DMA) \
+    case kind: plan_cfg<F, RT, CT, WM, WN, DMA>(M, N, K, num_cus, p); break;
+        FRQ_MMQ_KINDS(FRQ_PLAN)
+#undef FRQ_PLAN
+        default: break;
+    }
+    return p;
+}
+
+hipError_t launch_mmq(const MmqPlan& plan, int dtype, const uint8_t* w, ActView act, float* y, float* part, int M,
+                      int N, int K, int ldy, hipStream_t s, bool y_half) {
+    if (!mmq_supported(dtype)) return hipErrorInvalidValue;
+    switch (plan.kind) {
+#define FRQ_LAUNCH(kind, F, RT, CT, WM, WN, DMA) \
+    case kind: return launch_cfg<F, RT, CT, WM, WN, DMA>(plan, w, act, y, part, M, N, K, ldy, s, y_half);
+        FRQ_MMQ_KINDS(FRQ_LAUNCH)
+#undef FRQ_LAUNCH
+        default: return hipErrorInvalidValue;
+    }
+}
 
 int mmq_group_rows(int rows_per_expert) { return rows_per_expert >= 24 ? 32 : 16; }
 
@@ -716,29 +752,6 @@ hipError_t launch_mmq_grouped(int dtype, const uint8_t* w, ActView act, float* y
     // MoE layer's short K loops)
     if (dtype == GGML_Q4K) return launch_grouped_fmt<MmqQ4K>(w, act, y, bm, max_tiles, N, K, ldy, g, s);
     return launch_grouped_fmt<MmqQ6K>(w, act, y, bm, max_tiles, N, K, ldy, g, s);
-}
-
-bool mmq_supported(int dtype) { return dtype == GGML_Q4K || dtype == GGML_Q6K; }
-
-size_t mmq_partial_elems(int M, int N, int num_cus) {
-    // split partials for up to 16 K splits (launch_cfg steps its split down to what fits)
-    (void)num_cus;
-    return (size_t)M * N * 16;
-}
-
-hipError_t launch_mmq(int dtype, const uint8_t* w, ActView act, float* y, float* part, size_t part_elems, int M,
-                      int N, int K, int ldy, int num_cus, hipStream_t s, bool y_half) {
-    if (dtype == GGML_Q4K) {
-        // 144-byte blocks allow the LDS DMA staging; it wins from M = 64 on
-        // (M = 512: 4-7%), the register-staged kernel at M < 64
-        if (M >= 128)
-            return launch_dma_cfg<MmqQ4K, 4, 1, 2, 4>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s, y_half);
-        if (M >= 64)
-            return launch_dma_cfg<MmqQ4K, 2, 2, 2, 2>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s, y_half);
-        return launch_fmt<MmqQ4K>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s, y_half);
-    }
-    if (dtype == GGML_Q6K) return launch_fmt<MmqQ6K>(w, act, y, part, part_elems, M, N, K, ldy, num_cus, s, y_half);
-    return hipErrorInvalidValue;
 }
 
 }  // namespace frq

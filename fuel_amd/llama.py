@@ -153,6 +153,7 @@ class LlamaDecoder:
         self.logits = dev.alloc((cfg.vocab,), np.float32)
         self.tokens = dev.alloc((Cx,), np.int32)
         self.pos = dev.alloc((1,), np.int32)
+        self.plen = dev.from_numpy(np.zeros(1, np.int32))  # the prompt length, read by the captured step
         self.work_bytes = int(L.frq_attention_decode_workspace(H, Cx))
         self.work = _Buf(dev, self.work_bytes)
         check(L.frq_memset(dev.handle, C.c_void_p(self.work.ptr), 0, self.work_bytes))
@@ -335,6 +336,7 @@ class LlamaDecoder:
         self.tokens.copy_from(toks)
         self.pos.copy_from(np.zeros(1, np.int32))
         self.prompt_len = int(prompt.size)
+        self.plen.copy_from(np.array([self.prompt_len], np.int32))
         d = cfg.dim
         check(self.L.frq_memcpy_dtod(self.dev.handle, C.c_void_p(self.x.ptr),
                                      C.c_void_p(self.embed.ptr + int(prompt[0]) * d * 4), d * 4))
@@ -382,7 +384,7 @@ class LlamaDecoder:
         check(L.frq_qmatmul_fused(h, self.dt_out, 1, cfg.vocab, d, vp(self.wout.ptr), x, d, None,
                                   vp(self.final_gain.ptr), eps, 0, vp(self.logits.ptr), cfg.vocab))
         check(L.frq_argmax_embed(h, vp(self.logits.ptr), cfg.vocab, vp(self.embed.ptr), d, vp(self.tokens.ptr),
-                                 cfg.max_ctx, self.prompt_len, vp(self.pos.ptr), x))
+                                 cfg.max_ctx, vp(self.plen.ptr), vp(self.pos.ptr), x))
 
     def prefill(self, prompt) -> None:
         """The prompt as one batch (lazy.rs:7363-7446 at seq = M): every layer
@@ -421,7 +423,7 @@ class LlamaDecoder:
                                   None, vp(self.final_gain.ptr), eps, 0, vp(self.logits.ptr), cfg.vocab))
         self.pos.copy_from(np.array([M - 1], np.int32))
         check(L.frq_argmax_embed(h, vp(self.logits.ptr), cfg.vocab, vp(self.embed.ptr), d, vp(self.tokens.ptr),
-                                 cfg.max_ctx, self.prompt_len, vp(self.pos.ptr), vp(self.x.ptr)))
+                                 cfg.max_ctx, vp(self.plen.ptr), vp(self.pos.ptr), vp(self.x.ptr)))
 
     def _mm(self, dt, w, n, k, x_ptr, y_ptr, M) -> None:
         """y [M, n] = x [M, k] . W^T through the QMatMul KernelRef seam."""

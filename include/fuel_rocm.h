@@ -71,6 +71,10 @@ int frq_device_close(frq_device *dev);
 int frq_device_set_stream(frq_device *dev, void *hip_stream);
 int frq_sync(frq_device *dev);
 int frq_device_cu_count(const frq_device *dev, int *cus);
+/* Bytes of device workspace the handle holds (quantized activation rows,
+ * split-K partial sums, MoE routing scratch), grown on demand by the calls
+ * that need it and released by frq_device_close.  Introspection only. */
+int frq_device_workspace_bytes(const frq_device *dev, size_t *bytes);
 
 /* Device memory helpers standing in for DynBackendStorage buffers. */
 int frq_malloc(frq_device *dev, size_t bytes, void **dptr);
@@ -274,12 +278,14 @@ int frq_add(frq_device *dev, size_t n, const float *x_dev, float *y_dev);
 int frq_gather_rows(frq_device *dev, const float *table_dev, size_t rows, size_t dim, const int32_t *ids_dev,
                     size_t m, float *out_dev);
 /* Greedy next token and its embedding: next = tokens[pos + 1] while
- * pos + 1 < prompt_len, else the first-index argmax of logits [vocab]
+ * pos + 1 < *prompt_len_dev, else the first-index argmax of logits [vocab]
  * (argmax_dim_f32, byte_kernels.rs:8246-8261), stored at tokens[pos + 1]
  * (when pos + 1 < tokens_cap); x = table[next] ([vocab, dim] f32, dim % 4 == 0);
- * *pos_dev += 1.  Asynchronous, capturable. */
+ * *pos_dev += 1.  The prompt length is read on the device, like the position,
+ * so one captured step serves every prompt.  Asynchronous, capturable. */
 int frq_argmax_embed(frq_device *dev, const float *logits_dev, size_t vocab, const float *table_dev, size_t dim,
-                     int32_t *tokens_dev, size_t tokens_cap, size_t prompt_len, int32_t *pos_dev, float *x_dev);
+                     int32_t *tokens_dev, size_t tokens_cap, const int32_t *prompt_len_dev, int32_t *pos_dev,
+                     float *x_dev);
 
 /* ---- integer taps (build-internal parity probes; no reference counterpart) ----
  * Quantize rows of f32 activations into fuel's activation blocks

@@ -286,9 +286,12 @@ def test_argmax_embed(dev):
     pos = dev.from_numpy(np.array([0], np.int32))
     x = dev.alloc((dim,), np.float32)
 
+    plen = dev.alloc((1,), np.int32)
+
     def step(prompt_len):
+        plen.copy_from(np.array([prompt_len], np.int32))
         F._native.check(L().frq_argmax_embed(dev.handle, C.c_void_p(ld.ptr), vocab, C.c_void_p(td.ptr), dim,
-                                             C.c_void_p(toks.ptr), cap, prompt_len, C.c_void_p(pos.ptr),
+                                             C.c_void_p(toks.ptr), cap, C.c_void_p(plen.ptr), C.c_void_p(pos.ptr),
                                              C.c_void_p(x.ptr)))
 
     step(3)   # pos 0 -> forced prompt token 9
@@ -387,6 +390,37 @@ def test_decoder_greedy_graph_replay(dev, small_decoder):
             assert gap <= DEC_TOL, (p, chosen, best, gap)
             exact += chosen == best
     assert exact >= (n_steps - len(prompt) + 1) // 2
+
+
+def test_decoder_graph_replays_another_prompt_length(dev, small_decoder):
+    """The prompt length lives in device memory: a step captured while one
+    prompt was loaded forces the tokens of a later, longer or shorter prompt
+    exactly as the eager steps do."""
+    say("decoder graph replay, other prompt lengths")
+    dec = small_decoder
+    hip = HipRuntime()
+    s = hip.stream_create()
+    dev.set_stream(s)
+    try:
+        dec.start([1, 2, 3])
+        hip.stream_sync(s)
+        g = hip.capture(s, dec.enqueue_step)
+        for prompt in ([9, 8, 7, 6, 5, 4, 3], [42]):
+            n_steps = 12
+            dec.start(prompt)
+            for _ in range(n_steps):
+                dec.enqueue_step()
+            eager = dec.tokens_host()[:n_steps + 1].copy()
+            dec.start(prompt)
+            for _ in range(n_steps):
+                hip.graph_launch(g, s)
+            hip.stream_sync(s)
+            replay = dec.tokens_host()[:n_steps + 1].copy()
+            assert replay[:len(prompt)].tolist() == prompt
+            np.testing.assert_array_equal(replay, eager)
+        hip.graph_destroy(g)
+    finally:
+        dev.set_stream(None)
 
 
 def test_decoder_fused_oproj_matches_unfused(dev, small_decoder):

@@ -333,15 +333,70 @@ def test_qmatmul_mfma_rows(dev, dt, m):
 
 @pytest.mark.parametrize("dt", [O.Q4K, O.Q6K])
 @pytest.mark.parametrize("k,n", SHAPES_7B)
-def test_qmatmul_mfma_m32_7b_shapes(dev, dt, k, n):
-    say("mfma m=32", dt, k, n)
+@pytest.mark.parametrize("m", [32, 128, 512])
+def test_qmatmul_mfma_7b_shapes(dev, dt, k, n, m):
+    """M = 32 / 128 / 512 rows at the four 7B shapes (the
+    43-superblock rows of K = 11008, split K, the 128 x 64 tiles, the LDS-DMA
+    staging), against the oracle."""
+    say("mfma", dt, "m", m, k, n)
     wq = weights(dt, n, k)
-    x = acts(32, k)
+    x = acts(m, k)
     want = O.matmul(dt, x, wq)
-    out = dev.alloc((32, n), np.float32)
+    out = dev.alloc((m, n), np.float32)
     F.qmatmul_f32_rocm_wrapper([dev.from_numpy(x), dev.from_numpy(as_u32(wq))], [out],
-                               F.QMatMulParams(dt, 1, 32, n, k))
-    assert rel_err(out.numpy(), want) <= TOL
+                               F.QMatMulParams(dt, 1, m, n, k))
+    err = rel_err(out.numpy(), want)
+    say("  rel_err", err)
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("m", [64, 128])
+def test_qmatmul_q4k_weights_off_16_byte_alignment(dev, m):
+    """Q4_K blocks at a 4-byte (not 16-byte) aligned address, as a KernelRef
+    input slice may be: the LDS-DMA staging needs 16-byte aligned blocks, so
+    the plan takes the register-staged kernel; same results."""
+    k, n = 2048, 320
+    wq = weights(O.Q4K, n, k)
+    x = acts(m, k)
+    want = O.matmul(O.Q4K, x, wq)
+    raw = as_u32(wq)
+    buf = dev.from_numpy(np.concatenate([np.zeros(1, np.uint32), raw]))
+    import ctypes as C
+    from fuel_amd._native import check, lib
+    xd = dev.from_numpy(x)
+    out = dev.alloc((m, n), np.float32)
+    check(lib().frq_qmatmul(dev.handle, O.Q4K, 1, m, n, k, C.c_void_p(xd.ptr), x.nbytes, C.c_void_p(buf.ptr + 4),
+                            raw.nbytes, C.c_void_p(out.ptr), out.nbytes))
+    err = rel_err(out.numpy(), want)
+    say("  misaligned q4k m", m, "rel_err", err)
+    assert err <= TOL
+
+
+def test_qmatmul_workspace_holds_only_the_split_it_uses():
+    """A QMatMul whose tiles fill the GPU runs unsplit and sizes its workspace
+    for the quantized rows alone (no split-K partials): M = 1024 rows,
+    N = 32000, K = 4096 would otherwise reserve 16 * M * N floats (2.1 GB).
+    On a handle of its own, so that no earlier call has grown the workspace."""
+    import ctypes as C
+    from fuel_amd._native import check, lib
+    dev = F.RocmDevice(0)
+    m, n, k = 1024, 32000, 4096
+    wd = dev.alloc((n * (k // 256) * 144 // 4,), np.uint32)
+    check(lib().frq_memset(dev.handle, C.c_void_p(wd.ptr), 0, wd.nbytes))
+    xd = dev.alloc((m, k), np.float32)
+    check(lib().frq_memset(dev.handle, C.c_void_p(xd.ptr), 0, xd.nbytes))
+    out = dev.alloc((m, n), np.float32)
+    check(lib().frq_qmatmul(dev.handle, O.Q4K, 1, m, n, k, C.c_void_p(xd.ptr), xd.nbytes, C.c_void_p(wd.ptr),
+                            wd.nbytes, C.c_void_p(out.ptr), out.nbytes))
+    dev.synchronize()
+    ws = C.c_size_t()
+    check(lib().frq_device_workspace_bytes(dev.handle, C.byref(ws)))
+    act = m * k + m * (k // 256) * 4 + m * (k // 256) * 32   # Q8K rows: qs, d, bsums
+    say("  workspace bytes", ws.value, "quantized rows", act)
+    assert ws.value < 2 * act + (1 << 20)
+    assert np.all(out.numpy() == 0)
+    del wd, xd, out
+    dev.close()
 
 
 @pytest.mark.parametrize("dt", [O.Q4K, O.Q6K])
