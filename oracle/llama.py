@@ -98,5 +98,45 @@ class OracleLlama:
         xn = rms_norm(x, self.w["final_gain"], cfg.eps)
         return self._mm(Q6K, xn, self.w["out"])
 
+    def prefill(self, tokens, workers: int = 16) -> np.ndarray:
+        """The prompt as one batch (apply_layer at seq = M, lazy.rs:7363-7446):
+        every layer over all M positions with matmul<T> on M rows, the causal
+        attention of each query row over cache rows 0 .. its position (rows in
+        parallel threads: the C call releases the GIL), the caches filled as M
+        steps would fill them.  Returns the logits of the last position."""
+        from concurrent.futures import ThreadPoolExecutor
+
+        cfg = self.cfg
+        H, D = cfg.n_heads, cfg.head_dim
+        toks = np.asarray(tokens, np.int64)
+        M = toks.size
+        x = self.w["embed"][toks].astype(np.float32)
+        cs, sn = self.cos[:M], self.sin[:M]
+
+        def mm(dt, a, w):
+            return matmul(dt, a, w, avx2=True, threads=self.threads)
+
+        with ThreadPoolExecutor(workers) as pool:
+            for li, lw in enumerate(self.w["layers"]):
+                dts = layer_dtypes(cfg, li)
+                xn = rms_norm(x, lw["attn_gain"], cfg.eps)
+                q = rope(mm(dts["wq"], xn, lw["wq"]).reshape(M, H, D).transpose(1, 0, 2), cs, sn)  # [H, M, D]
+                k = rope(mm(dts["wk"], xn, lw["wk"]).reshape(M, H, D).transpose(1, 0, 2), cs, sn)
+                v = mm(dts["wv"], xn, lw["wv"]).reshape(M, H, D).transpose(1, 0, 2)
+                self.kc[li, :, :M] = k.astype(np.float16).astype(np.float32)
+                self.vc[li, :, :M] = v.astype(np.float16).astype(np.float32)
+                kc, vc = self.kc[li], self.vc[li]
+                rows = list(pool.map(lambda r: attention_decode(q[:, r], kc, vc, r + 1, float(self.scale)),
+                                     range(M)))
+                a = np.stack(rows).reshape(M, H * D)
+                x = (x + mm(dts["wo"], a, lw["wo"])).astype(np.float32)
+                xn = rms_norm(x, lw["ffn_gain"], cfg.eps)
+                g = mm(dts["wg"], xn, lw["wg"])
+                u = mm(dts["wu"], xn, lw["wu"])
+                h = (g / (np.float32(1.0) + np.exp(-g)) * u).astype(np.float32)
+                x = (x + mm(dts["wd"], h, lw["wd"])).astype(np.float32)
+        xn = rms_norm(x[M - 1], self.w["final_gain"], cfg.eps)
+        return self._mm(Q6K, xn, self.w["out"])
+
     def greedy(self, logits: np.ndarray) -> int:
         return argmax(logits)
