@@ -194,14 +194,16 @@ def gpu_leg(steps: int, warmup: int, q6k: bool = True):
     return ms_per_step, step_bytes, per_shape, R, batched, per_shape_q6k
 
 
-BATCHED_M = (32, 128, 512)
+BATCHED_M = (2, 4, 8, 16, 32, 128, 512)
 INT8_PEAK_TOPS = 5000.0
 
 
 def batched_leg(hip, dev, stream, mats):
     """QMatMul with M = 32, 128, 512 activation rows at the
-    same shapes and rotated weights (the int8-MFMA path).  Reported as
-    useful TOPS (2 M N K per call) against the dense int8 peak."""
+    same shapes and rotated weights (the int8-MFMA path), and small batches
+    M = 2, 4, 8, 16 (the one-pass small-batch mat-vec below 16 rows).
+    Reported as useful TOPS (2 M N K per call) against the dense int8 peak and
+    as weight bytes per second."""
     import ctypes as C
 
     import fuel_amd as F

@@ -88,9 +88,10 @@ int vec_dot_type(int t) { return t == GGML_Q8_0 ? GGML_Q8_0 : GGML_Q8K; }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// From this many activation rows on, QMatMul runs as an int8-MFMA GEMM instead
-// of the fused mat-vec (which streams the weights once per row group).
-constexpr size_t MMQ_MIN_ROWS = 16;
+// Activation rows per call: one row takes the fused quantize + mat-vec; up to
+// MMQ_MIN_ROWS - 1 rows the skinny MFMA kernel (one weight pass per 32-row
+// group); from MMQ_MIN_ROWS rows the tiled int8-MFMA GEMM.
+constexpr size_t MMQ_MIN_ROWS = 33;
 
 // Byte size of the quantized-activation workspace for rows x k.
 size_t act_bytes(int vt, size_t rows, size_t k) {
@@ -165,10 +166,13 @@ int run_qmatmul(frq_device* dev, int t, const uint8_t* w, const float* x, size_t
         return fail(FRQ_UNSUPPORTED, "qmatmul: rows=%zu n=%zu k=%zu exceed the launch limits", rows,
                     n, k);
     // each lane of the mat-vec holds at most 8 blocks of a row: K <= 8 * 16 * 256
-    // for the k-quants (4 lanes per superblock), K <= 8 * 32 * 32 for Q8_0
+    // for the k-quants (4 lanes per superblock), K <= 8 * 32 * 32 for Q8_0;
+    // longer rows (K a multiple of 256) take the skinny MFMA kernel, any K
     const size_t kmax = t == GGML_Q8_0 ? 8192 : 32768;
-    if (k > kmax) return fail(FRQ_UNSUPPORTED, "qmatmul: k=%zu exceeds %zu for dtype %d", k, kmax, t);
-    // the MFMA kernel addresses the weights with 32-bit offsets
+    const bool skinny = mmq_skinny_supported(t, (int)k);
+    if (k > kmax && !skinny)
+        return fail(FRQ_UNSUPPORTED, "qmatmul: k=%zu exceeds %zu for dtype %d", k, kmax, t);
+    // the tiled MFMA kernel addresses the weights with 32-bit offsets
     const bool w32 = n * (k / block_elems(t)) * type_size(t) <= 0xffffffffull;
     if (rows >= MMQ_MIN_ROWS && mmq_supported(t) && w32) {
         // many activation rows: quantize them once, then the int8-MFMA GEMM
@@ -182,6 +186,15 @@ int run_qmatmul(frq_device* dev, int t, const uint8_t* w, const float* x, size_t
         if (rc) return rc;
         float* part = plan.part_elems ? reinterpret_cast<float*>(static_cast<uint8_t*>(dev->ws) + abytes) : nullptr;
         HIP_TRY(launch_mmq(plan, t, w, act, y, part, (int)rows, (int)n, (int)k, (int)n, dev->stream));
+        return FRQ_OK;
+    }
+    if (skinny && (rows >= 2 || k > kmax)) {
+        // a few rows (and Q8_0 at any row count: it has no tiled MFMA
+        // kernel): quantize them once, then one weight pass per 32-row group
+        ActView act;
+        int rc = quantize_rows(dev, vec_dot_type(t), x, rows, k, nullptr, &act);
+        if (rc) return rc;
+        HIP_TRY(launch_mmq_skinny(t, w, act, y, (int)rows, (int)n, (int)k, (int)n, dev->num_cus, dev->stream));
         return FRQ_OK;
     }
     HIP_TRY(launch_qmv(t, w, x, y, (int)rows, (int)n, (int)k, (int)n, dev->stream, dev->num_cus));

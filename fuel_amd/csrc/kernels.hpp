@@ -98,6 +98,13 @@ hipError_t launch_moe_batches(const int* ids, int P, int E, int topk, int* offse
                               hipStream_t s);
 hipError_t launch_moe_combine(const float* yd, const int* ids, const float* w, const int* entry_pos, int T, int topk,
                               int d, float* out, hipStream_t s);
+// mmq_skinny.hip: int8-MFMA matmul for a few rows (activations already
+// quantized into the workspace, Q8K for the k-quants, Q8_0 for Q8_0), each
+// weight block read once for every row group of up to 32 rows; y [M, N] with
+// row stride ldy.  K must be a multiple of 256.
+bool mmq_skinny_supported(int dtype, int K);
+hipError_t launch_mmq_skinny(int dtype, const uint8_t* w, ActView act, float* y, int M, int N, int K, int ldy,
+                             int num_cus, hipStream_t s);
 // mmq.hip: int8-MFMA matmul for M >= 16 over activations already quantized
 // into the workspace (quantize_q8k), y [M, N] with row stride ldy.
 // mmq_plan picks the kernel (tile shape; the LDS-DMA staging only for 16-byte

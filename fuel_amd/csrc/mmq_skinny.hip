@@ -1,0 +1,363 @@
+// Quantized matmul for a few activation rows (2 <= M, up to 32 per row group):
+// fuel's matmul<T> (k_quants.rs:2284-2331) for T = BlockQ4K / BlockQ6K /
+// BlockQ8_0 on int8 MFMA, with each weight block read once from HBM straight
+// into registers.
+//
+// The activation rows are quantized once beforehand (quantize_q8k /
+// quantize_q8_0 into the device workspace, SoA: qs [M][K], d [M][K/blk],
+// bsums).  A workgroup owns 16 output columns and every row group of up to
+// 16*RT rows; its 16 wavefronts split K: wavefront w takes the 256-element
+// units w, w+16, ... (one Q4_K / Q6_K superblock, or eight Q8_0 blocks).
+// Lane l of a wavefront handles column l%16 and lane group c = l/16: it issues
+// exactly the loads of the one-row mat-vec's lane c for that column's block
+// (formats.hpp: Q4K/Q6K/Q80::load), so the 64 lanes read the 16 blocks once,
+// 16 bytes per load, and build the MFMA B fragments in registers.  The K
+// slots of an MFMA step are ordered to match those loads (a dot product does
+// not depend on the order of K, as long as A and B agree): lane group c of
+// step t holds elements
+//   Q4_K  64c + 16t + [0,16)            (nibbles of its two 16-byte qs pieces)
+//   Q6_K  128(c>>1) + 32t + 16(c&1) + [0,16)   (its ql / qh pieces, code t)
+//   Q8_0  32j + 8c + [0,8) of block j   (v_mfma_i32_16x16x32_i8, one block per MFMA)
+// and the A fragments are 16-byte (8-byte) loads of those elements of the
+// quantized rows, from L2.  Integer sums per superblock / block are exact:
+//   Q4_K  isum = 8*(X.Ba) + X.Bb, msum = X.Bm  (sc = 8a + b; mins broadcast),
+//   Q6_K  isum = 128*(X.Wh) + X.Wl            (w = (q-32)*sc = 128 wh + wl),
+//   Q8_0  isum = X.Q,
+// then one f32 step per superblock (block): y += d_x * (d*isum - dmin*msum).
+// At the end the 16 wavefronts' partial tiles are summed through LDS in
+// wavefront order (deterministic) and stored.
+#include "common.hpp"
+#include "formats.hpp"
+#include "kernels.hpp"
+#include "mfma.hpp"
+
+namespace frq {
+
+namespace {
+
+constexpr int SK_COLS = 16;    // output columns per workgroup
+constexpr int SK_UNIT = QK_K;  // elements per unit of the K loop
+
+typedef long i64;
+
+// ---- format policies: per unit, the lane's raw loads, its A fragment
+// offsets and the MFMAs + f32 step into facc[RT][4] ----
+
+struct SkQ4K {
+    using Raw = Q4K::Raw;
+    static constexpr int BYTES = Q4K_BYTES;
+    static constexpr int ACT = GGML_Q8K;
+    static constexpr int NA = 4;  // A fragments per row tile and unit (16 bytes each)
+    __device__ static void load(const uint8_t* row, int u, int c, Raw& r) { Q4K::load(row + (size_t)u * BYTES, c, r); }
+    __device__ static uint32_t aoff(int c, int t) { return 64u * c + 16u * t; }
+    template <int RT>
+    __device__ static void unit(const Raw& r, const v4i (&a)[RT][NA], int c, const float (&dx)[RT][4],
+                                float (&facc)[RT][4]) {
+        const uint32_t s0 = r.hd.y, s1 = r.hd.z, s2 = r.hd.w;
+        const uint32_t sc_a = s0 & 0x3f3f3f3fu;
+        const uint32_t sc_b = (s2 & 0x0f0f0f0fu) | (((s0 >> 6) & 0x03030303u) << 4);
+        const uint32_t mn_a = s1 & 0x3f3f3f3fu;
+        const uint32_t mn_b = ((s2 >> 4) & 0x0f0f0f0fu) | (((s1 >> 6) & 0x03030303u) << 4);
+        const uint32_t scw = c < 2 ? sc_a : sc_b, mnw = c < 2 ? mn_a : mn_b;
+        const uint32_t sh = 16u * (uint32_t)(c & 1);
+        const uint32_t sc2[2] = {(scw >> sh) & 0xffu, (scw >> (sh + 8)) & 0xffu};  // sub-blocks 2c, 2c+1
+        const uint32_t mn2[2] = {(mnw >> sh) & 0xffu, (mnw >> (sh + 8)) & 0xffu};
+        const uint32_t q[2][4] = {{r.q0.x, r.q0.y, r.q0.z, r.q0.w}, {r.q1.x, r.q1.y, r.q1.z, r.q1.w}};
+        v4i acc[RT][3];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int hi = t >> 1;  // t = 0, 1: low nibbles (sub-block 2c); 2, 3: high (2c+1)
+            const uint32_t* w = q[t & 1];
+            const uint32_t fa = sc2[hi] >> 3, fb = sc2[hi] & 7u;
+            uint32_t nb[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) nb[i] = (w[i] >> (4 * hi)) & 0x0f0f0f0fu;
+            const v4i ba = v4i{bytes_times(nb[0], fa), bytes_times(nb[1], fa), bytes_times(nb[2], fa),
+                               bytes_times(nb[3], fa)};
+            const v4i bb = v4i{bytes_times(nb[0], fb), bytes_times(nb[1], fb), bytes_times(nb[2], fb),
+                               bytes_times(nb[3], fb)};
+            const int mb = (int)(mn2[hi] * 0x01010101u);
+            const v4i bm = v4i{mb, mb, mb, mb};
+            const v4i zero = v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) {
+                acc[rt][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[rt][t], ba, t == 0 ? zero : acc[rt][0], 0, 0, 0);
+                acc[rt][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[rt][t], bb, t == 0 ? zero : acc[rt][1], 0, 0, 0);
+                acc[rt][2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[rt][t], bm, t == 0 ? zero : acc[rt][2], 0, 0, 0);
+            }
+        }
+        const float d = f16_to_f32(r.hd.x & 0xffffu), dmin = f16_to_f32(r.hd.x >> 16);
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int isum = 8 * acc[rt][0][i] + acc[rt][1][i];
+                facc[rt][i] = fmaf(dx[rt][i], fmaf(-dmin, (float)acc[rt][2][i], d * (float)isum), facc[rt][i]);
+            }
+    }
+};
+
+struct SkQ6K {
+    using Raw = Q6K::Raw;
+    static constexpr int BYTES = Q6K_BYTES;
+    static constexpr int ACT = GGML_Q8K;
+    static constexpr int NA = 4;
+    __device__ static void load(const uint8_t* row, int u, int c, Raw& r) { Q6K::load(row + (size_t)u * BYTES, c, r); }
+    __device__ static uint32_t aoff(int c, int t) { return 128u * (c >> 1) + 32u * t + 16u * (c & 1); }
+    template <int RT>
+    __device__ static void unit(const Raw& r, const v4i (&a)[RT][NA], int c, const float (&dx)[RT][4],
+                                float (&facc)[RT][4]) {
+        const uint32_t la[4] = {r.la.x, r.la.y, r.la.z, r.la.w}, lb[4] = {r.lb.x, r.lb.y, r.lb.z, r.lb.w};
+        const uint32_t qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+        const uint32_t sel = 8u * (uint32_t)(c & 1);
+        v4i acc[RT][2];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {  // code t: ql nibble t>>1 of la (t even) / lb (t odd), qh bits 2t
+            const uint32_t scw = t < 2 ? r.sc.x : r.sc.y;
+            const int sc = (int)(int8_t)((scw >> (16u * (uint32_t)(t & 1) + sel)) & 0xffu);  // scales[8hh + 2t + (c&1)]
+            const uint32_t f = (uint32_t)sc & 0xffffu, cst = (uint32_t)(-32 * sc) & 0xffffu;
+            const uint32_t sc16 = f | (f << 16), c16 = cst | (cst << 16);
+            const uint32_t* l = (t & 1) ? lb : la;
+            int wl[4], wh[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t u = ((l[i] >> (4 * (t >> 1))) & 0x0f0f0f0fu) | (((qh[i] >> (2 * t)) & 0x03030303u) << 4);
+                q6_planes(u, sc16, c16, wl[i], wh[i]);
+            }
+            const v4i bh = v4i{wh[0], wh[1], wh[2], wh[3]}, bl = v4i{wl[0], wl[1], wl[2], wl[3]};
+            const v4i zero = v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) {
+                acc[rt][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[rt][t], bh, t == 0 ? zero : acc[rt][0], 0, 0, 0);
+                acc[rt][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[rt][t], bl, t == 0 ? zero : acc[rt][1], 0, 0, 0);
+            }
+        }
+        const float d = f16_to_f32(r.dbits);
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int isum = 128 * acc[rt][0][i] + acc[rt][1][i];
+                facc[rt][i] = fmaf(dx[rt][i], d * (float)isum, facc[rt][i]);
+            }
+    }
+};
+
+// Q8_0: a unit is eight 34-byte blocks; lane group c holds bytes 8c..8c+7 of
+// each block's quants (one 8-byte load per block) and the block's f16 d.
+struct SkQ80 {
+    struct Raw {
+        uint2 q[8];
+        uint32_t dbits[8];
+    };
+    static constexpr int BYTES = 8 * Q8_0_BYTES;
+    static constexpr int ACT = GGML_Q8_0;
+    static constexpr int NA = 4;  // 16-byte A loads: blocks (2i, 2i+1)'s 8-byte slices
+    __device__ static void load(const uint8_t* row, int u, int c, Raw& r) {
+        const uint8_t* b = row + (size_t)u * BYTES;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            r.q[j] = load8_u(b + j * Q8_0_BYTES + 2 + 8 * c);
+            r.dbits[j] = load_u16(b + j * Q8_0_BYTES);
+        }
+    }
+    // A fragment i (16 bytes) = blocks 2i and 2i+1's slices 8c..8c+7: two
+    // 8-byte pieces 32 bytes apart; loaded as two halves by the kernel
+    __device__ static uint32_t aoff(int c, int t) { return 64u * t + 8u * c; }
+    // dx: the activation scales of the lane's output rows, d [M][K/32] (the
+    // unit's blocks are read per block: 4 per row tile)
+    template <int RT>
+    __device__ static void unit(const Raw& r, const v4i (&a)[RT][NA], int c, const float* const (&dx)[RT][4],
+                                float (&facc)[RT][4]) {
+        (void)c;
+        const v4i zero = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const i64 bq = (i64)(((unsigned long long)r.q[j].y << 32) | r.q[j].x);
+            const float dw = f16_to_f32(r.dbits[j]);
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) {
+                const v4i av = a[rt][j >> 1];
+                const i64 aq = (j & 1) ? (i64)(((unsigned long long)(uint32_t)av[3] << 32) | (uint32_t)av[2])
+                                       : (i64)(((unsigned long long)(uint32_t)av[1] << 32) | (uint32_t)av[0]);
+                const v4i s = __builtin_amdgcn_mfma_i32_16x16x32_i8(aq, bq, zero, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) facc[rt][i] = fmaf(dw * dx[rt][i][j], (float)s[i], facc[rt][i]);
+            }
+        }
+    }
+};
+
+// A fragments of unit u for the lane's row tiles: row m0 + 16rt + l%16
+// (clamped into [0, M)), bytes aoff(c, t) of the unit.
+template <class F, int RT>
+__device__ __forceinline__ void sk_load_a(const int8_t* __restrict__ qs, int K, int u, int c, const int (&arow)[RT],
+                                          v4i (&a)[RT][F::NA]) {
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        const int8_t* p = qs + (size_t)arow[rt] * K + (size_t)u * SK_UNIT;
+#pragma unroll
+        for (int t = 0; t < F::NA; t++) {
+            if constexpr (F::ACT == GGML_Q8_0) {  // blocks 2t, 2t+1: bytes 64t + 8c and 64t + 32 + 8c
+                const uint2 lo = *reinterpret_cast<const uint2*>(p + F::aoff(c, t));
+                const uint2 hi = *reinterpret_cast<const uint2*>(p + F::aoff(c, t) + 32);
+                a[rt][t] = v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+            } else {
+                a[rt][t] = *reinterpret_cast<const v4i*>(p + F::aoff(c, t));
+            }
+        }
+    }
+}
+
+// A workgroup is one 16-column tile; its NWV wavefronts split K (NWV is
+// sized by the launcher so that tiles x NWV wavefronts fill the GPU: 16 for
+// N = 4096, fewer for wider matrices, whose wavefronts then stream several
+// units each through the register ring).
+template <class F, int RT, int NWV>
+__global__ __launch_bounds__(64 * NWV) void mmq_skinny_kernel(const uint8_t* __restrict__ W, ActView act,
+                                                                    float* __restrict__ y, int M, int N, int K,
+                                                                    int ldy) {
+    __shared__ float red[NWV][RT][4][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = lane >> 4, l16 = lane & 15;
+    const int n0 = blockIdx.x * SK_COLS, m0 = blockIdx.y * 16 * RT;
+    const int KU = K / SK_UNIT;
+    const int n = n0 + l16 < N ? n0 + l16 : N - 1;  // tail columns re-read a valid row; their outputs are dropped
+    const size_t row_bytes = F::ACT == GGML_Q8_0 ? (size_t)(K / QK8_0) * Q8_0_BYTES : (size_t)(K / QK_K) * F::BYTES;
+    const uint8_t* wrow = W + (size_t)n * row_bytes;
+    int arow[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        const int m = m0 + 16 * rt + l16;
+        arow[rt] = m < M ? m : M - 1;
+    }
+    float facc[RT][4];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) facc[rt][i] = 0.0f;
+
+    // the lane's output rows (C layout: rows 4c + i of each 16-row tile)
+    int orow[RT][4];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = m0 + 16 * rt + 4 * c + i;
+            orow[rt][i] = m < M ? m : M - 1;
+        }
+
+    // Two-unit register ring: the next unit's weight and activation loads are
+    // in flight while the current one is multiplied.  The loads are
+    // unconditional (past the last unit a wavefront re-reads its current one,
+    // cache-resident), so no branch sits between a load and its use.
+    auto step = [&](const typename F::Raw& rw, const v4i(&av)[RT][F::NA], int uu) __attribute__((always_inline)) {
+        if constexpr (F::ACT == GGML_Q8_0) {
+            const float* dx[RT][4];  // d of blocks 8uu.. of the lane's output rows
+            const int KB = K / QK8_0;
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) dx[rt][i] = act.d + (size_t)orow[rt][i] * KB + 8 * uu;
+            F::template unit<RT>(rw, av, c, dx, facc);
+        } else {
+            float dx[RT][4];
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) dx[rt][i] = act.d[(size_t)orow[rt][i] * KU + uu];
+            F::template unit<RT>(rw, av, c, dx, facc);
+        }
+    };
+    typename F::Raw ra, rb;
+    v4i aa[RT][F::NA], ab[RT][F::NA];
+    int u = wave;
+    if (u < KU) {  // (uniform: a wavefront past the last unit only joins the reduction)
+        F::load(wrow, u, c, ra);
+        sk_load_a<F, RT>(act.qs, K, u, c, arow, aa);
+        while (true) {
+            int nu = u + NWV < KU ? u + NWV : u;
+            F::load(wrow, nu, c, rb);
+            sk_load_a<F, RT>(act.qs, K, nu, c, arow, ab);
+            step(ra, aa, u);
+            if (u + NWV >= KU) break;
+            u += NWV;
+            nu = u + NWV < KU ? u + NWV : u;
+            F::load(wrow, nu, c, ra);
+            sk_load_a<F, RT>(act.qs, K, nu, c, arow, aa);
+            step(rb, ab, u);
+            if (u + NWV >= KU) break;
+            u += NWV;
+        }
+    }
+
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) red[wave][rt][i][lane] = facc[rt][i];
+    __syncthreads();
+    for (int e = threadIdx.x; e < RT * 4 * 64; e += 64 * NWV) {
+        const int rt = e >> 8, i = (e >> 6) & 3, l = e & 63;
+        float s = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NWV; w++) s += red[w][rt][i][l];
+        const int m = m0 + 16 * rt + 4 * (l >> 4) + i, nn = n0 + (l & 15);
+        if (m < M && nn < N) y[(size_t)m * ldy + nn] = s;
+    }
+}
+
+template <class F, int RT, int NWV>
+hipError_t launch_sk(const uint8_t* w, ActView act, float* y, int M, int N, int K, int ldy, hipStream_t s) {
+    const dim3 grid((N + SK_COLS - 1) / SK_COLS, (M + 16 * RT - 1) / (16 * RT));
+    hipLaunchKernelGGL((mmq_skinny_kernel<F, RT, NWV>), grid, dim3(64 * NWV), 0, s, w, act, y, M, N, K, ldy);
+    return hipGetLastError();
+}
+
+// K split: about 16 wavefronts per CU over the whole grid (the tiles of every
+// row group), at most 16 per tile and no more than the tile has units.
+int sk_split(int tiles, int KU, int num_cus) {
+    const long target = 16L * num_cus;
+    int nwv = 16;
+    while (nwv > 2 && ((long)tiles * nwv / 2 >= target || nwv / 2 >= KU)) nwv /= 2;
+    return nwv;
+}
+
+template <class F, int RT>
+hipError_t launch_sk_rt(const uint8_t* w, ActView act, float* y, int M, int N, int K, int ldy, int num_cus,
+                        hipStream_t s) {
+    const int tiles = (N + SK_COLS - 1) / SK_COLS * ((M + 16 * RT - 1) / (16 * RT));
+    // (two row tiles: at most 8 wavefronts, 512 threads, for their registers)
+    const int nwv = sk_split(tiles, K / SK_UNIT, num_cus);
+    switch (RT == 2 && nwv > 8 ? 8 : nwv) {
+        case 16: return launch_sk<F, RT, RT == 2 ? 8 : 16>(w, act, y, M, N, K, ldy, s);
+        case 8: return launch_sk<F, RT, 8>(w, act, y, M, N, K, ldy, s);
+        case 4: return launch_sk<F, RT, 4>(w, act, y, M, N, K, ldy, s);
+        default: return launch_sk<F, RT, 2>(w, act, y, M, N, K, ldy, s);
+    }
+}
+
+template <class F>
+hipError_t launch_sk_fmt(const uint8_t* w, ActView act, float* y, int M, int N, int K, int ldy, int num_cus,
+                         hipStream_t s) {
+    return M <= 16 ? launch_sk_rt<F, 1>(w, act, y, M, N, K, ldy, num_cus, s)
+                   : launch_sk_rt<F, 2>(w, act, y, M, N, K, ldy, num_cus, s);
+}
+
+}  // namespace
+
+bool mmq_skinny_supported(int dtype, int K) {
+    return (dtype == GGML_Q4K || dtype == GGML_Q6K || dtype == GGML_Q8_0) && K > 0 && K % SK_UNIT == 0;
+}
+
+hipError_t launch_mmq_skinny(int dtype, const uint8_t* w, ActView act, float* y, int M, int N, int K, int ldy,
+                             int num_cus, hipStream_t s) {
+    if (!mmq_skinny_supported(dtype, K) || M < 1 || N < 1) return hipErrorInvalidValue;
+    switch (dtype) {
+        case GGML_Q4K: return launch_sk_fmt<SkQ4K>(w, act, y, M, N, K, ldy, num_cus, s);
+        case GGML_Q6K: return launch_sk_fmt<SkQ6K>(w, act, y, M, N, K, ldy, num_cus, s);
+        default: return launch_sk_fmt<SkQ80>(w, act, y, M, N, K, ldy, num_cus, s);
+    }
+}
+
+}  // namespace frq

@@ -1,0 +1,71 @@
+// Per-row building blocks of the quantized mat-vec kernels (mmvq.hip,
+// mmvq_multi.hip): launch sizes, the unconditional loads of one weight row
+// into registers and the row's dot product against an LDS activation row.
+#pragma once
+
+#include "common.hpp"
+#include "formats.hpp"
+
+namespace frq {
+
+// Workgroup size for many rows: 1024 threads while a row's raw weight
+// registers stay small (<= 36 dwords: the kernel then fits the 128 VGPRs a
+// 1024-thread workgroup allows), 512 up to 40 dwords, else 256.  Fewer,
+// larger workgroups quantize the activation row fewer times per CU (measured:
+// 4096x11008 Q4_K 7.8 -> 7.5 us, Q6_K 12.4 -> 11.0 us; 256 threads is slower).
+template <class F, int SPL>
+constexpr int qmv_wg() {
+    constexpr int raw = SPL * (int)(sizeof(typename F::Raw) / 4);
+    return raw <= 36 ? 1024 : raw <= 40 ? 512 : 256;
+}
+
+// Workgroup size for few rows (about two per wavefront at one workgroup per
+// CU): as large as the register budget allows, so that one workgroup per CU
+// quantizes the activation row once for all its wavefronts (1024 threads
+// need <= 128 VGPRs, 512 threads <= 256).
+template <class F, int SPL>
+constexpr int qmv_wg_big() {
+    constexpr int raw = SPL * (int)(sizeof(typename F::Raw) / 4);
+    return raw <= 36 ? 1024 : raw <= 48 ? 512 : qmv_wg<F, SPL>();
+}
+
+// The loads are unconditional (a slot past the row's last block re-reads that
+// block; qmv_row skips it): with no branch around them the in-order vmcnt
+// counter can wait for one row while the next row's loads stay in flight.
+template <class F, int SPL>
+__device__ __forceinline__ void qmv_load_row(const uint8_t* __restrict__ wr, int gi, int c, int KB,
+                                             typename F::Raw (&r)[SPL]) {
+    constexpr int BPW = 64 / F::LPB;
+#pragma unroll
+    for (int s = 0; s < SPL; s++) {
+        const int b = gi + BPW * s;
+        F::load(wr + (size_t)(b < KB ? b : KB - 1) * F::BYTES, c, r[s]);
+    }
+}
+
+// Row dot product of one weight row (raw registers) with the LDS activation;
+// the f32 total is valid in lane 63 (RPW > 1: each 64/RPW-lane segment holds
+// its own row, total in the segment's last lane).
+template <class F, int SPL, int RPW = 1>
+__device__ __forceinline__ float qmv_row(const typename F::Raw (&r)[SPL], const int8_t* s_qs, int qstride,
+                                         const float* s_d, const int16_t* s_bs, int gi, int c, int KB) {
+    constexpr int BPW = 64 / F::LPB;
+    float acc = 0.0f;
+#pragma unroll
+    for (int s = 0; s < SPL; s++) {
+        const int b = gi + BPW * s;
+        if (b < KB) {
+            typename F::Act xa;
+            F::load_act(s_qs, qstride, s_d, s_bs, b, c, xa);
+            int isum, msum;
+            float dw, dmw;
+            F::dot(r[s], xa, c, isum, msum, dw, dmw);
+            acc = fmaf(dw * xa.d, (float)isum, acc);
+            acc = fmaf(-(dmw * xa.d), (float)msum, acc);
+        }
+    }
+    if constexpr (RPW == 1) return dpp_wave_sum(acc);
+    else return dpp_seg_sum<RPW>(acc);
+}
+
+}  // namespace frq

@@ -114,6 +114,55 @@ def test_qmatmul_m1_7b_shapes(dev, dt, k, n):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("dt", [O.Q4K, O.Q6K, O.Q8_0])
+@pytest.mark.parametrize("m,k,n", [(2, 4096, 4096), (3, 4096, 1000), (8, 4096, 4096), (15, 11008, 4096),
+                                   (5, 11008, 776), (9, 2048, 300), (16, 256, 40), (24, 4096, 1000),
+                                   (32, 11008, 4096)])
+def test_qmatmul_small_batch(dev, dt, m, k, n):
+    """2 <= M <= 32 rows (and Q8_0 at any M) take the skinny int8-MFMA kernel
+    (rows quantized once, each weight block read once per 32-row group, K
+    split over the workgroup's wavefronts): within the tolerance of the
+    oracle, and independent of the other rows of the batch: every row
+    computed beside a single other row (a two-row call; 16-row tiles up to 16
+    rows, two tiles up to 32) gives the same bits."""
+    say("small batch", dt, m, k, n)
+    wq = weights(dt, n, k)
+    x = acts(m, k, seed=m)
+    want = O.matmul(dt, x, wq)
+    w = dev.from_numpy(as_u32(wq))
+    xd = dev.from_numpy(x)
+    out = dev.alloc((m, n), np.float32)
+    F.qmatmul_f32_rocm_wrapper([xd, w], [out], F.QMatMulParams(dt, 1, m, n, k))
+    got = out.numpy()
+    err = rel_err(got, want)
+    say("  rel_err", err)
+    assert err <= TOL
+    if m > 16:
+        return  # (a two-row call takes the one-tile kernel; its split of K differs)
+    two = dev.alloc((2, n), np.float32)
+    for r in range(m):
+        pair = np.ascontiguousarray(x[[r, (r + 1) % m]])
+        F.qmatmul_f32_rocm_wrapper([dev.from_numpy(pair), w], [two], F.QMatMulParams(dt, 1, 2, n, k))
+        assert np.array_equal(two.numpy()[0].view(np.uint32), got[r].view(np.uint32)), r
+
+
+@pytest.mark.parametrize("m", [16, 32, 100])
+def test_qmatmul_q8_0_batched(dev, m):
+    """Q8_0 (no MFMA kernel) at 16 or more rows: the small-batch mat-vec in
+    groups of 8 rows, against the oracle at 4096 x 4096."""
+    say("q8_0 batched", m)
+    k = n = 4096
+    wq = weights(O.Q8_0, n, k)
+    x = acts(m, k)
+    want = O.matmul(O.Q8_0, x, wq)
+    out = dev.alloc((m, n), np.float32)
+    F.qmatmul_f32_rocm_wrapper([dev.from_numpy(x), dev.from_numpy(as_u32(wq))], [out],
+                               F.QMatMulParams(O.Q8_0, 1, m, n, k))
+    err = rel_err(out.numpy(), want)
+    say("  rel_err", err)
+    assert err <= TOL
+
+
 def test_qmatmul_q8_0_config1(dev):
     # BASELINE config 1: Q8_0 QMatMul, x [1,4096] ~ N(0,1), W [4096,4096] ~ N(0,0.02)
     k = n = 4096
