@@ -209,8 +209,12 @@ int run_qmatmul_f16(frq_device* dev, int t, const uint8_t* w, const uint16_t* x,
     if (rows == 0 || n == 0) return FRQ_OK;
     if (k > (size_t)0x7fffffff || n > (size_t)0x7fffffff || rows > 65535)
         return fail(FRQ_UNSUPPORTED, "qmatmul_f16: rows=%zu n=%zu k=%zu exceed the launch limits", rows, n, k);
+    // the same kernels as run_qmatmul for the same rows (so that the outputs
+    // are the f32 path's, rounded), with f16 activation loads and stores
     const size_t kmax = t == GGML_Q8_0 ? 8192 : 32768;
-    if (k > kmax) return fail(FRQ_UNSUPPORTED, "qmatmul_f16: k=%zu exceeds %zu for dtype %d", k, kmax, t);
+    const bool skinny = mmq_skinny_supported(t, (int)k);
+    if (k > kmax && !skinny)
+        return fail(FRQ_UNSUPPORTED, "qmatmul_f16: k=%zu exceeds %zu for dtype %d", k, kmax, t);
     const bool w32 = n * (k / block_elems(t)) * type_size(t) <= 0xffffffffull;
     if (rows >= MMQ_MIN_ROWS && mmq_supported(t) && w32) {
         const MmqPlan plan = mmq_plan(t, w, (int)rows, (int)n, (int)k, dev->num_cus);
@@ -222,6 +226,17 @@ int run_qmatmul_f16(frq_device* dev, int t, const uint8_t* w, const uint16_t* x,
         float* part = plan.part_elems ? reinterpret_cast<float*>(static_cast<uint8_t*>(dev->ws) + abytes) : nullptr;
         HIP_TRY(launch_mmq(plan, t, w, act, reinterpret_cast<float*>(y), part, (int)rows, (int)n, (int)k, (int)n,
                            dev->stream, true));
+        return FRQ_OK;
+    }
+    if (skinny && (rows >= 2 || k > kmax)) {
+        const int vt = vec_dot_type(t);
+        int rc = ensure_ws(dev, act_bytes(vt, rows, k));
+        if (rc) return rc;
+        const ActView act = act_view(dev->ws, vt, rows, k);
+        HIP_TRY(vt == GGML_Q8K ? launch_quantize_q8k_h(x, (int)rows, (int)k, act, dev->stream)
+                               : launch_quantize_q8_0_h(x, (int)rows, (int)k, act, dev->stream));
+        HIP_TRY(launch_mmq_skinny(t, w, act, reinterpret_cast<float*>(y), (int)rows, (int)n, (int)k, (int)n,
+                                  dev->num_cus, dev->stream, true));
         return FRQ_OK;
     }
     HIP_TRY(launch_qmv_half(t, w, x, y, (int)rows, (int)n, (int)k, (int)n, dev->stream, dev->num_cus));

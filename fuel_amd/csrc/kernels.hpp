@@ -17,6 +17,7 @@ hipError_t launch_quantize_q8_0(const float* x, int rows, int K, ActView act, ui
                                 hipStream_t s);
 // Q8K rows of f16 activations (widened exactly to f32 first).
 hipError_t launch_quantize_q8k_h(const uint16_t* x, int rows, int K, ActView act, hipStream_t s);
+hipError_t launch_quantize_q8_0_h(const uint16_t* x, int rows, int K, ActView act, hipStream_t s);
 
 // mmvq.hip: y[m, n] = sum_b blockdot(W[n, b], quantize(x[m])_b) for rows m < M,
 // activation quantization fused into the kernel.
@@ -104,7 +105,7 @@ hipError_t launch_moe_combine(const float* yd, const int* ids, const float* w, c
 // row stride ldy.  K must be a multiple of 256.
 bool mmq_skinny_supported(int dtype, int K);
 hipError_t launch_mmq_skinny(int dtype, const uint8_t* w, ActView act, float* y, int M, int N, int K, int ldy,
-                             int num_cus, hipStream_t s);
+                             int num_cus, hipStream_t s, bool y_half = false);
 // mmq.hip: int8-MFMA matmul for M >= 16 over activations already quantized
 // into the workspace (quantize_q8k), y [M, N] with row stride ldy.
 // mmq_plan picks the kernel (tile shape; the LDS-DMA staging only for 16-byte

@@ -75,6 +75,31 @@ __global__ __launch_bounds__(64) void quantize_q8_0_kernel(const float* __restri
     }
 }
 
+// f16 rows of the Q8_0 path (matmul_f16): halves widened exactly to f32, then
+// the Q8_0 from_float of the kernel above; grid = (ceil(K/256), rows).
+__global__ __launch_bounds__(64) void quantize_q8_0_h_kernel(const uint16_t* __restrict__ x, int K, ActView act) {
+    const int m = blockIdx.y, lane = threadIdx.x;
+    const int KB = K / QK8_0;
+    const int blk = blockIdx.x * 8 + (lane >> 3);
+    const bool live = blk < KB;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live) {
+        const uint2 h = reinterpret_cast<const uint2*>(x + (size_t)m * K + (size_t)blk * QK8_0)[lane & 7];
+        v = make_float4(f16_to_f32(h.x & 0xffffu), f16_to_f32(h.x >> 16), f16_to_f32(h.y & 0xffffu),
+                        f16_to_f32(h.y >> 16));
+    }
+    const Q80Wave r = q8_0_quantize_vals(v, lane);
+    if (!live) return;
+    reinterpret_cast<uint32_t*>(act.qs + (size_t)m * K + (size_t)blk * QK8_0)[lane & 7] = r.packed;
+    if ((lane & 7) == 0) act.d[(size_t)m * KB + blk] = f16_to_f32(r.dbits);
+}
+
+hipError_t launch_quantize_q8_0_h(const uint16_t* x, int rows, int K, ActView act, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(quantize_q8_0_h_kernel, dim3((K / QK8_0 + 7) / 8, rows), dim3(64), 0, s, x, K, act);
+    return hipGetLastError();
+}
+
 hipError_t launch_quantize_q8k(const float* x, int rows, int K, ActView act, uint8_t* aos,
                                hipStream_t s) {
     dim3 grid(K / QK_K, rows);
