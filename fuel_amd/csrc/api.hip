@@ -16,6 +16,15 @@
 
 using namespace frq;
 
+// Scratch of frq_qmatmul_noalloc: quantized activation rows and split-K
+// partial sums, in a device array of fixed size rather than the handle's
+// hipMalloc'd workspace.  Every GPU the library runs on holds its own copy
+// until the process ends.  In host code the array's name is only a stand-in:
+// its device address (per GPU) comes from hipGetSymbolAddress at
+// frq_device_open and is what kernels are given.
+constexpr size_t FRQ_NOALLOC_SCRATCH_BYTES = (size_t)32 << 20;
+static __device__ __align__(256) uint8_t scratch[FRQ_NOALLOC_SCRATCH_BYTES];
+
 struct frq_device {
     int ordinal = 0;
     hipStream_t own_stream = nullptr;
@@ -23,6 +32,7 @@ struct frq_device {
     int num_cus = 0;
     void* ws = nullptr;  // activation workspace (quantized rows)
     size_t ws_bytes = 0;
+    void* scratch = nullptr;  // this device's copy of the allocation-free entry point's scratch array
     // references: the open handle plus one per live storage; the struct is
     // deleted when the last one is dropped (a storage may outlive close)
     std::atomic<int> refs{1};
@@ -143,6 +153,41 @@ void release_device(frq_device* dev) {
     if (dev->refs.fetch_sub(1) == 1) delete dev;
 }
 
+// Device memory a call may use as scratch: the handle's workspace, grown with
+// hipMalloc on demand (base == nullptr), or a fixed region that is never grown
+// (the allocation-free entry point's).
+struct Scratch {
+    uint8_t* base = nullptr;
+    size_t bytes = 0;
+};
+
+int scratch_at_least(frq_device* dev, const Scratch& fx, size_t bytes, uint8_t** base, const char* who) {
+    if (fx.base) {
+        if (bytes > fx.bytes)
+            return fail(FRQ_WORKSPACE, "%s: needs %zu bytes of scratch; the allocation-free entry point holds %zu",
+                        who, bytes, fx.bytes);
+        *base = fx.base;
+        return FRQ_OK;
+    }
+    int rc = ensure_ws(dev, bytes);
+    if (rc) return rc;
+    *base = static_cast<uint8_t*>(dev->ws);
+    return FRQ_OK;
+}
+
+// Quantize rows x [rows, k] into scratch at `base` (and optionally into fuel's
+// block layout at `aos`), returning the view.
+int quantize_rows_at(frq_device* dev, int vt, const float* x, size_t rows, size_t k, void* aos, uint8_t* base,
+                     ActView* view) {
+    *view = act_view(base, vt, rows, k);
+    if (rows == 0) return FRQ_OK;
+    hipError_t e = vt == GGML_Q8K
+                       ? launch_quantize_q8k(x, (int)rows, (int)k, *view, (uint8_t*)aos, dev->stream)
+                       : launch_quantize_q8_0(x, (int)rows, (int)k, *view, (uint8_t*)aos, dev->stream);
+    HIP_TRY(e);
+    return FRQ_OK;
+}
+
 // Quantize rows x [rows, k] into the workspace (and optionally into fuel's
 // block layout at `aos`), returning the workspace view.
 int quantize_rows(frq_device* dev, int vt, const float* x, size_t rows, size_t k, void* aos,
@@ -158,9 +203,10 @@ int quantize_rows(frq_device* dev, int vt, const float* x, size_t rows, size_t k
     return FRQ_OK;
 }
 
-// y[rows, n] = x[rows, k] @ dequant(W[n, k])^T through the int8 path.
+// y[rows, n] = x[rows, k] @ dequant(W[n, k])^T through the int8 path, with
+// its scratch (quantized rows, split-K partials) from `fx` when that is set.
 int run_qmatmul(frq_device* dev, int t, const uint8_t* w, const float* x, size_t rows, size_t n,
-                size_t k, float* y) {
+                size_t k, float* y, const Scratch& fx = Scratch{}) {
     if (rows == 0 || n == 0) return FRQ_OK;
     if (k > (size_t)0x7fffffff || n > (size_t)0x7fffffff || rows > 65535)
         return fail(FRQ_UNSUPPORTED, "qmatmul: rows=%zu n=%zu k=%zu exceed the launch limits", rows,
@@ -176,23 +222,29 @@ int run_qmatmul(frq_device* dev, int t, const uint8_t* w, const float* x, size_t
     const bool w32 = n * (k / block_elems(t)) * type_size(t) <= 0xffffffffull;
     if (rows >= MMQ_MIN_ROWS && mmq_supported(t) && w32) {
         // many activation rows: quantize them once, then the int8-MFMA GEMM
-        // workspace: quantized rows, then the split-K partial sums the plan needs
-        const MmqPlan plan = mmq_plan(t, w, (int)rows, (int)n, (int)k, dev->num_cus);
+        // scratch: quantized rows, then the split-K partial sums the plan needs
+        // (a fixed scratch region lowers the split until they fit)
         const size_t abytes = align256(act_bytes(vec_dot_type(t), rows, k));
-        int rc = ensure_ws(dev, abytes + plan.part_elems * sizeof(float));
+        const size_t pcap = !fx.base ? ~(size_t)0 : fx.bytes > abytes ? (fx.bytes - abytes) / sizeof(float) : 0;
+        const MmqPlan plan = mmq_plan(t, w, (int)rows, (int)n, (int)k, dev->num_cus, pcap);
+        uint8_t* base = nullptr;
+        int rc = scratch_at_least(dev, fx, abytes + plan.part_elems * sizeof(float), &base, "qmatmul");
         if (rc) return rc;
         ActView act;
-        rc = quantize_rows(dev, vec_dot_type(t), x, rows, k, nullptr, &act);
+        rc = quantize_rows_at(dev, vec_dot_type(t), x, rows, k, nullptr, base, &act);
         if (rc) return rc;
-        float* part = plan.part_elems ? reinterpret_cast<float*>(static_cast<uint8_t*>(dev->ws) + abytes) : nullptr;
+        float* part = plan.part_elems ? reinterpret_cast<float*>(base + abytes) : nullptr;
         HIP_TRY(launch_mmq(plan, t, w, act, y, part, (int)rows, (int)n, (int)k, (int)n, dev->stream));
         return FRQ_OK;
     }
     if (skinny && (rows >= 2 || k > kmax)) {
         // a few rows (and Q8_0 at any row count: it has no tiled MFMA
         // kernel): quantize them once, then one weight pass per 32-row group
+        uint8_t* base = nullptr;
+        int rc = scratch_at_least(dev, fx, act_bytes(vec_dot_type(t), rows, k), &base, "qmatmul");
+        if (rc) return rc;
         ActView act;
-        int rc = quantize_rows(dev, vec_dot_type(t), x, rows, k, nullptr, &act);
+        rc = quantize_rows_at(dev, vec_dot_type(t), x, rows, k, nullptr, base, &act);
         if (rc) return rc;
         HIP_TRY(launch_mmq_skinny(t, w, act, y, (int)rows, (int)n, (int)k, (int)n, dev->num_cus, dev->stream));
         return FRQ_OK;
@@ -326,9 +378,15 @@ int frq_device_open(int ordinal, frq_device** out) {
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(FRQ_UNSUPPORTED, "device %d is %s; this library is built for gfx950", ordinal,
                     prop.gcnArchName);
+    // this device's copy of the allocation-free entry point's scratch array
+    // (looked up with the device current)
+    void* sp = nullptr;
+    HIP_TRY(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)));
+    if (!sp) return fail(FRQ_INTERNAL, "hipGetSymbolAddress(scratch) returned a null address on device %d", ordinal);
     frq_device* d = new frq_device();
     d->ordinal = ordinal;
     d->num_cus = prop.multiProcessorCount;
+    d->scratch = sp;
     hipError_t e = hipStreamCreateWithFlags(&d->own_stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         delete d;
@@ -580,8 +638,12 @@ int frq_qstorage_fwd_f16(const frq_qstorage* q, size_t n, size_t k, const uint16
 
 // ---- KernelRef seam ----
 
-int frq_qmatmul(frq_device* dev, int t, size_t batch, size_t m, size_t n, size_t k, const float* act,
-                size_t act_b, const uint32_t* w, size_t w_b, float* out, size_t out_b) {
+namespace {
+
+// frq_qmatmul's checks (qmatmul_generic_f32, byte_kernels.rs:4767-4806), then
+// the matmul with its scratch from `fx` when set.
+int qmatmul_checked(frq_device* dev, int t, size_t batch, size_t m, size_t n, size_t k, const float* act,
+                    size_t act_b, const uint32_t* w, size_t w_b, float* out, size_t out_b, const Scratch& fx) {
     int rc = use_device(dev);
     if (rc) return rc;
     if (!is_weight_type(t)) return fail(FRQ_UNSUPPORTED, "qmatmul: unsupported quant_type %d", t);
@@ -603,7 +665,23 @@ int frq_qmatmul(frq_device* dev, int t, size_t batch, size_t m, size_t n, size_t
     if (!aligned4(w) || !aligned4(act) || !aligned4(out))
         return fail(FRQ_MISALIGNED, "qmatmul: buffers must be 4-byte aligned");
     // The batch shares W, so all batch*m activation rows go through one launch.
-    return run_qmatmul(dev, t, reinterpret_cast<const uint8_t*>(w), act, batch * m, n, k, out);
+    return run_qmatmul(dev, t, reinterpret_cast<const uint8_t*>(w), act, batch * m, n, k, out, fx);
+}
+
+}  // namespace
+
+int frq_qmatmul(frq_device* dev, int t, size_t batch, size_t m, size_t n, size_t k, const float* act,
+                size_t act_b, const uint32_t* w, size_t w_b, float* out, size_t out_b) {
+    return qmatmul_checked(dev, t, batch, m, n, k, act, act_b, w, w_b, out, out_b, Scratch{});
+}
+
+int frq_qmatmul_noalloc(frq_device* dev, int t, size_t batch, size_t m, size_t n, size_t k, const float* act,
+                        size_t act_b, const uint32_t* w, size_t w_b, float* out, size_t out_b) {
+    if (!dev) return fail(FRQ_INVALID, "null device handle");
+    Scratch fx;
+    fx.base = static_cast<uint8_t*>(dev->scratch);
+    fx.bytes = FRQ_NOALLOC_SCRATCH_BYTES;
+    return qmatmul_checked(dev, t, batch, m, n, k, act, act_b, w, w_b, out, out_b, fx);
 }
 
 // ---- taps ----

@@ -118,7 +118,8 @@ struct MmqPlan {
     int ks;             // K splits (1: none)
     size_t part_elems;  // split partial sums: ks * M * N, or 0
 };
-MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus);
+// max_part_elems caps the partials: the K split is lowered until they fit.
+MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus, size_t max_part_elems = ~(size_t)0);
 hipError_t launch_mmq(const MmqPlan& plan, int dtype, const uint8_t* w, ActView act, float* y, float* part, int M,
                       int N, int K, int ldy, hipStream_t s, bool y_half = false);
 

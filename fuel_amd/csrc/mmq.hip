@@ -683,7 +683,7 @@ enum MmqKind {
 
 bool mmq_supported(int dtype) { return dtype == GGML_Q4K || dtype == GGML_Q6K; }
 
-MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus) {
+MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus, size_t max_part_elems) {
     MmqPlan p{};
     // 144-byte Q4_K blocks at a 16-byte aligned base allow the LDS DMA staging
     // (16-byte global_load_lds); it wins from M = 64 on (M = 512: 4-7%), the
@@ -699,6 +699,8 @@ MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus) {
 #undef FRQ_PLAN
         default: break;
     }
+    while (p.ks > 1 && (size_t)p.ks * M * N > max_part_elems) p.ks--;
+    p.part_elems = p.ks > 1 ? (size_t)p.ks * M * N : 0;
     return p;
 }
 

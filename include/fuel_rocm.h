@@ -134,6 +134,20 @@ int frq_qstorage_fwd_f16(const frq_qstorage *qs, size_t n, size_t k, const uint1
 int frq_qmatmul(frq_device *dev, int quant_type, size_t batch, size_t m, size_t n, size_t k,
                 const float *act_dev, size_t act_bytes, const uint32_t *w_dev, size_t w_bytes,
                 float *out_dev, size_t out_bytes);
+/* frq_qmatmul without any device allocation.  No counterpart in the
+ * reference: for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
+ * checks and results as frq_qmatmul; the quantized activation rows and the
+ * split-K partial sums live in a fixed 32 MiB device array per GPU instead
+ * of the handle's growable workspace (the K split is lowered until the
+ * partials fit).  A call whose quantized rows need more (about 1.14 * rows *
+ * k bytes for the k-quants, 1.125 * rows * k for Q8_0) fails with status 4
+ * (workspace).  Calls share that array: calls that overlap on one GPU (two
+ * streams, two threads) race, as does one that overlaps an frq_qmatmul_noalloc
+ * on another handle of the same GPU. */
+int frq_qmatmul_noalloc(frq_device *dev, int quant_type, size_t batch, size_t m, size_t n, size_t k,
+                        const float *act_dev, size_t act_bytes, const uint32_t *w_dev, size_t w_bytes,
+                        float *out_dev, size_t out_bytes);
 
 /* ---- MoE mul_mat_id ----
  * Routing (LazyMoeRouter::route, fuel-core/src/lazy_nn/moe.rs:90-127;
