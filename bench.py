@@ -317,6 +317,60 @@ def moe_leg():
     return res
 
 
+def probe_leg(k: int, n: int, dtype: int, m: int, reps_target: int = 200) -> dict:
+    """One QMatMul configuration alone (profiling runs): M rows x [N, K] of
+    `dtype`, weights rotated over >= 1.2 GB, graph-replayed, HIP-event timed."""
+    import ctypes as C
+
+    import fuel_amd as F
+    from fuel_amd.hiprt import HipRuntime
+
+    hip = HipRuntime()
+    dev = F.RocmDevice(0)
+    stream = hip.stream_create()
+    dev.set_stream(stream)
+    lib = F.lib()
+    w32 = F.fill_normal(dev, (n, k), SEED, 900, 0.0, 0.02)
+    q0 = dev.qzeros(n * k, dtype)
+    q0.quantize(w32)
+    dev.synchronize()
+    w32.free()
+    nbytes = q0.storage_size_in_bytes()
+    R = max(2, math.ceil(ROTATE_BYTES / nbytes))
+    ws = [q0]
+    for _ in range(R - 1):
+        q = dev.qzeros(n * k, dtype)
+        F._native.check(lib.frq_memcpy_dtod(dev.handle, C.c_void_p(q.device_ptr()), C.c_void_p(q0.device_ptr()),
+                                            nbytes))
+        ws.append(q)
+    x = F.fill_normal(dev, (m, k), SEED, 901)
+    y = dev.alloc((m, n), np.float32)
+
+    def call(i):
+        F._native.check(lib.frq_qmatmul(dev.handle, dtype, 1, m, n, k, C.c_void_p(x.ptr), x.nbytes,
+                                        C.c_void_p(ws[i % R].device_ptr()), nbytes, C.c_void_p(y.ptr), y.nbytes))
+
+    call(0)
+    dev.synchronize()
+    g = hip.capture(stream, lambda: [call(i) for i in range(R)])
+    hip.graph_launch(g, stream)
+    hip.stream_sync(stream)
+    reps = max(2, reps_target // R)
+    e0, e1 = hip.event_create(), hip.event_create()
+    hip.event_record(e0, stream)
+    for _ in range(reps):
+        hip.graph_launch(g, stream)
+    hip.event_record(e1, stream)
+    hip.event_sync(e1)
+    us = hip.elapsed_ms(e0, e1) * 1e3 / (reps * R)
+    hip.graph_destroy(g)
+    dev.close()
+    tops = 2.0 * m * n * k / us / 1e6
+    return {"probe": f"{k}x{n} dtype {dtype} M={m}", "us": round(us, 3), "TOPS": round(tops, 1),
+            "int8_peak_frac": round(tops / INT8_PEAK_TOPS, 4), "weight_GB_s": round(nbytes / us / 1e3, 1),
+            "calls": reps * R}
+
+
 DECODE_PROMPT = 512
 DECODE_NEW = 256
 
@@ -512,12 +566,18 @@ def main() -> int:
     ap.add_argument("--no-moe", action="store_true", help="skip the config-5 MoE leg")
     ap.add_argument("--no-q6k", action="store_true", help="skip the Q6_K sweep and Q6_K batched rows")
     ap.add_argument("--decode-only", action="store_true", help="run only the config-4 decode legs")
+    ap.add_argument("--probe", default=None, metavar="K,N,DTYPE,M",
+                    help="time one QMatMul configuration alone (profiling runs) and print its JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported "
               "(this build has no multi-GPU path; the sharding design is documented only)", file=sys.stderr)
         return 2
 
+    if args.probe:
+        k, n, dt, m = (int(v) for v in args.probe.split(","))
+        print(json.dumps(probe_leg(k, n, dt, m)), flush=True)
+        return 0
     global SHAPES
     if args.shape:
         SHAPES = [tuple(int(v) for v in sh.split("x")) for sh in args.shape]

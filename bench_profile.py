@@ -12,7 +12,13 @@ With --leg decode / batched / moe it instead runs one --kernel-trace --stats
 pass over that bench.py leg (config 4 decode + batched prompt, config 3
 M = 32/128/512 matmuls, config 5 MoE layer) and writes the per-kernel summary.
 
-Usage: python bench_profile.py [--shape 4096x32000] [--leg matvec|decode|batched|moe] [--out DIR]
+With --leg counters it runs a kernel trace and counter passes (instruction
+mix, MFMA busy and int8 MOPS, LDS conflicts, waits, HBM bytes) over one QMatMul
+configuration (`bench.py --probe K,N,DTYPE,M`) and summarises the kernel whose
+name contains --kernel.
+
+Usage: python bench_profile.py [--shape 4096x32000] [--leg matvec|counters|decode|batched|moe]
+                               [--probe K,N,DTYPE,M --kernel NAME] [--out DIR]
 """
 from __future__ import annotations
 
@@ -87,16 +93,90 @@ def trace_leg(leg: str, out: str, summarize_only: bool) -> int:
     return 0
 
 
+# Counter passes over one QMatMul configuration (bench.py --probe): at most
+# 8 SQ counters per pass; FETCH_SIZE and WRITE_SIZE in passes of their own.
+PMC_PASSES = [
+    "SQ_WAVES SQ_BUSY_CYCLES SQ_WAVE_CYCLES SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_LDS SQ_INSTS_SALU SQ_INSTS_VMEM_RD",
+    "SQ_WAIT_INST_LDS SQ_WAIT_INST_ANY SQ_VALU_MFMA_BUSY_CYCLES SQ_LDS_BANK_CONFLICT SQ_ACTIVE_INST_VALU "
+    "SQ_ACTIVE_INST_LDS SQ_INST_CYCLES_VMEM_RD SQ_INSTS_VALU_MFMA_MOPS_I8",
+    "FETCH_SIZE",
+    "WRITE_SIZE",
+]
+
+
+def counters_leg(probe: str, pattern: str, out: str, summarize_only: bool) -> int:
+    """Kernel trace + counter passes over `bench.py --probe K,N,DTYPE,M`,
+    summarised for the dispatches whose kernel name contains `pattern`."""
+    k, n, dt, m = (int(v) for v in probe.split(","))
+    name = f"counters_{k}x{n}_dt{dt}_m{m}"
+    base = ["python3", "bench.py", "--probe", probe]
+    cmds = {"trace": ["rocprofv3", "--kernel-trace", "--stats", "--output-format", "csv", "-d", f"{out}/{name}/trace",
+                      "-o", "run", "--"] + base}
+    for i, p in enumerate(PMC_PASSES):
+        cmds[f"pmc{i + 1}"] = ["rocprofv3", "--pmc"] + p.split() + ["--output-format", "csv", "-d",
+                                                                     f"{out}/{name}/pmc{i + 1}", "-o", "run", "--"] + base
+    if not summarize_only:
+        for key, c in cmds.items():
+            run(c, f"{out}/{name}_{key}.log", 240 if key == "trace" else 90)
+    durs = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+            for r in rows(f"{out}/{name}/trace", "run_kernel_trace.csv") if pattern in r["Kernel_Name"]]
+    per = {}
+    kname = ""
+    for i in range(len(PMC_PASSES)):
+        for r in rows(f"{out}/{name}/pmc{i + 1}", "run_counter_collection.csv"):
+            if pattern not in r["Kernel_Name"]:
+                continue
+            kname = r["Kernel_Name"]
+            per.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    med = {c: statistics.median(v) for c, v in per.items()}
+    avg_us = statistics.mean(durs) / 1e3 if durs else float("nan")
+    useful = 2.0 * m * n * k
+    res = {"probe": probe, "kernel_pattern": pattern, "kernel": kname[:160], "dispatches": len(durs),
+           "kernel_avg_us": round(avg_us, 3), "useful_TOPS": round(useful / avg_us / 1e6, 1),
+           "useful_int8_peak_frac": round(useful / avg_us / 1e6 / 5000.0, 4),
+           "counters_median_per_dispatch": med, "commands": {kk: " ".join(v) for kk, v in cmds.items()}}
+    mops = med.get("SQ_INSTS_VALU_MFMA_MOPS_I8")
+    if mops:  # MOPS counters count 512 ops per unit
+        res["mfma_int8_ops_per_dispatch"] = mops * 512
+        res["mfma_pipe_TOPS"] = round(mops * 512 / avg_us / 1e6, 1)
+        res["mfma_pipe_int8_peak_frac"] = round(mops * 512 / avg_us / 1e6 / 5000.0, 4)
+        res["mfma_ops_over_useful"] = round(mops * 512 / useful, 3)
+    json.dump(res, open(os.path.join(ROOT, out, f"{name}.json"), "w"), indent=1)
+    with open(os.path.join(ROOT, out, f"{name}.md"), "w") as f:
+        f.write(f"# Counters: QMatMul K x N = {k} x {n}, GGML dtype {dt}, M = {m}\n\n")
+        f.write(f"Made by `python3 bench_profile.py --leg counters --probe {probe} --kernel '{pattern}'` "
+                "(repository root, one MI355X), which runs:\n\n")
+        for kk, v in cmds.items():
+            f.write(f"- {kk}: `{' '.join(v)}`\n")
+        f.write(f"\nKernel: `{kname[:150]}`\n\n")
+        f.write(f"Trace: {len(durs)} dispatches, average {avg_us:.2f} us; useful 2MNK = {useful / 1e9:.2f} GOP "
+                f"-> {res['useful_TOPS']} TOPS = {100 * res['useful_int8_peak_frac']:.1f}% of the 5 POPS int8 "
+                "peak.\n\n")
+        if mops:
+            f.write(f"MFMA pipe: SQ_INSTS_VALU_MFMA_MOPS_I8 x 512 = {mops * 512 / 1e9:.2f} GOP per dispatch "
+                    f"({res['mfma_ops_over_useful']}x the useful ops) -> {res['mfma_pipe_TOPS']} TOPS = "
+                    f"{100 * res['mfma_pipe_int8_peak_frac']:.1f}% of peak.\n\n")
+        f.write("| counter | median per dispatch |\n|---|---|\n")
+        for c in sorted(med):
+            f.write(f"| {c} | {med[c]:.6g} |\n")
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--shape", default="4096x32000")
-    ap.add_argument("--leg", default="matvec", choices=["matvec"] + sorted(LEGS))
+    ap.add_argument("--leg", default="matvec", choices=["matvec", "counters"] + sorted(LEGS))
+    ap.add_argument("--probe", default="4096,11008,12,512", help="K,N,DTYPE,M for --leg counters")
+    ap.add_argument("--kernel", default="mmq", help="kernel-name substring for --leg counters")
     ap.add_argument("--out", default="gpurun_out/profiles")
     ap.add_argument("--summarize-only", action="store_true", help="re-read existing pass outputs")
     args = ap.parse_args()
     os.makedirs(os.path.join(ROOT, args.out), exist_ok=True)
     out = args.out  # relative to the repository root, where every pass runs
     os.environ.setdefault("TMPDIR", "/tmp")
+    if args.leg == "counters":
+        return counters_leg(args.probe, args.kernel, out, args.summarize_only)
     if args.leg != "matvec":
         return trace_leg(args.leg, out, args.summarize_only)
     bench = ["python3", "bench.py", "--shape", args.shape, "--steps", "50", "--warmup", "5", "--no-cpu",
