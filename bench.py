@@ -155,27 +155,36 @@ def gpu_leg(steps: int, warmup: int, q6k: bool = True):
     say(f"[bench] weights generated and quantized on device in {time.time() - t0:.1f}s; "
         f"copies per shape: {[len(m['ws']) for m in mats]}")
 
-    # one graph per rotation index: a step = the four QMatMuls
+    # A step is the four QMatMuls (one per shape, the next weight copy of
+    # each).  The warmup steps and the timed steps are each captured into one
+    # HIP graph and replayed back to back, the way per-shape times are taken:
+    # a graph per step would time the host's graph-launch submissions (about
+    # 7 us a step, more than the four kernels' launch gaps) instead of the GPU.
     R = max(len(m["ws"]) for m in mats)
     for m in mats:           # first launches outside capture (workspace sizing, lazy init)
         qmatmul_call(dev, m, 0)
     dev.synchronize()
-    graphs = [hip.capture(stream, lambda r=r: [qmatmul_call(dev, m, r) for m in mats]) for r in range(R)]
-    e0, e1 = hip.event_create(), hip.event_create()
 
-    for i in range(warmup):
-        hip.graph_launch(graphs[i % R], stream)
+    def steps_graph(first: int, count: int):
+        return hip.capture(stream, lambda: [qmatmul_call(dev, m, (first + i) % R)
+                                            for i in range(count) for m in mats])
+
+    e0, e1 = hip.event_create(), hip.event_create()
+    g_timed = steps_graph(warmup, steps)
+    if warmup > 0:
+        g_warm = steps_graph(0, warmup)
+        hip.graph_launch(g_warm, stream)
+        hip.stream_sync(stream)
+        hip.graph_destroy(g_warm)
     hip.stream_sync(stream)
     hip.event_record(e0, stream)
-    for i in range(steps):
-        hip.graph_launch(graphs[(warmup + i) % R], stream)
+    hip.graph_launch(g_timed, stream)
     hip.event_record(e1, stream)
     hip.event_sync(e1)
     ms_total = hip.elapsed_ms(e0, e1)
+    hip.graph_destroy(g_timed)
     ms_per_step = ms_total / steps
     step_bytes = sum(algo_bytes(m["k"], m["n"]) for m in mats)
-    for g in graphs:
-        hip.graph_destroy(g)
 
     per_shape = shape_times(hip, dev, stream, mats)
     batched = {}

@@ -95,6 +95,9 @@ def trace_leg(leg: str, out: str, summarize_only: bool) -> int:
 
 # Counter passes over one QMatMul configuration (bench.py --probe): at most
 # 8 SQ counters per pass; FETCH_SIZE and WRITE_SIZE in passes of their own.
+BLOCK_ELEMS = {8: 32, 12: 256, 14: 256}   # GGUF codes: Q8_0, Q4_K, Q6_K
+BLOCK_BYTES = {8: 34, 12: 144, 14: 210}
+
 PMC_PASSES = [
     "SQ_WAVES SQ_BUSY_CYCLES SQ_WAVE_CYCLES SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_LDS SQ_INSTS_SALU SQ_INSTS_VMEM_RD",
     "SQ_WAIT_INST_LDS SQ_WAIT_INST_ANY SQ_VALU_MFMA_BUSY_CYCLES SQ_LDS_BANK_CONFLICT SQ_ACTIVE_INST_VALU "
@@ -135,6 +138,20 @@ def counters_leg(probe: str, pattern: str, out: str, summarize_only: bool) -> in
            "kernel_avg_us": round(avg_us, 3), "useful_TOPS": round(useful / avg_us / 1e6, 1),
            "useful_int8_peak_frac": round(useful / avg_us / 1e6 / 5000.0, 4),
            "counters_median_per_dispatch": med, "commands": {kk: " ".join(v) for kk, v in cmds.items()}}
+    # HBM side: algorithmic bytes (weights + f32 x and y) against the FETCH_SIZE /
+    # WRITE_SIZE counters, scaled by the copy calibration (one FETCH_SIZE unit
+    # reads 2048 B, one WRITE_SIZE unit 1024 B on this MI355X)
+    wbytes = n * (k // BLOCK_ELEMS[dt]) * BLOCK_BYTES[dt]
+    algo = wbytes + 4 * m * k + 4 * m * n
+    res["algorithmic_bytes"] = algo
+    res["algorithmic_GB_s"] = round(algo / avg_us / 1e3, 1)
+    res["hbm_peak_frac"] = round(algo / avg_us / 1e3 / 8000.0, 4)
+    if "FETCH_SIZE" in med and "WRITE_SIZE" in med:
+        traffic = med["FETCH_SIZE"] * 2048 + med["WRITE_SIZE"] * 1024
+        res["hbm_traffic_bytes"] = round(traffic)
+        res["traffic_over_algorithmic"] = round(traffic / algo, 3)
+    if "SQ_BUSY_CYCLES" in med and "SQ_WAVE_CYCLES" in med and "SQ_WAIT_INST_ANY" in med:
+        res["wave_wait_frac"] = round(med["SQ_WAIT_INST_ANY"] / med["SQ_WAVE_CYCLES"], 4)
     mops = med.get("SQ_INSTS_VALU_MFMA_MOPS_I8")
     if mops:  # MOPS counters count 512 ops per unit
         res["mfma_int8_ops_per_dispatch"] = mops * 512
@@ -152,6 +169,14 @@ def counters_leg(probe: str, pattern: str, out: str, summarize_only: bool) -> in
         f.write(f"Trace: {len(durs)} dispatches, average {avg_us:.2f} us; useful 2MNK = {useful / 1e9:.2f} GOP "
                 f"-> {res['useful_TOPS']} TOPS = {100 * res['useful_int8_peak_frac']:.1f}% of the 5 POPS int8 "
                 "peak.\n\n")
+        f.write(f"HBM: algorithmic {algo / 1e6:.2f} MB (weights + f32 x, y) -> {res['algorithmic_GB_s']} GB/s = "
+                f"{100 * res['hbm_peak_frac']:.1f}% of 8 TB/s")
+        if "hbm_traffic_bytes" in res:
+            f.write(f"; counted traffic {res['hbm_traffic_bytes'] / 1e6:.2f} MB = {res['traffic_over_algorithmic']}x "
+                    "algorithmic (FETCH_SIZE x 2048 B + WRITE_SIZE x 1024 B, the copy calibration)")
+        f.write(".\n\n")
+        if "wave_wait_frac" in res:
+            f.write(f"Waves waiting (SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES): {100 * res['wave_wait_frac']:.1f}%.\n\n")
         if mops:
             f.write(f"MFMA pipe: SQ_INSTS_VALU_MFMA_MOPS_I8 x 512 = {mops * 512 / 1e9:.2f} GOP per dispatch "
                     f"({res['mfma_ops_over_useful']}x the useful ops) -> {res['mfma_pipe_TOPS']} TOPS = "

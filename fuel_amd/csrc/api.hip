@@ -310,7 +310,12 @@ int run_indexed(frq_device* dev, int t, const uint8_t* w, const float* x, size_t
         const size_t rows = M - m0 < step ? M - m0 : step;
         QmvOpts c = ix;
         const float* xc = x;
-        c.w_sel = ix.w_sel + m0;
+        c.w_sel = ix.w_sel ? ix.w_sel + m0 : nullptr;
+        if (ix.route_logits) {  // rows m0.. start on a token boundary (step is a multiple of x_div)
+            c.route_logits = ix.route_logits + m0 / ix.x_div * (size_t)ix.n_experts;
+            c.route_ids = ix.route_ids + m0;
+            c.route_w = ix.route_w + m0;
+        }
         if (ix.x_row) {
             c.x_row = ix.x_row + m0;
         } else {
@@ -318,7 +323,12 @@ int run_indexed(frq_device* dev, int t, const uint8_t* w, const float* x, size_t
             xc = x + xo;
             if (ix.x2) c.x2 = ix.x2 + xo;
         }
-        HIP_TRY(launch_qmv_indexed(t, w, xc, y + m0 * (size_t)ldy, (int)rows, N, K, ldy, c, dev->stream, dev->num_cus));
+        if (ix.route_logits)
+            HIP_TRY(launch_qmv_indexed_route(t, w, xc, y + m0 * (size_t)ldy, (int)rows, N, K, ldy, c, dev->stream,
+                                             dev->num_cus));
+        else
+            HIP_TRY(launch_qmv_indexed(t, w, xc, y + m0 * (size_t)ldy, (int)rows, N, K, ldy, c, dev->stream,
+                                       dev->num_cus));
     }
     return FRQ_OK;
 }
@@ -833,7 +843,7 @@ int frq_moe_ffn(frq_device* dev, int dt, size_t t, size_t d, size_t ffn, size_t 
         if ((rc = route_and_batch(dev, logits, t, e, topk, ids, wts, offsets, sorted_token, nullptr, entry_expert,
                                   entry_pos, tiles)))
             return rc;
-    } else {
+    } else if (e > (size_t)QMV_ROUTE_MAX_EXPERTS) {  // (with fewer experts the gate|up launch routes)
         HIP_TRY(launch_moe_route(logits, (int)t, (int)e, (int)topk, ids, wts, dev->stream));
     }
     const size_t gate_bytes = ffn * (d / bs) * type_size(dt);
@@ -875,9 +885,21 @@ int frq_moe_ffn(frq_device* dev, int dt, size_t t, size_t d, size_t ffn, size_t 
     gi.expert_bytes = gate_bytes;
     gi.w2 = static_cast<const uint8_t*>(w_up);
     gi.n_split = (int)ffn;
+    if (e <= (size_t)QMV_ROUTE_MAX_EXPERTS) {  // each workgroup routes its token from the logits
+        gi.w_sel = nullptr;
+        gi.route_logits = logits;
+        gi.route_ids = ids;
+        gi.route_w = wts;
+    }
     if ((rc = run_indexed(dev, dt, static_cast<const uint8_t*>(w_gate), x, p, (int)(2 * ffn), (int)d, gu,
                           (int)(2 * ffn), gi)))
         return rc;
+    // down over silu(gate) * up and the combine in one launch where it fits
+    if (moe_down_combine_supported(dt, (int)topk, (int)ffn)) {
+        HIP_TRY(launch_moe_down_combine(dt, static_cast<const uint8_t*>(w_down), down_bytes, (int)e, gu, ids, wts,
+                                        (int)t, (int)topk, (int)ffn, (int)d, out, dev->stream, dev->num_cus));
+        return FRQ_OK;
+    }
     // down over silu(gate) * up, quantized inside the mat-vec
     QmvOpts di{};
     di.x_row = nullptr;

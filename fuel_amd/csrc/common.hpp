@@ -192,11 +192,37 @@ __device__ __forceinline__ float scan_key(float v, int j) {
     return v != v ? (j == 0 ? __builtin_inff() : -__builtin_inff()) : v;
 }
 
+// (bitwise and selects: no branch or exec-mask juggling in the reductions)
 __device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
-    if (ov > v || (ov == v && oi < i)) {
-        v = ov;
-        i = oi;
+    const bool take = (ov > v) | ((ov == v) & (oi < i));
+    v = take ? ov : v;
+    i = take ? oi : i;
+}
+
+// Wave64 reduction of (key, index) pairs under argmax_merge's total order
+// (any tree gives the same pair): DPP row steps leave each 16-lane row's best
+// in its lanes, four readlanes combine the rows.  The result is wave-uniform.
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+#define FRQ_DPP_ARGMAX(ctrl)                                                                                     \
+    {                                                                                                           \
+        const float ov =                                                                                        \
+            __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false)); \
+        const int oi = __builtin_amdgcn_update_dpp(0, i, ctrl, 0xF, 0xF, false);                                 \
+        argmax_merge(v, i, ov, oi);                                                                             \
     }
+    FRQ_DPP_ARGMAX(0xB1);   // quad_perm [1,0,3,2]
+    FRQ_DPP_ARGMAX(0x4E);   // quad_perm [2,3,0,1]
+    FRQ_DPP_ARGMAX(0x141);  // row_half_mirror
+    FRQ_DPP_ARGMAX(0x140);  // row_mirror
+#undef FRQ_DPP_ARGMAX
+    float bv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    int bi = __builtin_amdgcn_readlane(i, 0);
+#pragma unroll
+    for (int r = 16; r < 64; r += 16)
+        argmax_merge(bv, bi, __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), r)),
+                     __builtin_amdgcn_readlane(i, r));
+    v = bv;
+    i = bi;
 }
 
 }  // namespace frq

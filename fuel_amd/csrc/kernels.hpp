@@ -56,9 +56,19 @@ struct QmvOpts {
     int attn_nsplit;
     int attn_max_ctx;
     const int* attn_pos;
+    // routing mode (launch_qmv_indexed_route): launch row m is slot m % x_div
+    // of token m / x_div, whose expert the workgroup picks itself from the
+    // token's router logits (n_experts <= 128 of them, x_div = topk); the
+    // workgroups with blockIdx.x = 0 store the picks and their weights
+    const float* route_logits;
+    int* route_ids;
+    float* route_w;
 };
 hipError_t launch_qmv_indexed(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
                               const QmvOpts& ix, hipStream_t s, int num_cus);
+hipError_t launch_qmv_indexed_route(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K,
+                                    int ldy, const QmvOpts& ix, hipStream_t s, int num_cus);
+constexpr int QMV_ROUTE_MAX_EXPERTS = 128;
 hipError_t launch_qmv_fused(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
                             const QmvOpts& o, hipStream_t s, int num_cus);
 // y [M, N] = silu(Wg a(x)) * (Wu a(x)), a(x) as launch_qmv_fused (RMS norm
@@ -99,6 +109,15 @@ hipError_t launch_moe_batches(const int* ids, int P, int E, int topk, int* offse
                               hipStream_t s);
 hipError_t launch_moe_combine(const float* yd, const int* ids, const float* w, const int* entry_pos, int T, int topk,
                               int d, float* out, hipStream_t s);
+// The down projection and the combine in one launch for the mat-vec path:
+// out [T, d] from gu [T * topk, 2 ffn] (gate | up per routed entry, routing
+// order), ids / w [T, topk] and the experts' down matrices [d, ffn]
+// (expert_bytes apart).  Supported for Q4_K / Q6_K / Q8_0 when an entry's
+// blocks fit 32 lanes and topk and the activation rows fit its instantiations.
+bool moe_down_combine_supported(int dtype, int topk, int ffn);
+hipError_t launch_moe_down_combine(int dtype, const uint8_t* w, size_t expert_bytes, int E, const float* gu,
+                                   const int* ids, const float* wts, int T, int topk, int ffn, int d, float* out,
+                                   hipStream_t s, int num_cus);
 // mmq_skinny.hip: int8-MFMA matmul for a few rows (activations already
 // quantized into the workspace, Q8K for the k-quants, Q8_0 for Q8_0), each
 // weight block read once for every row group of up to 32 rows; y [M, N] with

@@ -20,6 +20,7 @@
 #include "kernels.hpp"
 #include "q8.hpp"
 #include "qmv.hpp"
+#include "route.hpp"
 
 namespace frq {
 
@@ -33,6 +34,8 @@ namespace frq {
 // with the run-time choice of activation loader compiled out, nothing merges
 // registers at a join, so the first weight rows are requested before the
 // activation row has arrived).
+// QMV_INDEXED_ROUTE: QMV_INDEXED with the expert of each launch row picked in
+// the workgroup from the token's router logits (route.hpp).
 enum QmvMode {
     QMV_PLAIN = 0,
     QMV_INDEXED = 1,
@@ -40,7 +43,8 @@ enum QmvMode {
     QMV_HALF = 3,
     QMV_ATTN = 4,
     QMV_GLU = 5,
-    QMV_FUSED_NOX = 6
+    QMV_FUSED_NOX = 6,
+    QMV_INDEXED_ROUTE = 7
 };
 
 // Activation stage of QMV_ATTN: lane `lane`'s four elements of chunk
@@ -119,7 +123,8 @@ __device__ __forceinline__ float block_sum_waves(float v, float* s_red, int w, i
 template <class F, int SPL, int WG, int MODE, int RPW = 1>
 __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const float* __restrict__ x,
                                          float* __restrict__ y, int N, int K, int ldy, const QmvOpts& ix, int bx,
-                                         int gxn, uint8_t* smem, float* s_red) {
+                                         int gxn, uint8_t* smem, float* s_red, float* s_rt = nullptr,
+                                         int* s_pick = nullptr) {
     constexpr int NW = WG / 64;
     const int m = blockIdx.y;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -151,6 +156,13 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
             W2 = ix.w2 + eoff;
             n_split = ix.n_split;
         }
+    }
+    float lv = 0.0f;  // (QMV_INDEXED_ROUTE: logit threadIdx.x of the token, loaded before the activation row)
+    if constexpr (MODE == QMV_INDEXED_ROUTE) {
+        const int li = (int)threadIdx.x < ix.n_experts ? (int)threadIdx.x : ix.n_experts - 1;
+        lv = attn_load_early(ix.route_logits + (size_t)(m / ix.x_div) * ix.n_experts + li);
+        xr = x + (size_t)(m / ix.x_div) * ix.ldx;
+        if (ix.w2) n_split = ix.n_split;
     }
     if constexpr (MODE == QMV_FUSED || MODE == QMV_GLU || MODE == QMV_FUSED_NOX) {
         const size_t xo = (size_t)m * ix.ldx;
@@ -184,6 +196,37 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
     else
         act_row_load<F::ACT, NW, MAXQ>(xr, K, w, lane, pre);
     __builtin_amdgcn_sched_barrier(0);  // the activation loads go out ahead of the weight loads
+    if constexpr (MODE == QMV_INDEXED_ROUTE) {
+        // wavefront 0 runs the token's routing rounds (a serial chain: copies
+        // in every wavefront would only compete for the SIMDs) while the
+        // activation loads are in flight, and hands the picks to the others
+        // through LDS; workgroups with blockIdx.x = 0 also store the launch
+        // row's pick and its softmax weight
+        const int E = ix.n_experts, topk = ix.x_div, slot = m % topk;
+        if ((int)threadIdx.x < E) s_rt[threadIdx.x] = lv;
+        __syncthreads();
+        if (w == 0) {
+            RouteRow<2> rrow;
+#pragma unroll
+            for (int i = 0; i < 2; i++) rrow.v[i] = s_rt[lane + 64 * i < E ? lane + 64 * i : E - 1];
+            int id;
+            float wv;
+            route_topk<2>(rrow, E, topk, lane, id, wv);
+            if (lane < topk) s_pick[lane] = id;
+        }
+        __syncthreads();
+        const int sel = __builtin_amdgcn_readfirstlane(s_pick[slot]);
+        if (bx == 0 && w == 0) {
+            const float wv = route_softmax(lane < topk ? s_rt[s_pick[lane < topk ? lane : 0]] : 0.0f, topk, lane);
+            if (lane == slot) {
+                ix.route_ids[m] = sel;
+                ix.route_w[m] = wv;
+            }
+        }
+        const size_t eoff = (size_t)sel * ix.expert_bytes;
+        W += eoff;
+        if (ix.w2) W2 = ix.w2 + eoff;
+    }
     // rows >= n_split live in the second matrix (row - n_split)
     auto wrow = [&](int r) { return r < n_split ? W + (size_t)r * row_bytes : W2 + (size_t)(r - n_split) * row_bytes; };
     typename F::Raw ra[SPL], rb[SPL];
@@ -311,7 +354,13 @@ __global__ __launch_bounds__(WG) void qmv_kernel(const uint8_t* __restrict__ W, 
                                                  float* __restrict__ y, int N, int K, int ldy, QmvOpts ix) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float s_red[WG / 64];
-    qmv_body<F, SPL, WG, MODE, RPW>(W, x, y, N, K, ldy, ix, blockIdx.x, gridDim.x, smem, s_red);
+    if constexpr (MODE == QMV_INDEXED_ROUTE) {  // the token's logits and picks
+        __shared__ __align__(16) float s_rt[QMV_ROUTE_MAX_EXPERTS];
+        __shared__ int s_pick[QMV_ROUTE_MAX_EXPERTS];
+        qmv_body<F, SPL, WG, MODE, RPW>(W, x, y, N, K, ldy, ix, blockIdx.x, gridDim.x, smem, s_red, s_rt, s_pick);
+    } else {
+        qmv_body<F, SPL, WG, MODE, RPW>(W, x, y, N, K, ldy, ix, blockIdx.x, gridDim.x, smem, s_red);
+    }
 }
 
 // Two matrices of the same activation rows in one launch: workgroups
@@ -473,6 +522,13 @@ hipError_t launch_qmv(int dtype, const uint8_t* w, const float* x, float* y, int
 hipError_t launch_qmv_indexed(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
                               const QmvOpts& ix, hipStream_t s, int num_cus) {
     return launch_dtype<QMV_INDEXED>(dtype, w, x, y, M, N, K, ldy, ix, s, num_cus);
+}
+
+hipError_t launch_qmv_indexed_route(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K,
+                                    int ldy, const QmvOpts& ix, hipStream_t s, int num_cus) {
+    if (ix.n_experts < 1 || ix.n_experts > QMV_ROUTE_MAX_EXPERTS || ix.x_div < 1 || ix.x_div > ix.n_experts)
+        return hipErrorInvalidValue;
+    return launch_dtype<QMV_INDEXED_ROUTE>(dtype, w, x, y, M, N, K, ldy, ix, s, num_cus);
 }
 
 hipError_t launch_qmv_half(int dtype, const uint8_t* w, const uint16_t* x, uint16_t* y, int M, int N, int K, int ldy,

@@ -14,8 +14,12 @@
 //             ascending order, product then sum).
 #include <hip/hip_runtime.h>
 
+#include "attn.hpp"
 #include "common.hpp"
+#include "formats.hpp"
 #include "kernels.hpp"
+#include "q8.hpp"
+#include "route.hpp"
 
 namespace frq {
 
@@ -29,58 +33,14 @@ __global__ __launch_bounds__(ROUTE_WG) void moe_route_kernel(const float* __rest
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * (ROUTE_WG / 64) + (threadIdx.x >> 6);
     if (t >= T) return;  // whole wavefront
-    const float* lr = logits + (size_t)t * E;
-    float v[EPL], orig[EPL];  // element j = lane + 64 i (orig: as loaded, for the softmax)
-#pragma unroll
-    for (int i = 0; i < EPL; i++) {
-        const int j = lane + 64 * i;
-        orig[i] = lr[j < E ? j : E - 1];
-        v[i] = orig[i];
-    }
-    int my_id = 0;       // lane s < topk keeps the s-th pick
-    float my_val = 0.0f; // and its original logit
-    for (int s = 0; s < topk; s++) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-#pragma unroll
-        for (int i = 0; i < EPL; i++) {
-            const int j = lane + 64 * i;
-            if (j < E) argmax_merge(bv, bi, scan_key(v[i], j), j);
-        }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            const float ov = __shfl_xor(bv, off);
-            const int oi = __shfl_xor(bi, off);
-            argmax_merge(bv, bi, ov, oi);
-        }
-        float pv = 0.0f;  // the pick's original logit, from its owner lane
-#pragma unroll
-        for (int i = 0; i < EPL; i++) {
-            const float o = __shfl(orig[i], bi & 63);
-            if ((bi >> 6) == i) pv = o;
-        }
-        if (lane == s) {
-            my_id = bi;
-            my_val = pv;
-        }
-#pragma unroll
-        for (int i = 0; i < EPL; i++)
-            if (lane + 64 * i == bi) v[i] += -1e30f;
-    }
-    // softmax over the picked (original) logits, in pick order
-    const float p = lane < topk ? my_val : 0.0f;
-    float mx = __shfl(p, 0);
-    for (int s = 1; s < topk; s++) {
-        const float ps = __shfl(p, s);
-        if (ps > mx) mx = ps;
-    }
-    const float ex = lane < topk ? expf(p - mx) : 0.0f;
-    float sum = 0.0f;
-    for (int s = 0; s < topk; s++) sum += __shfl(ex, s);
-    const float inv = 1.0f / sum;
+    RouteRow<EPL> row;
+    route_load<EPL>(logits + (size_t)t * E, E, lane, row);
+    int id;
+    float wv;
+    route_topk<EPL>(row, E, topk, lane, id, wv);
     if (lane < topk) {
-        ids[(size_t)t * topk + lane] = my_id;
-        wts[(size_t)t * topk + lane] = ex * inv;
+        ids[(size_t)t * topk + lane] = id;
+        wts[(size_t)t * topk + lane] = wv;
     }
 }
 
@@ -233,6 +193,247 @@ __global__ __launch_bounds__(COMBINE_WG) void moe_combine_kernel(const float* __
     }
 }
 
+// ---- down projection + combine, few tokens ----
+
+constexpr int DC_NW = 8;  // wavefronts per workgroup
+
+template <int SEG>
+__device__ __forceinline__ float seg_total(float v) {  // valid in the segment's last lane
+    if constexpr (SEG == 16) return dpp_seg_sum<4>(v);
+    else if constexpr (SEG == 32) return dpp_seg_sum<2>(v);
+    else return dpp_wave_sum(v);
+}
+
+// out[t, n] = sum over token t's entries in ascending expert order (equal
+// experts in slot order) of w * (W_e[n] . q8(silu(g) * u)), the sum starting
+// from 0 with each product rounded before it is added: the indexed down
+// mat-vec and moe_combine_kernel in one launch.  A workgroup quantizes the
+// token's topk activation rows silu(g) * u (gu [P, 2 ffn], row t * topk +
+// slot) into LDS; a wavefront takes output rows n with SEG lanes per entry
+// (the entry's ffn / ELEMS blocks, LPB lanes each) and 64 / SEG entries per
+// pass.  The combine order is worked out in registers from the token's ids
+// (no LDS round trip), so the first row's weight loads go out before the
+// activation quantize.  An expert id outside [0, E) gives a NaN product (its
+// loads read expert 0).
+template <class F, int SEG, int NPASS, int MAXQ>
+__global__ __launch_bounds__(64 * DC_NW) void moe_down_combine_kernel(const uint8_t* __restrict__ W,
+                                                                      size_t expert_bytes, int E,
+                                                                      const float* __restrict__ gu,
+                                                                      const int* __restrict__ ids,
+                                                                      const float* __restrict__ wts, int topk,
+                                                                      int ffn, int d, float* __restrict__ out) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int SPP = 64 / SEG;
+    const int t = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const ActLds lay = act_lds_layout(F::ACT, ffn);
+    const int abytes = align16i(lay.bytes);
+    const int nch = (ffn + QK_K - 1) / QK_K;
+    const int total = topk * nch;
+    const float* gt = gu + (size_t)t * topk * 2 * ffn;
+
+    // 1. the token's ids and weights (lane l < topk: entry l), then every
+    //    activation load of the wavefront's chunks (entry s, chunk lc)
+    const int li = lane < topk ? lane : topk - 1;
+    const int my_e = __float_as_int(attn_load_early(reinterpret_cast<const float*>(ids + (size_t)t * topk + li)));
+    const float my_w = attn_load_early(wts + (size_t)t * topk + li);
+    float4 g[MAXQ], u[MAXQ];
+#pragma unroll
+    for (int i = 0; i < MAXQ; i++) {
+        const int c = w + DC_NW * i;
+        const int cc = c < total ? c : total - 1;
+        const int s = cc / nch, lc = cc - s * nch;
+        const float* row = gt + (size_t)s * 2 * ffn + act_elem(lc, nch, ffn, lane);
+        g[i] = load_f4_early(row);
+        u[i] = load_f4_early(row + ffn);
+    }
+    // 2. combine order: entry l's rank among the token's entries (ascending
+    //    expert, equal experts in slot order); rank r's entry by ballot
+    int my_rank = 0;
+    for (int s = 0; s < topk; s++) {
+        const int es = __builtin_amdgcn_readlane(my_e, s);
+        my_rank += es < my_e || (es == my_e && s < lane);
+    }
+    auto entry_of_rank = [&](int r) {  // r < topk, wave-uniform
+        return (int)__builtin_ctzll(__ballot(lane < topk && my_rank == r));
+    };
+    const int seg = lane / SEG, sl = lane % SEG;
+    const int KB = ffn / F::ELEMS;
+    const size_t row_bytes = (size_t)KB * F::BYTES;
+    const int gb = sl / F::LPB, c = sl % F::LPB;
+    const int bl = gb < KB ? gb : KB - 1;
+    int p_slot[NPASS], p_exp[NPASS];  // this lane's entry in each pass (its segment's rank)
+#pragma unroll
+    for (int q = 0; q < NPASS; q++) {
+        int sl_q = 0;
+#pragma unroll
+        for (int j = 0; j < SPP; j++) {
+            const int r = q * SPP + j;
+            const int sj = entry_of_rank(r < topk ? r : topk - 1);
+            if (seg == j) sl_q = sj;
+        }
+        p_slot[q] = sl_q;
+        p_exp[q] = __builtin_amdgcn_ds_bpermute(4 * sl_q, my_e);
+    }
+    int n = blockIdx.x * DC_NW + w;
+    auto load_row = [&](int nn, typename F::Raw(&raw)[NPASS]) {
+#pragma unroll
+        for (int q = 0; q < NPASS; q++) {
+            const int ev = (unsigned)p_exp[q] < (unsigned)E ? p_exp[q] : 0;
+            F::load(W + (size_t)ev * expert_bytes + (size_t)nn * row_bytes + (size_t)bl * F::BYTES, c, raw[q]);
+        }
+    };
+    typename F::Raw raw[NPASS];
+    load_row(n < d ? n : d - 1, raw);
+
+    // 3. silu(g) * u, quantized into the entry's LDS row
+#pragma unroll
+    for (int i = 0; i < MAXQ; i++) {
+        const int cq = w + DC_NW * i;
+        if (cq >= total) break;
+        const int s = cq / nch, lc = cq - s * nch;
+        const float4 v = make_float4(silu_mul(g[i].x, u[i].x), silu_mul(g[i].y, u[i].y), silu_mul(g[i].z, u[i].z),
+                                     silu_mul(g[i].w, u[i].w));
+        uint8_t* base = smem + (size_t)s * abytes;
+        act_chunk_quantize<F::ACT>(v, lc, ffn, reinterpret_cast<int8_t*>(base), lay.qstride,
+                                   reinterpret_cast<float*>(base + lay.off_d), reinterpret_cast<int16_t*>(base + lay.off_bs),
+                                   lane);
+    }
+    __syncthreads();
+
+    // 4. output rows, a two-row register ring: the next row's loads are in
+    //    flight while a row is reduced (past the last row a wavefront re-reads
+    //    its current row rather than branching around the loads)
+    auto reduce_row = [&](int nn, const typename F::Raw(&rr)[NPASS]) {
+        float y[NPASS];
+#pragma unroll
+        for (int q = 0; q < NPASS; q++) {
+            const uint8_t* base = smem + (size_t)p_slot[q] * abytes;
+            float acc = 0.0f;
+            if (gb < KB) {
+                typename F::Act xa;
+                F::load_act(reinterpret_cast<const int8_t*>(base), lay.qstride,
+                            reinterpret_cast<const float*>(base + lay.off_d),
+                            reinterpret_cast<const int16_t*>(base + lay.off_bs), gb, c, xa);
+                int isum, msum;
+                float dw, dmw;
+                F::dot(rr[q], xa, c, isum, msum, dw, dmw);
+                acc = fmaf(dw * xa.d, (float)isum, acc);
+                acc = fmaf(-(dmw * xa.d), (float)msum, acc);
+            }
+            y[q] = seg_total<SEG>(acc);
+        }
+        float o = 0.0f;
+#pragma unroll
+        for (int q = 0; q < NPASS; q++)
+#pragma unroll
+            for (int j = 0; j < SPP; j++) {
+                const int r = q * SPP + j;
+                if (r < topk) {
+                    const int sr = entry_of_rank(r);
+                    float yr = __builtin_bit_cast(float,
+                                                  __builtin_amdgcn_readlane(__builtin_bit_cast(int, y[q]), j * SEG + SEG - 1));
+                    if ((unsigned)__builtin_amdgcn_readlane(my_e, sr) >= (unsigned)E) yr = __builtin_nanf("");
+                    const float wr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_w), sr));
+                    o = o + yr * wr;
+                }
+            }
+        if (lane == 0) out[(size_t)t * d + nn] = o;
+    };
+    const int stride = gridDim.x * DC_NW;
+    typename F::Raw rb[NPASS];
+    while (n < d) {
+        int nn = n + stride;
+        load_row(nn < d ? nn : n, rb);
+        reduce_row(n, raw);
+        n = nn;
+        if (n >= d) break;
+        nn = n + stride;
+        load_row(nn < d ? nn : n, raw);
+        reduce_row(n, rb);
+        n = nn;
+    }
+}
+
+// Launch shape of the fused down + combine: lanes per entry (SEG), passes
+// (NPASS) and activation chunks per wavefront (MAXQ); false when the layer
+// is outside what it is instantiated for.
+struct DcShape {
+    int seg, npass, maxq;
+    size_t lds;
+};
+
+bool dc_shape(int dtype, int topk, int ffn, DcShape& sh) {
+    int lpb, elems;
+    if (dtype == GGML_Q4K || dtype == GGML_Q6K) {
+        lpb = 4;
+        elems = QK_K;
+    } else if (dtype == GGML_Q8_0) {
+        lpb = 2;
+        elems = QK8_0;
+    } else {
+        return false;
+    }
+    if (topk < 1 || topk > MOE_MAX_TOPK || ffn < elems || ffn % elems) return false;
+    const int lanes = lpb * (ffn / elems);
+    sh.seg = lanes <= 16 ? 16 : lanes <= 32 ? 32 : 0;
+    if (!sh.seg) return false;
+    const int passes = (topk + 64 / sh.seg - 1) / (64 / sh.seg);
+    sh.npass = passes <= 1 ? 1 : passes <= 2 ? 2 : passes <= 4 ? 4 : 0;
+    const int q = (topk * ((ffn + QK_K - 1) / QK_K) + DC_NW - 1) / DC_NW;
+    sh.maxq = q <= 1 ? 1 : q <= 2 ? 2 : q <= 4 ? 4 : 0;
+    sh.lds = (size_t)topk * align16i(act_lds_layout(dtype == GGML_Q8_0 ? GGML_Q8_0 : GGML_Q8K, ffn).bytes);
+    return sh.npass && sh.maxq && sh.lds <= 65536;
+}
+
+template <class F, int SEG, int NPASS, int MAXQ>
+hipError_t launch_dc(const DcShape& sh, const uint8_t* w, size_t eb, int E, const float* gu, const int* ids,
+                     const float* wts, int T, int topk, int ffn, int d, float* out, hipStream_t s, int num_cus) {
+    static int occ = -1;
+    if (occ < 0) {
+        int o = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, moe_down_combine_kernel<F, SEG, NPASS, MAXQ>, 64 * DC_NW,
+                                                         sh.lds) != hipSuccess ||
+            o < 1)
+            o = 1;
+        occ = o;
+    }
+    const int need = (d + DC_NW - 1) / DC_NW;
+    int cap = num_cus * occ / T;
+    if (cap < 1) cap = 1;
+    hipLaunchKernelGGL((moe_down_combine_kernel<F, SEG, NPASS, MAXQ>), dim3(need < cap ? need : cap, T),
+                       dim3(64 * DC_NW), sh.lds, s, w, eb, E, gu, ids, wts, topk, ffn, d, out);
+    return hipGetLastError();
+}
+
+template <class F, int SEG, int NPASS>
+hipError_t launch_dc_q(const DcShape& sh, const uint8_t* w, size_t eb, int E, const float* gu, const int* ids,
+                       const float* wts, int T, int topk, int ffn, int d, float* out, hipStream_t s, int num_cus) {
+    switch (sh.maxq) {
+        case 1: return launch_dc<F, SEG, NPASS, 1>(sh, w, eb, E, gu, ids, wts, T, topk, ffn, d, out, s, num_cus);
+        case 2: return launch_dc<F, SEG, NPASS, 2>(sh, w, eb, E, gu, ids, wts, T, topk, ffn, d, out, s, num_cus);
+        default: return launch_dc<F, SEG, NPASS, 4>(sh, w, eb, E, gu, ids, wts, T, topk, ffn, d, out, s, num_cus);
+    }
+}
+
+template <class F, int SEG>
+hipError_t launch_dc_p(const DcShape& sh, const uint8_t* w, size_t eb, int E, const float* gu, const int* ids,
+                       const float* wts, int T, int topk, int ffn, int d, float* out, hipStream_t s, int num_cus) {
+    switch (sh.npass) {
+        case 1: return launch_dc_q<F, SEG, 1>(sh, w, eb, E, gu, ids, wts, T, topk, ffn, d, out, s, num_cus);
+        case 2: return launch_dc_q<F, SEG, 2>(sh, w, eb, E, gu, ids, wts, T, topk, ffn, d, out, s, num_cus);
+        default: return launch_dc_q<F, SEG, 4>(sh, w, eb, E, gu, ids, wts, T, topk, ffn, d, out, s, num_cus);
+    }
+}
+
+template <class F>
+hipError_t launch_dc_f(const DcShape& sh, const uint8_t* w, size_t eb, int E, const float* gu, const int* ids,
+                       const float* wts, int T, int topk, int ffn, int d, float* out, hipStream_t s, int num_cus) {
+    return sh.seg == 16 ? launch_dc_p<F, 16>(sh, w, eb, E, gu, ids, wts, T, topk, ffn, d, out, s, num_cus)
+                        : launch_dc_p<F, 32>(sh, w, eb, E, gu, ids, wts, T, topk, ffn, d, out, s, num_cus);
+}
+
 }  // namespace
 
 hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int* ids, float* w, hipStream_t s) {
@@ -274,6 +475,24 @@ hipError_t launch_moe_combine(const float* yd, const int* ids, const float* w, c
     const int gy = (d4 + COMBINE_WG - 1) / COMBINE_WG;
     hipLaunchKernelGGL(moe_combine_kernel, dim3(T, gy), dim3(COMBINE_WG), 0, s, yd, ids, w, entry_pos, topk, d, out);
     return hipGetLastError();
+}
+
+bool moe_down_combine_supported(int dtype, int topk, int ffn) {
+    DcShape sh;
+    return dc_shape(dtype, topk, ffn, sh);
+}
+
+hipError_t launch_moe_down_combine(int dtype, const uint8_t* w, size_t expert_bytes, int E, const float* gu,
+                                   const int* ids, const float* wts, int T, int topk, int ffn, int d, float* out,
+                                   hipStream_t s, int num_cus) {
+    DcShape sh;
+    if (!dc_shape(dtype, topk, ffn, sh) || T < 0 || d < 1) return hipErrorInvalidValue;
+    if (T == 0) return hipSuccess;
+    switch (dtype) {
+        case GGML_Q4K: return launch_dc_f<Q4K>(sh, w, expert_bytes, E, gu, ids, wts, T, topk, ffn, d, out, s, num_cus);
+        case GGML_Q6K: return launch_dc_f<Q6K>(sh, w, expert_bytes, E, gu, ids, wts, T, topk, ffn, d, out, s, num_cus);
+        default: return launch_dc_f<Q80>(sh, w, expert_bytes, E, gu, ids, wts, T, topk, ffn, d, out, s, num_cus);
+    }
 }
 
 }  // namespace frq

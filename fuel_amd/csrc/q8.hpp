@@ -237,6 +237,26 @@ __device__ __forceinline__ void act_row_rms_norm(ActRowPre<MAXQ>& p, const float
     }
 }
 
+// Chunk `ch` (256 elements: one Q8K superblock or eight Q8_0 blocks) of an
+// activation row of K elements, lane `lane` holding elements 4*lane.. of it.
+template <int ACT>
+__device__ __forceinline__ void act_chunk_quantize(const float4 v, int ch, int K, int8_t* qs, int qstride, float* dv,
+                                                   int16_t* bsums, int lane) {
+    if constexpr (ACT == GGML_Q8K) {
+        const Q8KWave r = q8k_quantize_vals(v, lane);
+        reinterpret_cast<uint32_t*>(qs + (size_t)ch * qstride)[lane] = r.packed;
+        if ((lane & 3) == 0) bsums[ch * 16 + (lane >> 2)] = (int16_t)r.bsum;
+        if (lane == 0) dv[ch] = r.d;
+    } else {
+        const Q80Wave r = q8_0_quantize_vals(v, lane);
+        const int blk = ch * 8 + (lane >> 3);
+        if (blk < K / QK8_0) {
+            reinterpret_cast<uint32_t*>(qs + (size_t)blk * qstride)[lane & 7] = r.packed;
+            if ((lane & 7) == 0) dv[blk] = f16_to_f32(r.dbits);
+        }
+    }
+}
+
 template <int ACT, int NW, int MAXQ>
 __device__ __forceinline__ void act_row_quantize(const ActRowPre<MAXQ>& p, int K, int8_t* qs, int qstride,
                                                  float* dv, int16_t* bsums, int w, int lane) {
@@ -245,19 +265,7 @@ __device__ __forceinline__ void act_row_quantize(const ActRowPre<MAXQ>& p, int K
     for (int i = 0; i < MAXQ; i++) {
         const int ch = w + NW * i;
         if (ch >= nchunks) break;
-        if constexpr (ACT == GGML_Q8K) {
-            const Q8KWave r = q8k_quantize_vals(p.v[i], lane);
-            reinterpret_cast<uint32_t*>(qs + (size_t)ch * qstride)[lane] = r.packed;
-            if ((lane & 3) == 0) bsums[ch * 16 + (lane >> 2)] = (int16_t)r.bsum;
-            if (lane == 0) dv[ch] = r.d;
-        } else {
-            const Q80Wave r = q8_0_quantize_vals(p.v[i], lane);
-            const int blk = ch * 8 + (lane >> 3);
-            if (blk < K / QK8_0) {
-                reinterpret_cast<uint32_t*>(qs + (size_t)blk * qstride)[lane & 7] = r.packed;
-                if ((lane & 7) == 0) dv[blk] = f16_to_f32(r.dbits);
-            }
-        }
+        act_chunk_quantize<ACT>(p.v[i], ch, K, qs, qstride, dv, bsums, lane);
     }
 }
 

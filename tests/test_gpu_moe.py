@@ -158,6 +158,8 @@ def device_experts(dev, dt, e, rows, cols, seed, stream):
     (5, 256, 512, 6, 2, O.Q4K),
     (9, 512, 256, 10, 3, O.Q6K),
     (11, 256, 512, 7, 2, O.Q8_0),
+    (2, 256, 8192, 4, 2, O.Q4K),          # an entry's blocks past 32 lanes: indexed down + combine kernel
+    (1, 512, 256, 300, 16, O.Q4K),        # 16 entries: four passes of the fused down + combine
 ])
 def test_moe_ffn(dev, t, d, ffn, e, k, dt):
     say("moe_ffn", t, d, ffn, e, k, dt)
