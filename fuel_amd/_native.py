@@ -63,6 +63,7 @@ SIGNATURES = {
     "frq_qstorage_dequantize": (_i32, [_vp, _sz, _vp]),
     "frq_qstorage_dequantize_f16": (_i32, [_vp, _sz, _vp]),
     "frq_qstorage_quantize": (_i32, [_vp, _vp, _sz]),
+    "frq_qstorage_quantize_imatrix": (_i32, [_vp, _vp, _sz, _vp, _sz]),
     "frq_qstorage_fwd": (_i32, [_vp, _sz, _sz, _vp, _sz, _vp]),
     "frq_qstorage_fwd_f16": (_i32, [_vp, _sz, _sz, _vp, _sz, _vp]),
     "frq_qmatmul": (_i32, [_vp, _i32, _sz, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz]),

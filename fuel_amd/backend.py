@@ -193,6 +193,20 @@ class RocmQStorage:
             raise FuelRocmError(N.FRQ_INVALID, f"quantize: expected f32 source, got {src.dtype}")
         check(lib().frq_qstorage_quantize(self._h, C.c_void_p(src.ptr), src.nbytes // 4))
 
+    def quantize_imatrix(self, src: RocmStorage, imatrix_weights, n_per_row: int) -> None:
+        """from_float_imatrix of a device f32 source onto this storage
+        (quantize_imatrix / quantize_imatrix_onto of the trait seam): Q4_K and
+        Q6_K; imatrix_weights is a host sequence of n_per_row f32 weights."""
+        if src.dtype != np.float32:
+            raise FuelRocmError(N.FRQ_INVALID, f"quantize_imatrix: expected f32 source, got {src.dtype}")
+        w = np.ascontiguousarray(imatrix_weights, dtype=np.float32)
+        if w.size < n_per_row:
+            raise FuelRocmError(N.FRQ_INVALID, f"quantize_imatrix: {w.size} weights for n_per_row={n_per_row}")
+        check(lib().frq_qstorage_quantize_imatrix(self._h, C.c_void_p(src.ptr), src.nbytes // 4,
+                                                  w.ctypes.data_as(C.c_void_p), n_per_row))
+
+    quantize_imatrix_onto = quantize_imatrix
+
     def fwd(self, self_shape: Sequence[int], inp: RocmStorage):
         """QMatMul forward: input [..., k] -> fresh output [..., n]
         (fuel-cpu-backend/src/quantized.rs:85-142 semantics): f32 input gives

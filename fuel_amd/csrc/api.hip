@@ -617,6 +617,33 @@ int frq_qstorage_quantize(frq_qstorage* q, const float* src, size_t elem_count) 
     return FRQ_OK;
 }
 
+int frq_qstorage_quantize_imatrix(frq_qstorage* q, const float* src, size_t elem_count, const float* imatrix,
+                                  size_t n_per_row) {
+    if (!q) return fail(FRQ_INVALID, "null storage");
+    int rc = use_device(q->dev);
+    if (rc) return rc;
+    if (q->dtype != GGML_Q4K && q->dtype != GGML_Q6K)
+        return fail(FRQ_UNSUPPORTED, "quantize_imatrix: from_float_imatrix is not implemented for dtype %d", q->dtype);
+    const size_t blocks = q->nbytes / type_size(q->dtype);
+    if (elem_count != blocks * QK_K)
+        return fail(FRQ_INVALID, "quantize_imatrix: %zu source elements for a storage of %zu", elem_count,
+                    blocks * (size_t)QK_K);
+    if (n_per_row == 0 || n_per_row % QK_K)
+        return fail(FRQ_INVALID, "quantize_imatrix: n_per_row=%zu must be a positive multiple of %d", n_per_row, QK_K);
+    if (!imatrix || (elem_count && !src)) return fail(FRQ_INVALID, "quantize_imatrix: null buffer");
+    if (((uintptr_t)src & 15u) != 0) return fail(FRQ_MISALIGNED, "quantize_imatrix: source must be 16-byte aligned");
+    if (blocks == 0) return FRQ_OK;
+    // the importance weights go to the workspace (stream-ordered before the kernel)
+    if ((rc = ensure_ws(q->dev, n_per_row * sizeof(float)))) return rc;
+    float* wdev = static_cast<float*>(q->dev->ws);
+    HIP_TRY(hipMemcpyAsync(wdev, imatrix, n_per_row * sizeof(float), hipMemcpyHostToDevice, q->dev->stream));
+    HIP_TRY(launch_quantize_weights_imatrix(q->dtype, src, blocks, wdev, n_per_row / QK_K, q->d_ptr,
+                                            q->dev->stream));
+    // the host buffer may be reused once this returns: wait for the copy
+    HIP_TRY(hipStreamSynchronize(q->dev->stream));
+    return FRQ_OK;
+}
+
 int frq_qstorage_fwd(const frq_qstorage* q, size_t n, size_t k, const float* x, size_t m, float* y) {
     if (!q) return fail(FRQ_INVALID, "null storage");
     int rc = use_device(q->dev);

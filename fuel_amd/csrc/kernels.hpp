@@ -170,6 +170,10 @@ hipError_t launch_dequantize(int dtype, const uint8_t* w, size_t nblocks, float*
 // weights.hip: from_float on the device (one thread per superblock), and the
 // Philox synthetic-input generator.
 hipError_t launch_quantize_weights(int dtype, const float* x, size_t nblocks, uint8_t* out, hipStream_t s);
+// from_float_imatrix (Q4_K, Q6_K): superblock ib uses the importance weights
+// imatrix[(ib % blocks_per_row) * 256 ...] (device memory).
+hipError_t launch_quantize_weights_imatrix(int dtype, const float* x, size_t nblocks, const float* imatrix,
+                                           size_t blocks_per_row, uint8_t* out, hipStream_t s);
 hipError_t launch_random_bits(uint32_t* y, size_t n, unsigned long long start, unsigned long long seed,
                               uint32_t base, uint32_t stream, hipStream_t s);
 hipError_t launch_normal(float* y, size_t n, unsigned long long seed, uint32_t stream, float mean, float stdv,

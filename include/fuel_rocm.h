@@ -110,6 +110,17 @@ int frq_qstorage_dequantize_f16(const frq_qstorage *qs, size_t elem_count, uint1
  * :2005-2075, BlockQ8_0::from_float :629-658), bit-exact with the CPU
  * quantizer; elem_count must equal the storage's element count. */
 int frq_qstorage_quantize(frq_qstorage *qs, const float *src_dev, size_t elem_count);
+/* quantize_imatrix(src, imatrix_weights, n_per_row) and
+ * quantize_imatrix_onto (fuel-backend-contract/src/quantized.rs:37-54;
+ * CPU backend fuel-cpu-backend/src/quantized.rs:51-72): from_float_imatrix
+ * of elem_count f32 values on the device (BlockQ4K k_quants.rs:1530-1593,
+ * BlockQ6K :2077-2145), bit-exact with the CPU quantizer.  imatrix_host holds
+ * n_per_row f32 importance weights (host memory, as the trait's slice); the
+ * superblock with flat index s uses weights [(s % (n_per_row / 256)) * 256,
+ * +256).  n_per_row must be a positive multiple of 256.  Q8_0 (and every
+ * type without from_float_imatrix in the reference) gives FRQ_UNSUPPORTED. */
+int frq_qstorage_quantize_imatrix(frq_qstorage *qs, const float *src_dev, size_t elem_count,
+                                  const float *imatrix_host, size_t n_per_row);
 /* fwd(self_shape = [n, k], input [m, k] contiguous f32) -> y [m, n] f32.
  * The trait method returns a fresh storage; here the caller passes the
  * output buffer (the host-side mirror allocates it). */

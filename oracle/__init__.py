@@ -61,6 +61,7 @@ def lib():
             "fo_quantize_q4k": (None, [vp, sz, vp]),
             "fo_quantize_q6k": (None, [vp, sz, vp]),
             "fo_quantize_rows": (None, [i32, vp, sz, sz, vp]),
+            "fo_quantize_imatrix": (i32, [i32, vp, sz, vp, sz, vp]),
             "fo_dequantize": (None, [i32, vp, sz, vp]),
             "fo_q4k_unpack_scales": (None, [vp, vp, vp]),
             "fo_vec_dot_q4k_unopt": (f32, [sz, vp, vp]),
@@ -156,6 +157,19 @@ def quantize(dtype: int, x: np.ndarray) -> np.ndarray:
     rows = x.size // k
     y = np.zeros(x.shape[:-1] + (k // bs,), BLOCK_DTYPE[dtype])
     lib().fo_quantize_rows(dtype, _p(x), rows, k, _p(y))
+    return y
+
+
+def quantize_imatrix(dtype: int, x: np.ndarray, imatrix: np.ndarray, n_per_row: int) -> np.ndarray:
+    """from_float_imatrix (Q4_K / Q6_K) over the flattened x: superblock s uses
+    the importance weights imatrix[(s % (n_per_row / 256)) * 256 ...]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(imatrix, dtype=np.float32)
+    assert w.size >= n_per_row and x.size % 256 == 0
+    y = np.zeros(x.shape[:-1] + (x.shape[-1] // 256,), BLOCK_DTYPE[dtype])
+    rc = lib().fo_quantize_imatrix(dtype, _p(x), x.size, _p(w), n_per_row, _p(y))
+    if rc:
+        raise ValueError(f"quantize_imatrix: dtype {dtype}, n_per_row {n_per_row}")
     return y
 
 

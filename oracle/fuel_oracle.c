@@ -357,6 +357,27 @@ static void make_qkx1_quants(int nmax, int ntry, const float *x, int n, float *o
     *out_min = -min;
 }
 
+/* The 4-bit codes of a Q4_K superblock from its d, dmin and packed scales
+ * (k_quants.rs:1511-1527, also the tail of from_float_imatrix). */
+static void q4k_codes(const float *x, fo_block_q4k *b) {
+    uint8_t L[FO_QK_K];
+    memset(L, 0, sizeof L);
+    for (int j = 0; j < 8; j++) {
+        uint8_t sc, m;
+        get_scale_min_k4(j, b->scales, &sc, &m);
+        float d = fo_f16_to_f32(b->d) * (float)sc;
+        if (d != 0.0f) {
+            float dm = fo_f16_to_f32(b->dmin) * (float)m;
+            for (int ii = 0; ii < 32; ii++) {
+                int32_t lv = nearest_int((x[32 * j + ii] + dm) / d);
+                L[32 * j + ii] = (uint8_t)clamp_i32(lv, 0, 15);
+            }
+        }
+    }
+    for (int c = 0; c < 4; c++)
+        for (int l = 0; l < 32; l++) b->qs[32 * c + l] = (uint8_t)(L[64 * c + l] | (L[64 * c + l + 32] << 4));
+}
+
 /* BlockQ4K::from_float (k_quants.rs:1470-1528). */
 void fo_quantize_q4k(const float *xin, size_t k, fo_block_q4k *y) {
     size_t nb = k / FO_QK_K;
@@ -387,29 +408,215 @@ void fo_quantize_q4k(const float *xin, size_t k, fo_block_q4k *y) {
         }
         b->d = fo_f32_to_f16(max_scale / 63.0f);
         b->dmin = fo_f32_to_f16(max_min / 63.0f);
-        uint8_t L[FO_QK_K];
-        memset(L, 0, sizeof L);
-        for (int j = 0; j < 8; j++) {
-            uint8_t sc, m;
-            get_scale_min_k4(j, b->scales, &sc, &m);
-            float d = fo_f16_to_f32(b->d) * (float)sc;
-            if (d != 0.0f) {
-                float dm = fo_f16_to_f32(b->dmin) * (float)m;
-                for (int ii = 0; ii < 32; ii++) {
-                    int32_t lv = nearest_int((x[32 * j + ii] + dm) / d);
-                    L[32 * j + ii] = (uint8_t)clamp_i32(lv, 0, 15);
-                }
-            }
-        }
-        for (int c = 0; c < 4; c++)
-            for (int l = 0; l < 32; l++)
-                b->qs[32 * c + l] = (uint8_t)(L[64 * c + l] | (L[64 * c + l + 32] << 4));
+        q4k_codes(x, b);
     }
 }
 
-/* utils.rs:62-226 make_qx_quants, specialised to what BlockQ6K::from_float
- * passes: rmse_type = 1 (weights w = x*x), qw = null. */
-static float make_qx_quants_rmse1(int n, int nmax, const float *x, int8_t *ls) {
+/* utils.rs:358-469 make_qkx3_quants(nmax, x, Some(weights), rmin, rdelta,
+ * nstep, use_mad = false): returns (scale, -min). */
+static void make_qkx3_quants_w(int nmax, const float *x, const float *w, int n, float rmin, float rdelta, int nstep,
+                               float *out_scale, float *out_neg_min) {
+    uint8_t l[32], laux[32];
+    float min_val = x[0], max_val = x[0];
+    float sum_w = w[0];
+    float sum_x = sum_w * x[0];
+    for (int i = 1; i < n; i++) {
+        if (x[i] < min_val) min_val = x[i];
+        if (x[i] > max_val) max_val = x[i];
+        sum_w += w[i];
+        sum_x += w[i] * x[i];
+    }
+    if (min_val > 0.0f) min_val = 0.0f;
+    if (max_val <= min_val) {
+        *out_scale = 0.0f;
+        *out_neg_min = -min_val;
+        return;
+    }
+    float iscale = (float)nmax / (max_val - min_val);
+    float scale = 1.0f / iscale;
+    float best_mad = 0.0f;
+    for (int i = 0; i < n; i++) {
+        uint8_t lv = (uint8_t)clamp_i32(nearest_int(iscale * (x[i] - min_val)), 0, nmax);
+        l[i] = lv;
+        float diff = scale * (float)lv + min_val - x[i];
+        diff = diff * diff;
+        best_mad += w[i] * diff;
+    }
+    if (nstep >= 1) {
+        for (int is = 0; is <= nstep; is++) {
+            iscale = (rmin + rdelta * (float)is + (float)nmax) / (max_val - min_val);
+            float sum_l = 0.0f, sum_l2 = 0.0f, sum_xl = 0.0f;
+            for (int i = 0; i < n; i++) {
+                uint8_t lv = (uint8_t)clamp_i32(nearest_int(iscale * (x[i] - min_val)), 0, nmax);
+                laux[i] = lv;
+                sum_l += w[i] * (float)lv;
+                sum_l2 += w[i] * ((float)lv * (float)lv);
+                sum_xl += w[i] * (float)lv * x[i];
+            }
+            float d = sum_w * sum_l2 - sum_l * sum_l;
+            if (d > 0.0f) {
+                float this_scale = (sum_w * sum_xl - sum_x * sum_l) / d;
+                float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / d;
+                if (this_min > 0.0f) {
+                    this_min = 0.0f;
+                    this_scale = sum_xl / sum_l2;
+                }
+                float mad = 0.0f;
+                for (int i = 0; i < n; i++) {
+                    float diff = this_scale * (float)laux[i] + this_min - x[i];
+                    diff = diff * diff;
+                    mad += w[i] * diff;
+                }
+                if (mad < best_mad) {
+                    memcpy(l, laux, sizeof l);
+                    best_mad = mad;
+                    scale = this_scale;
+                    min_val = this_min;
+                }
+            }
+        }
+    }
+    *out_scale = scale;
+    *out_neg_min = -min_val;
+}
+
+/* Rust `f as u8` for a float: saturating, NaN -> 0. */
+static inline uint8_t sat_u8(float v) {
+    if (v != v || v <= 0.0f) return 0;
+    if (v >= 255.0f) return 255;
+    return (uint8_t)v;
+}
+
+/* utils.rs:472-563 make_qp_quants(n, nmax, x, l, quant_weights): the scale
+ * of n non-negative values on 0..nmax by a grid search over iscale and a
+ * coordinate descent, weighted; returns sumlx / suml2. */
+static float make_qp_quants(int n, int nmax, const float *x, uint8_t *l, const float *qw) {
+    float max = 0.0f;
+    for (int i = 0; i < n; i++) max = fmaxf(max, x[i]); /* f32::max: a NaN operand is ignored */
+    if (max == 0.0f) {
+        for (int i = 0; i < n; i++) l[i] = 0;
+        return 0.0f;
+    }
+    float iscale = (float)nmax / max;
+    for (int i = 0; i < n; i++) l[i] = (uint8_t)nearest_int(iscale * x[i]); /* i32 as u8: wraps */
+    float scale = 1.0f / iscale;
+    float best_mse = -0.0f;
+    for (int i = 0; i < n; i++) {
+        float diff = x[i] - scale * (float)l[i];
+        best_mse += qw[i] * diff * diff;
+    }
+    for (int is = -4; is <= 4; is++) {
+        if (is == 0) continue;
+        float iscale_is = (0.1f * (float)is + (float)nmax) / max;
+        float scale_is = 1.0f / iscale_is;
+        float mse = -0.0f;
+        for (int i = 0; i < n; i++) {
+            uint8_t li = (uint8_t)nearest_int(iscale_is * x[i]);
+            if (li > nmax) li = (uint8_t)nmax;
+            float diff = x[i] - scale_is * (float)li;
+            mse += qw[i] * diff * diff;
+        }
+        if (mse < best_mse) {
+            best_mse = mse;
+            iscale = iscale_is;
+        }
+    }
+    float sumlx = 0.0f, suml2 = 0.0f;
+    for (int i = 0; i < n; i++) {
+        uint8_t li = sat_u8(roundf(iscale * x[i]));
+        if (li > nmax) li = (uint8_t)nmax;
+        l[i] = li;
+        sumlx += qw[i] * x[i] * (float)li;
+        suml2 += qw[i] * ((float)li * (float)li);
+    }
+    for (int it = 0; it < 5; it++) {
+        int n_changed = 0;
+        for (int i = 0; i < n; i++) {
+            float slx = sumlx - qw[i] * x[i] * (float)l[i];
+            float sl2 = suml2 - qw[i] * ((float)l[i] * (float)l[i]);
+            if (slx > 0.0f && sl2 > 0.0f) {
+                uint8_t new_li = (uint8_t)nearest_int(x[i] * sl2 / slx);
+                if (new_li > nmax) new_li = (uint8_t)nmax;
+                if (new_li != l[i]) {
+                    slx += qw[i] * x[i] * (float)new_li;
+                    sl2 += qw[i] * ((float)new_li * (float)new_li);
+                    if (slx * slx * suml2 > sumlx * sumlx * sl2) {
+                        l[i] = new_li;
+                        sumlx = slx;
+                        suml2 = sl2;
+                        n_changed++;
+                    }
+                }
+            }
+        }
+        if (n_changed == 0) break;
+    }
+    return sumlx / suml2;
+}
+
+/* BlockQ4K::from_float_imatrix (k_quants.rs:1530-1593), one superblock; qw =
+ * the superblock's 256 importance weights. */
+static void q4k_block_imatrix(const float *x, const float *qw, fo_block_q4k *b) {
+    memset(b, 0, sizeof *b);
+    float mins[8], scales[8], weights[32], sw[8];
+    uint8_t ls[8], lm[8];
+    float sum_x2 = -0.0f;
+    for (int i = 0; i < FO_QK_K; i++) sum_x2 += x[i] * x[i];
+    float sigma2 = 2.0f * sum_x2 / (float)FO_QK_K;
+    for (int j = 0; j < 8; j++) {
+        for (int l = 0; l < 32; l++) {
+            float xe = x[32 * j + l];
+            weights[l] = qw[32 * j + l] * sqrtf(sigma2 + xe * xe);
+        }
+        float sumw = -0.0f;
+        for (int l = 0; l < 32; l++) sumw += weights[l];
+        sw[j] = sumw;
+        make_qkx3_quants_w(15, x + 32 * j, weights, 32, -0.9f, 0.05f, 36, &scales[j], &mins[j]);
+    }
+    float d_block = make_qp_quants(8, 63, scales, ls, sw);
+    float m_block = make_qp_quants(8, 63, mins, lm, sw);
+    for (int j = 0; j < 8; j++) {
+        if (j < 4) {
+            b->scales[j] = ls[j];
+            b->scales[j + 4] = lm[j];
+        } else {
+            b->scales[j + 4] = (uint8_t)((ls[j] & 0xF) | ((lm[j] & 0xF) << 4));
+            b->scales[j - 4] |= (uint8_t)((ls[j] >> 4) << 6);
+            b->scales[j] |= (uint8_t)((lm[j] >> 4) << 6);
+        }
+    }
+    b->d = fo_f32_to_f16(d_block);
+    b->dmin = fo_f32_to_f16(m_block);
+    q4k_codes(x, b);
+}
+
+static void q6k_block(const float *x, const float *qw, int8_t *L, fo_block_q6k *b);
+
+/* from_float_imatrix over a tensor of k elements (whole superblocks): the
+ * superblock with flat index s takes the importance weights of column block
+ * s % (n_per_row / 256) (k_quants.rs:1544, 2092).  Q4_K and Q6_K only. */
+int fo_quantize_imatrix(int t, const float *x, size_t k, const float *imatrix, size_t n_per_row, void *y) {
+    if (n_per_row < FO_QK_K || n_per_row % FO_QK_K || k % FO_QK_K) return -1;
+    size_t nbr = n_per_row / FO_QK_K;
+    if (t == FO_Q4K) {
+        for (size_t s = 0; s < k / FO_QK_K; s++)
+            q4k_block_imatrix(x + s * FO_QK_K, imatrix + (s % nbr) * FO_QK_K, (fo_block_q4k *)y + s);
+        return 0;
+    }
+    if (t == FO_Q6K) {
+        int8_t L[FO_QK_K];
+        memset(L, 0, sizeof L);
+        for (size_t s = 0; s < k / FO_QK_K; s++)
+            q6k_block(x + s * FO_QK_K, imatrix + (s % nbr) * FO_QK_K, L, (fo_block_q6k *)y + s);
+        return 0;
+    }
+    return -1;
+}
+
+/* utils.rs:62-226 make_qx_quants with rmse_type = 1, as BlockQ6K::from_float
+ * (qw = null: weights w = x*x) and from_float_imatrix (qw = the importance
+ * weights) call it. */
+static float make_qx_quants_w(int n, int nmax, const float *x, int8_t *ls, const float *qw) {
     float max = 0.0f, amax = 0.0f;
     for (int i = 0; i < n; i++) {
         float ax = fabsf(x[i]);
@@ -427,7 +634,7 @@ static float make_qx_quants_rmse1(int n, int nmax, const float *x, int8_t *ls) {
     for (int i = 0; i < n; i++) {
         int32_t l = clamp_i32(nearest_int(iscale * x[i]), -nmax, nmax - 1);
         ls[i] = (int8_t)(l + nmax);
-        float w = x[i] * x[i];
+        float w = qw ? qw[i] : x[i] * x[i];
         float lf = (float)l;
         sumlx += w * x[i] * lf;
         suml2 += w * lf * lf;
@@ -441,7 +648,7 @@ static float make_qx_quants_rmse1(int n, int nmax, const float *x, int8_t *ls) {
         for (int i = 0; i < n; i++) {
             int32_t l = clamp_i32(nearest_int(is2 * x[i]), -nmax, nmax - 1);
             if (l + nmax != (int32_t)ls[i]) changed = 1;
-            float w = x[i] * x[i];
+            float w = qw ? qw[i] : x[i] * x[i];
             float lf = (float)l;
             slx += w * x[i] * lf;
             sl2 += w * lf * lf;
@@ -459,7 +666,7 @@ static float make_qx_quants_rmse1(int n, int nmax, const float *x, int8_t *ls) {
     for (int itry = 0; itry < 5; itry++) {
         int n_changed = 0;
         for (int i = 0; i < n; i++) {
-            float w = x[i] * x[i];
+            float w = qw ? qw[i] : x[i] * x[i];
             int32_t l = (int32_t)ls[i] - nmax;
             float slx = sumlx - w * x[i] * (float)l;
             if (slx > 0.0f) {
@@ -485,19 +692,17 @@ static float make_qx_quants_rmse1(int n, int nmax, const float *x, int8_t *ls) {
     return scale;
 }
 
-/* BlockQ6K::from_float (k_quants.rs:2005-2075). */
-void fo_quantize_q6k(const float *xin, size_t k, fo_block_q6k *y) {
-    size_t nb = k / FO_QK_K;
-    int8_t L[FO_QK_K];
-    memset(L, 0, sizeof L);
-    for (size_t ibk = 0; ibk < nb; ibk++) {
-        const float *x = xin + ibk * FO_QK_K;
-        fo_block_q6k *b = &y[ibk];
+/* One superblock of BlockQ6K::from_float (qw = NULL) or of
+ * from_float_imatrix (k_quants.rs:2077-2145: qw = the superblock's 256
+ * importance weights).  L carries the codes from block to block, as the
+ * reference's buffer does. */
+static void q6k_block(const float *x, const float *qw, int8_t *L, fo_block_q6k *b) {
+    {
         memset(b, 0, sizeof *b);
         float scales[16];
         float max_scale = 0.0f, max_abs_scale = 0.0f;
         for (int ib = 0; ib < 16; ib++) {
-            float s = make_qx_quants_rmse1(16, 32, x + 16 * ib, L + 16 * ib);
+            float s = make_qx_quants_w(16, 32, x + 16 * ib, L + 16 * ib, qw ? qw + 16 * ib : NULL);
             scales[ib] = s;
             float as = fabsf(s);
             if (as > max_abs_scale) {
@@ -533,6 +738,13 @@ void fo_quantize_q6k(const float *xin, size_t k, fo_block_q6k *y) {
             }
         }
     }
+}
+
+/* BlockQ6K::from_float (k_quants.rs:2005-2075). */
+void fo_quantize_q6k(const float *xin, size_t k, fo_block_q6k *y) {
+    int8_t L[FO_QK_K];
+    memset(L, 0, sizeof L);
+    for (size_t ibk = 0; ibk < k / FO_QK_K; ibk++) q6k_block(xin + ibk * FO_QK_K, NULL, L, &y[ibk]);
 }
 
 void fo_quantize_rows(int t, const float *x, size_t rows, size_t k, void *y) {

@@ -80,6 +80,10 @@ void fo_quantize_q8_0(const float *x, size_t k, fo_block_q8_0 *y); /* k_quants.r
 /* ---- weight quantizers (from_float) ---- */
 void fo_quantize_q4k(const float *x, size_t k, fo_block_q4k *y);   /* k_quants.rs:1470-1528 */
 void fo_quantize_q6k(const float *x, size_t k, fo_block_q6k *y);   /* k_quants.rs:2005-2075 */
+/* from_float_imatrix (k_quants.rs:1530-1593 Q4_K, 2077-2145 Q6_K): importance
+ * weights imatrix[n_per_row], the flat superblock s using column block
+ * s % (n_per_row / 256).  Returns -1 for other types or a bad n_per_row. */
+int fo_quantize_imatrix(int ggml_dtype, const float *x, size_t k, const float *imatrix, size_t n_per_row, void *y);
 /* Row-parallel (OpenMP) wrappers over the per-row quantizers above;
  * rows are independent so the bytes are identical to the serial call. */
 void fo_quantize_rows(int ggml_dtype, const float *x, size_t rows, size_t k, void *y);
