@@ -16,7 +16,8 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "build", "libfuel_oracle.so")
+# (FUEL_ORACLE_LIB: another build of the same source, e.g. the sanitizer run's)
+LIB_PATH = os.environ.get("FUEL_ORACLE_LIB") or os.path.join(HERE, "build", "libfuel_oracle.so")
 
 # GgmlDType codes (fuel-ir/src/quantized.rs:36-76)
 Q8_0, Q4K, Q6K, Q8K = 8, 12, 14, 15
