@@ -28,6 +28,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-decode] [--deco
 from __future__ import annotations
 
 import argparse
+import glob
 import json
 import math
 import os
@@ -466,6 +467,74 @@ def decode_leg(new_tokens: int = DECODE_NEW, prompt_len: int = DECODE_PROMPT):
     return res, dec, dev, tokens, logits0
 
 
+def counter_refs() -> dict:
+    """The committed counter runs (profiles/*_counters.json, bench_profile.py
+    --leg counters: rocprofv3 SQ / MFMA / FETCH_SIZE / WRITE_SIZE passes over
+    bench.py --probe, separate processes from this one): per probe, the
+    kernel's average time, its HBM fraction and counted-traffic ratio, and for
+    the int8-MFMA kernels the MFMA-pipe utilisation from
+    SQ_INSTS_VALU_MFMA_MOPS_I8 against the 5 POPS int8 peak."""
+    out = {}
+    for f in sorted(glob.glob(os.path.join(ROOT, "profiles", "*_counters.json"))):
+        d = json.load(open(f))
+        keep = ("probe", "kernel_avg_us", "hbm_peak_frac", "traffic_over_algorithmic", "useful_int8_peak_frac",
+                "mfma_pipe_int8_peak_frac", "mfma_ops_over_useful", "wave_wait_frac")
+        out[os.path.basename(f)[:-len("_counters.json")]] = {k: d[k] for k in keep if k in d}
+    return out
+
+
+def decode_breakdown_leg(new_tokens: int = 128, prompt_len: int = DECODE_PROMPT) -> dict:
+    """Per-kernel-class time of the config-4 decode step, from HIP events in
+    the process: the decoder is run to position prompt_len + new_tokens (the
+    prompt forced, then greedy steps), then each class of the step's launches
+    (LlamaDecoder.STEP_PARTS: the q|k + v pair, attention with the
+    o-projection, gate|up, down, logits, argmax + embedding) is captured alone
+    over all layers and replayed; the whole step is timed the same way."""
+    import fuel_amd as F
+    from fuel_amd.hiprt import HipRuntime
+    from fuel_amd.llama import LlamaConfig, LlamaDecoder
+
+    cfg = LlamaConfig(max_ctx=prompt_len + DECODE_NEW)
+    hip = HipRuntime()
+    dev = F.RocmDevice(0)
+    stream = hip.stream_create()
+    dev.set_stream(stream)
+    dec = LlamaDecoder(dev, cfg, seed=SEED)
+    bits = F.fill_random_bits(dev, prompt_len, 0, SEED, 0, 77).numpy()
+    dec.start((bits % cfg.vocab).astype(np.int32))
+    g = hip.capture(stream, dec.enqueue_step)
+    for _ in range(prompt_len - 1 + new_tokens):
+        hip.graph_launch(g, stream)
+    hip.stream_sync(stream)
+    hip.graph_destroy(g)
+    e0, e1 = hip.event_create(), hip.event_create()
+
+    def timed(parts, reps=20):
+        gg = hip.capture(stream, lambda: dec.enqueue_step(parts))
+        hip.graph_launch(gg, stream)
+        hip.stream_sync(stream)
+        hip.event_record(e0, stream)
+        for _ in range(reps):
+            hip.graph_launch(gg, stream)
+        hip.event_record(e1, stream)
+        hip.event_sync(e1)
+        hip.graph_destroy(gg)
+        return hip.elapsed_ms(e0, e1) * 1e3 / reps
+
+    per_layer = {"qkv": 32, "attention": 32, "gate_up": 32, "down": 32, "logits": 1, "argmax": 1}
+    res = {"position": prompt_len - 1 + new_tokens, "max_ctx": cfg.max_ctx, "parts": {}}
+    for part in dec.STEP_PARTS:
+        us = timed({part})
+        res["parts"][part] = {"us_per_token": round(us, 2), "launches": per_layer[part],
+                              "us_per_launch": round(us / per_layer[part], 2)}
+    full = timed(None)
+    res["step_us"] = round(full, 2)
+    res["sum_of_parts_us"] = round(sum(v["us_per_token"] for v in res["parts"].values()), 2)
+    res["tokens_per_s"] = round(1e6 / full, 1)
+    dev.close()
+    return res
+
+
 def cpu_decode_leg(dec, tokens, logits0, target_s: float, prompt_len: int = DECODE_PROMPT):
     """fuel's CPU quantized path (oracle restatement of the decode step, AVX2
     vec_dot) on the same weights and KV state: decode tokens/s on the host
@@ -575,6 +644,8 @@ def main() -> int:
     ap.add_argument("--no-moe", action="store_true", help="skip the config-5 MoE leg")
     ap.add_argument("--no-q6k", action="store_true", help="skip the Q6_K sweep and Q6_K batched rows")
     ap.add_argument("--decode-only", action="store_true", help="run only the config-4 decode legs")
+    ap.add_argument("--decode-breakdown", action="store_true",
+                    help="time each kernel class of the config-4 decode step (HIP events) and print its JSON line")
     ap.add_argument("--probe", default=None, metavar="K,N,DTYPE,M",
                     help="time one QMatMul configuration alone (profiling runs) and print its JSON line")
     args = ap.parse_args()
@@ -583,6 +654,9 @@ def main() -> int:
               "(this build has no multi-GPU path; the sharding design is documented only)", file=sys.stderr)
         return 2
 
+    if args.decode_breakdown:
+        print(json.dumps(decode_breakdown_leg()), flush=True)
+        return 0
     if args.probe:
         k, n, dt, m = (int(v) for v in args.probe.split(","))
         print(json.dumps(probe_leg(k, n, dt, m)), flush=True)
@@ -638,6 +712,7 @@ def main() -> int:
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
         "per_shape": per_shape,
         "per_shape_q6k": per_shape_q6k,
+        "counters_from_profiles": counter_refs(),
         "decode_tokens_per_s": None,
         "roofline": {
             "bound": "hbm",

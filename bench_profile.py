@@ -188,10 +188,38 @@ def counters_leg(probe: str, pattern: str, out: str, summarize_only: bool) -> in
     return 0
 
 
+def breakdown_leg(out: str, summarize_only: bool) -> int:
+    """Config-4 decode step per kernel class from HIP events in the process
+    (bench.py --decode-breakdown), without a profiler."""
+    name = "decode_7b_q4km_breakdown"
+    cmd = ["python3", "bench.py", "--decode-breakdown"]
+    log = os.path.join(ROOT, out, f"{name}.log")
+    if not summarize_only:
+        run(cmd, f"{out}/{name}.log", 600)
+    res = None
+    for line in open(log):
+        if line.startswith("{"):
+            res = json.loads(line)
+    if res is None:
+        raise SystemExit(f"no JSON line in {log}")
+    with open(os.path.join(ROOT, out, f"{name}.md"), "w") as f:
+        f.write("# Config 4: decode step of the 7B-shaped Q4_K_M decoder, per kernel class\n\n")
+        f.write(f"Made by `python3 bench_profile.py --leg decode_breakdown` (repository root, one MI355X), which runs "
+                f"`{' '.join(cmd)}`: HIP events around graph replays of each class of the step's launches over all "
+                f"32 layers, at position {res['position']} (max_ctx {res['max_ctx']}).\n\n")
+        f.write("| class | launches per token | us per token | us per launch |\n|---|---|---|---|\n")
+        for part, v in res["parts"].items():
+            f.write(f"| {part} | {v['launches']} | {v['us_per_token']} | {v['us_per_launch']} |\n")
+        f.write(f"\nWhole step (one graph): {res['step_us']} us = {res['tokens_per_s']} tokens/s; the classes timed "
+                f"alone sum to {res['sum_of_parts_us']} us.\n")
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--shape", default="4096x32000")
-    ap.add_argument("--leg", default="matvec", choices=["matvec", "counters"] + sorted(LEGS))
+    ap.add_argument("--leg", default="matvec", choices=["matvec", "counters", "decode_breakdown"] + sorted(LEGS))
     ap.add_argument("--probe", default="4096,11008,12,512", help="K,N,DTYPE,M for --leg counters")
     ap.add_argument("--kernel", default="mmq", help="kernel-name substring for --leg counters")
     ap.add_argument("--out", default="gpurun_out/profiles")
@@ -202,6 +230,8 @@ def main() -> int:
     os.environ.setdefault("TMPDIR", "/tmp")
     if args.leg == "counters":
         return counters_leg(args.probe, args.kernel, out, args.summarize_only)
+    if args.leg == "decode_breakdown":
+        return breakdown_leg(out, args.summarize_only)
     if args.leg != "matvec":
         return trace_leg(args.leg, out, args.summarize_only)
     bench = ["python3", "bench.py", "--shape", args.shape, "--steps", "50", "--warmup", "5", "--no-cpu",
