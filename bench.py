@@ -590,6 +590,24 @@ def cpu_decode_leg(dec, tokens, logits0, target_s: float, prompt_len: int = DECO
     }
 
 
+def host_llc_bytes() -> int:
+    """Total last-level (L3) cache of the host, from sysfs: the size of each
+    distinct L3 instance (shared_cpu_list) summed; 0 when sysfs has none."""
+    seen, total = set(), 0
+    for idx in glob.glob("/sys/devices/system/cpu/cpu*/cache/index3"):
+        try:
+            share = open(os.path.join(idx, "shared_cpu_list")).read().strip()
+            size = open(os.path.join(idx, "size")).read().strip()
+        except OSError:
+            continue
+        if share in seen:
+            continue
+        seen.add(share)
+        mult = {"K": 1024, "M": 1024 ** 2}.get(size[-1:], 1)
+        total += int(size.rstrip("KM")) * mult
+    return total
+
+
 def cpu_leg(target_s: float):
     """fuel's CPU quantized path (oracle restatement, AVX2 vec_dot) on the host
     cores: median time of repeated 4-shape sweeps."""
@@ -598,11 +616,14 @@ def cpu_leg(target_s: float):
     threads = int(os.environ.get("RAYON_NUM_THREADS") or os.environ.get("OMP_NUM_THREADS") or 0)
     if threads <= 0:
         threads = len(os.sched_getaffinity(0))
+    step_bytes = sum(algo_bytes(k, n) for k, n in SHAPES)
+    llc = host_llc_bytes()
+    # rotated copies, as on the GPU: at least twice the host's last-level cache
+    copies = min(16, max(CPU_COPIES, math.ceil(2 * llc / step_bytes)))
     mats = []
     for si, (k, n) in enumerate(SHAPES):
         w = O.quantize(O.Q4K, O.normal((n, k), SEED, 100 + si, std=0.02))
-        # rotated copies, as on the GPU: the sweep's weights exceed the host's last-level cache
-        mats.append((O.normal((1, k), SEED, 200 + si), [w] + [w.copy() for _ in range(CPU_COPIES - 1)]))
+        mats.append((O.normal((1, k), SEED, 200 + si), [w] + [w.copy() for _ in range(copies - 1)]))
     for x, ws in mats:
         O.matmul(O.Q4K, x, ws[0], avx2=True, threads=threads)
     times = []
@@ -611,18 +632,19 @@ def cpu_leg(target_s: float):
     while time.time() < t_end or len(times) < 3:
         t = time.perf_counter()
         for x, ws in mats:
-            O.matmul(O.Q4K, x, ws[i % CPU_COPIES], avx2=True, threads=threads)
+            O.matmul(O.Q4K, x, ws[i % copies], avx2=True, threads=threads)
         times.append(time.perf_counter() - t)
         i += 1
     med = float(np.median(times))
-    step_bytes = sum(algo_bytes(k, n) for k, n in SHAPES)
     return {
         "value": round(step_bytes / med / 1e9, 2),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
+        "host_llc_bytes": llc,
         "sample": f"{len(times)} sweeps of the 4-shape Q4_K M=1 QMatMul ({step_bytes / 1e6:.1f} MB each, "
-                  f"weights rotated over {CPU_COPIES} copies), "
+                  f"weights rotated over {copies} copies = {copies * step_bytes / 1e6:.0f} MB against a "
+                  f"host last-level cache of {llc / 1e6:.0f} MB), "
                   f"median {med * 1e3:.2f} ms; oracle matmul<BlockQ4K> with the AVX2 vec_dot, "
                   f"{threads} OpenMP threads; avx2={'yes' if O.have_avx2() else 'no (scalar)'}",
     }
