@@ -11,7 +11,8 @@
 //   attention_prefill causal scaled-dot-product attention of each query row
 //                     over cache rows 0 .. its position (lazy.rs:7415-7425:
 //                     scores * scale + causal mask, softmax_last_dim, . V),
-//                     one pass with a running maximum, eight rows per step
+//                     one pass with a running maximum, on f16 MFMA with the
+//                     f32 operands split exactly into two f16 halves
 //   swiglu_rows       silu(g) * u (lazy.rs:7442)
 //   add_rows          the residual adds (lazy.rs:7434, 7446)
 //   gather_rows       embedding rows of the prompt tokens
@@ -78,96 +79,157 @@ __global__ __launch_bounds__(HD) void rope_append_rows_kernel(float* __restrict_
     vc[crow + tid] = __float2half(v[(size_t)m * ldv + (size_t)h * HD + tid]);
 }
 
-constexpr int AP_WG = 256;
-constexpr int AP_Q = AP_WG / 16;  // query rows per workgroup (16 lanes each, 8 dims per lane)
-constexpr int AP_KB = 8;          // cache rows whose loads are in flight together
+// Attention of a query tile on f16 MFMA.  A wavefront owns 16 query rows of
+// one head and walks the cache rows 0 .. its last row's position 16 at a time
+// with a running maximum (flash attention):
+//   S^T (16 keys x 16 queries) = K_blk (16 x 128) . Q^T (128 x 16) on
+//     v_mfma_f32_16x16x32_f16, four 32-dim steps; K rows are f16 already and
+//     each q value is split exactly into f16 hi + lo (hi = f16(q), lo =
+//     f16(q - hi): hi + lo = q to 2^-22), two MFMAs per step, f32 sums;
+//   s = S^T * scale, causal mask by select, block max / sum over the 16 keys,
+//     rescale of the running sum and output;
+//   O^T (128 x 16) += V^T (128 x 16 keys) . P^T (16 keys x 16) on
+//     v_mfma_f32_16x16x16_f16 per 16-dim tile, P split into f16 hi + lo the
+//     same way.
+// Lane l = 16 g + r: the S^T MFMA's C layout leaves it keys 4g + i (i < 4) of
+// query r, which is exactly the B operand (keys 4g .. 4g+3, column r) the PV
+// MFMA wants, so P never moves between lanes.  V is the PV MFMA's A operand
+// (row = dim, k = key): tile t takes the dims 8 * row + t, so lane l's four
+// 16-byte loads of rows 4g + i (dims 8r .. 8r+7) hold its A values for all
+// eight tiles.  Output: the C layout of tile t leaves lane l dims
+// 8 (4g + i) + t of query r, eight consecutive floats per i.
+typedef _Float16 af_h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 af_h4 __attribute__((ext_vector_type(4)));
+typedef float af_f4 __attribute__((ext_vector_type(4)));
+constexpr int AF_WAVES = 4;  // query tiles (16 rows each) per workgroup
 
-__device__ __forceinline__ float group16_sum(float v) {
-#pragma unroll
-    for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-    return v;
+__device__ __forceinline__ void split_f16(float v, _Float16& hi, _Float16& lo) {
+    hi = (_Float16)v;
+    lo = (_Float16)(v - (float)hi);
 }
 
-__device__ __forceinline__ void h8_to_f(const uint4& u, float (&f)[8]) {
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        f[2 * i] = __half2float(__ushort_as_half((unsigned short)(w[i] & 0xffffu)));
-        f[2 * i + 1] = __half2float(__ushort_as_half((unsigned short)(w[i] >> 16)));
-    }
-}
-
-// grid (heads, ceil(M / AP_Q)), AP_WG threads: 16-lane group g takes query row
-// m = AP_Q * blockIdx.y + g (position pos0 + m) and walks cache rows
-// 0 .. position AP_KB at a time with a running maximum: the step's scores
-// s_j = (q . k_j) * scale, M' = max(M, s_j of the step), l = l e^(M - M') +
-// sum e^(s_j - M'), o = o e^(M - M') + sum e^(s_j - M') v_j; out = o / l.
-// Rows past a group's position (the wave runs to its last group's) are
-// dropped by selects.
-__global__ __launch_bounds__(AP_WG) void attention_prefill_kernel(const float* __restrict__ q, int ldq,
-                                                                  const __half* __restrict__ kc,
-                                                                  const __half* __restrict__ vc, int pos0, int M,
-                                                                  int max_ctx, float scale, float* __restrict__ out,
-                                                                  int ldo) {
-    const int h = blockIdx.x, tid = threadIdx.x, g = tid >> 4, l16 = tid & 15;
-    const int m = AP_Q * blockIdx.y + g;
+__global__ __launch_bounds__(64 * AF_WAVES) void attention_prefill_kernel(const float* __restrict__ q, int ldq,
+                                                                          const uint16_t* __restrict__ kc,
+                                                                          const uint16_t* __restrict__ vc, int pos0,
+                                                                          int M, int max_ctx, float scale,
+                                                                          float* __restrict__ out, int ldo) {
+    const int h = blockIdx.x, lane = threadIdx.x & 63;
+    const int m0 = 16 * ((int)blockIdx.y * AF_WAVES + (int)(threadIdx.x >> 6));
+    if (m0 >= M) return;  // (the whole wavefront)
+    const int r = lane & 15, g = lane >> 4;
+    const int m = m0 + r;
     const int mq = m < M ? m : M - 1;
-    const int pos = pos0 + mq;
-    // the wave's last query row bounds its loop (4 groups per wave)
-    const int wlast = min(AP_Q * (int)blockIdx.y + (tid >> 6) * 4 + 3, M - 1);
-    const int jend = pos0 + wlast;
-    const float* qr = q + (size_t)mq * ldq + (size_t)h * HD + 8 * l16;
-    float q8[8];
+    const int qpos = pos0 + mq;                          // this lane's query position
+    const int jmax = pos0 + (m0 + 15 < M ? m0 + 15 : M - 1);  // the tile's last cache row
+    const uint16_t* kh = kc + (size_t)h * max_ctx * HD;
+    const uint16_t* vh = vc + (size_t)h * max_ctx * HD;
+
+    // Q^T as the S^T MFMA's B operand: dims 32t + 8g + e of query r
+    af_h8 qhi[4], qlo[4];
+    const float* qr = q + (size_t)mq * ldq + (size_t)h * HD;
 #pragma unroll
-    for (int e = 0; e < 8; e++) q8[e] = qr[e];
-    const size_t cbase = (size_t)h * max_ctx * HD + 8 * l16;
-    float mx = -__builtin_inff(), l = 0.0f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    // AP_KB cache rows per step, all their loads issued before the first is
-    // used (rows past jend repeat row jend and are skipped like any row past a
-    // group's position), so a step costs one memory round trip, not AP_KB
-    for (int j0 = 0; j0 <= jend; j0 += AP_KB) {
-        uint4 kr[AP_KB], vr[AP_KB];
+    for (int t = 0; t < 4; t++) {
+        const float4 x0 = *reinterpret_cast<const float4*>(qr + 32 * t + 8 * g);
+        const float4 x1 = *reinterpret_cast<const float4*>(qr + 32 * t + 8 * g + 4);
+        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-        for (int u = 0; u < AP_KB; u++) {
-            const size_t jr = (size_t)min(j0 + u, jend) * HD;
-            kr[u] = *reinterpret_cast<const uint4*>(kc + cbase + jr);
-            vr[u] = *reinterpret_cast<const uint4*>(vc + cbase + jr);
+        for (int e = 0; e < 8; e++) {
+            _Float16 a, b;
+            split_f16(xv[e], a, b);
+            qhi[t][e] = a;
+            qlo[t][e] = b;
         }
-        // the step's scores (rows past the group's position: -inf), one
-        // rescale to the step's maximum, then the rows' weighted values
-        float sv[AP_KB];
-        float mn = mx;
+    }
+    // one block's loads: K row j0 + r (dims 32t + 8g ..), V rows j0 + 4g + i
+    // (dims 8r ..); rows past the tile's last are clamped to it (their
+    // weights are 0; the row is written, so 0 * v stays 0)
+    auto load_blk = [&](int j0, uint4 (&kf)[4], uint4 (&vf)[4]) {
+        const int kr = j0 + r < jmax ? j0 + r : jmax;
 #pragma unroll
-        for (int u = 0; u < AP_KB; u++) {
-            float kv[8];
-            h8_to_f(kr[u], kv);
-            float d = 0.0f;
+        for (int t = 0; t < 4; t++) kf[t] = *reinterpret_cast<const uint4*>(kh + (size_t)kr * HD + 32 * t + 8 * g);
 #pragma unroll
-            for (int e = 0; e < 8; e++) d = fmaf(q8[e], kv[e], d);
-            const float sc = group16_sum(d) * scale;
-            sv[u] = j0 + u <= pos ? sc : -__builtin_inff();
-            mn = fmaxf(mn, sv[u]);
+        for (int i = 0; i < 4; i++) {
+            const int vr = j0 + 4 * g + i < jmax ? j0 + 4 * g + i : jmax;
+            vf[i] = *reinterpret_cast<const uint4*>(vh + (size_t)vr * HD + 8 * r);
         }
-        const float c = expf(mx - mn);  // (the first step: mx = -inf, l = o = 0; row 0 is always live)
-        l *= c;
+    };
+    af_f4 o[8];
 #pragma unroll
-        for (int e = 0; e < 8; e++) o[e] *= c;
+    for (int t = 0; t < 8; t++) o[t] = af_f4{0.f, 0.f, 0.f, 0.f};
+    float mrun = -__builtin_inff(), lrun = 0.0f;
+    auto block = [&](int j0, const uint4 (&kf)[4], const uint4 (&vf)[4]) {
+        af_f4 st = af_f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int u = 0; u < AP_KB; u++) {
-            const bool live = j0 + u <= pos;
-            const float p = expf(sv[u] - mn);
-            float vv[8];
-            h8_to_f(vr[u], vv);
-            l = live ? l + p : l;
-#pragma unroll
-            for (int e = 0; e < 8; e++) o[e] = live ? fmaf(p, vv[e], o[e]) : o[e];
+        for (int t = 0; t < 4; t++) {
+            const af_h8 a = __builtin_bit_cast(af_h8, kf[t]);
+            st = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qhi[t], st, 0, 0, 0);
+            st = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qlo[t], st, 0, 0, 0);
         }
-        mx = mn;
+        float sv[4], bmax = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            sv[i] = j0 + 4 * g + i <= qpos ? st[i] * scale : -__builtin_inff();
+            bmax = fmaxf(bmax, sv[i]);
+        }
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+        const float mnew = fmaxf(mrun, bmax);  // finite: cache row 0 is live for every query
+        const float c = expf(mrun - mnew);     // (0 on the first block, where lrun = o = 0)
+        float p[4], psum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            p[i] = expf(sv[i] - mnew);
+            psum += p[i];
+        }
+        psum += __shfl_xor(psum, 16);
+        psum += __shfl_xor(psum, 32);
+        lrun = lrun * c + psum;
+        mrun = mnew;
+        af_h4 phi, plo;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            _Float16 a, b;
+            split_f16(p[i], a, b);
+            phi[i] = a;
+            plo[i] = b;
+        }
+        const uint32_t vw[4][4] = {{vf[0].x, vf[0].y, vf[0].z, vf[0].w}, {vf[1].x, vf[1].y, vf[1].z, vf[1].w},
+                                   {vf[2].x, vf[2].y, vf[2].z, vf[2].w}, {vf[3].x, vf[3].y, vf[3].z, vf[3].w}};
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            // A (dim row r of tile t, keys 4g + i): half t of each V row's load
+            const uint32_t sel = (t & 1) ? 0x07060302u : 0x05040100u;  // high or low halves of two words
+            const uint32_t w01 = __builtin_amdgcn_perm(vw[1][t >> 1], vw[0][t >> 1], sel);
+            const uint32_t w23 = __builtin_amdgcn_perm(vw[3][t >> 1], vw[2][t >> 1], sel);
+            const af_h4 a = __builtin_bit_cast(af_h4, (unsigned long long)w01 | ((unsigned long long)w23 << 32));
+            af_f4 ot = o[t] * c;
+            ot = __builtin_amdgcn_mfma_f32_16x16x16f16(a, phi, ot, 0, 0, 0);
+            o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, plo, ot, 0, 0, 0);
+        }
+    };
+    // two-block register ring: the next block's loads are in flight while a
+    // block is computed (past the last block the ring re-reads its last one)
+    uint4 ka[4], va[4], kb[4], vb[4];
+    load_blk(0, ka, va);
+    int j0 = 0;
+    while (j0 <= jmax) {
+        load_blk(j0 + 16 <= jmax ? j0 + 16 : j0, kb, vb);
+        block(j0, ka, va);
+        j0 += 16;
+        if (j0 > jmax) break;
+        load_blk(j0 + 16 <= jmax ? j0 + 16 : j0, ka, va);
+        block(j0, kb, vb);
+        j0 += 16;
     }
     if (m < M) {
-        float* orow = out + (size_t)m * ldo + (size_t)h * HD + 8 * l16;
+        const float inv = 1.0f / lrun;
+        float* orow = out + (size_t)m * ldo + (size_t)h * HD;
 #pragma unroll
-        for (int e = 0; e < 8; e++) orow[e] = o[e] / l;
+        for (int i = 0; i < 4; i++) {
+            float4* dst = reinterpret_cast<float4*>(orow + 8 * (4 * g + i));
+            dst[0] = make_float4(o[0][i] * inv, o[1][i] * inv, o[2][i] * inv, o[3][i] * inv);
+            dst[1] = make_float4(o[4][i] * inv, o[5][i] * inv, o[6][i] * inv, o[7][i] * inv);
+        }
     }
 }
 
@@ -209,9 +271,9 @@ hipError_t launch_rope_append_rows(float* qk, int ldqk, const float* v, int ldv,
 
 hipError_t launch_attention_prefill(const float* q, int ldq, const uint16_t* kc, const uint16_t* vc, int pos0, int M,
                                     int n_heads, int max_ctx, float scale, float* out, int ldo, hipStream_t s) {
-    hipLaunchKernelGGL(attention_prefill_kernel, dim3(n_heads, (M + AP_Q - 1) / AP_Q), dim3(AP_WG), 0, s, q, ldq,
-                       reinterpret_cast<const __half*>(kc), reinterpret_cast<const __half*>(vc), pos0, M, max_ctx,
-                       scale, out, ldo);
+    if (M <= 0) return hipSuccess;
+    hipLaunchKernelGGL(attention_prefill_kernel, dim3(n_heads, (M + 16 * AF_WAVES - 1) / (16 * AF_WAVES)),
+                       dim3(64 * AF_WAVES), 0, s, q, ldq, kc, vc, pos0, M, max_ctx, scale, out, ldo);
     return hipGetLastError();
 }
 
