@@ -108,7 +108,7 @@ size_t act_bytes(int vt, size_t rows, size_t k) {
     const size_t kb = k / block_elems(vt);
     size_t b = align256(rows * k);                       // qs
     b += align256(rows * kb * sizeof(float));            // d
-    if (vt == GGML_Q8K) b += align256(rows * kb * 16 * sizeof(int16_t));  // bsums
+    if (vt == GGML_Q8K) b += 2 * align256(rows * kb * 16 * sizeof(int16_t));  // bsums, bsh
     return b;
 }
 
@@ -121,6 +121,7 @@ ActView act_view(void* base, int vt, size_t rows, size_t k) {
     v.d = reinterpret_cast<float*>(p);
     p += align256(rows * kb * sizeof(float));
     v.bsums = vt == GGML_Q8K ? reinterpret_cast<int16_t*>(p) : nullptr;
+    v.bsh = vt == GGML_Q8K ? reinterpret_cast<uint16_t*>(p + align256(rows * kb * 16 * sizeof(int16_t))) : nullptr;
     return v;
 }
 

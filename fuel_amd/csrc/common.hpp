@@ -144,11 +144,14 @@ __device__ __forceinline__ int wave_sum_i(int v) {
 //   qs    : int8  [rows][K]
 //   d     : f32   [rows][K/blk]    (Q8K: the f32 d; Q8_0: f16 d widened)
 //   bsums : int16 [rows][K/256][16] (Q8K only: sums of 16 consecutive quants)
+//   bsh   : f16   [rows][K/256][16] (Q8K only: the same sums as binary16 bits,
+//           exact since |sum| <= 2032; an MFMA operand of the batched kernel)
 // ---------------------------------------------------------------------------
 struct ActView {
     int8_t* qs;
     float* d;
     int16_t* bsums;
+    uint16_t* bsh;
 };
 
 // LDS copy of one quantized activation row inside the mat-vec kernels.  Q8K

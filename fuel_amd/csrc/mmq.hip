@@ -32,6 +32,7 @@
 // separates the two buffers' roles.  Lanes build their B fragments in
 // registers from the raw blocks.
 #include <type_traits>
+#include <utility>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -569,6 +570,328 @@ __global__ __launch_bounds__(64 * WM * WN) void mmq_dma_kernel(const uint8_t* __
         }
 }
 
+// ---- Q4_K, wide tiles: two MFMAs per product ----
+// NW wavefronts side by side in N share BM = 16 RT activation rows; each owns
+// 16 CT weight columns, so every weight block is unpacked by one wavefront.
+// Per superblock, one LDS ring slot receives, by DMA (global_load_lds, no
+// staging registers, no LDS stores): the activation rows (256 bytes each,
+// chunk j of row r at position j ^ (r & 15)), the raw weight blocks of the
+// BN columns (144 bytes apart, in their byte order), the rows' 16-element
+// sums (32 bytes a row) and their scales.  Three slots: superblock b+2 is in
+// flight while b is multiplied; the DMA instructions of a slot are dealt out
+// round-robin to the wavefronts, each issuing the same count (the spare ones
+// repeat the slot's last instruction: same source, same bytes, same place).
+//
+// K order inside a superblock: K step t (64 elements) has lane group kb take
+// the 16 elements of qs bytes 64 (t&1) + 16 kb .. +15, low nibbles for t < 2
+// and high nibbles for t >= 2 (the shift is uniform per step).  In fuel's
+// layout (k_quants.rs:1421-1440) qs byte i holds element 64 (i/32) + i%32 in
+// its low nibble and that + 32 in its high one, so the lane's elements are
+// 32 s + 16 (kb&1) + [0,16) of sub-block s = 4 (t&1) + 2 (kb>>1) + (t>>1):
+// its scale is byte 2 (kb>>1) + (t>>1) of scale word t&1 and its activation
+// chunk is 2 s + (kb&1).
+//
+// isum = 8 (X . Ba) + (X . Bb) as in MmqQ4K; msum = sum_j m_j S_j comes from
+// one f16 MFMA per superblock, K = 16 over the activation's 16-element sums
+// b_i (the quantizer's f16 copy: |b_i| <= 2032 is exact) against m_{i/2}
+// (<= 63): every product and partial sum is an integer below 2^24, exact in
+// the f32 accumulator.
+// The f32 step is MmqQ4K's y += d_x * (d * isum - dmin * msum), the same
+// operations in the same order.
+typedef _Float16 wh4 __attribute__((ext_vector_type(4)));
+typedef float wf4 __attribute__((ext_vector_type(4)));
+
+// LDS pointers kept in the LDS address space, so that no generic -> LDS
+// conversion (and its null check) sits between a ring slot and its DMA
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+__device__ __forceinline__ void lds_dma16_l(const uint8_t* g, lds_u8* l) {
+    __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+}
+__device__ __forceinline__ void lds_dma4_l(const uint8_t* g, lds_u8* l) { __builtin_amdgcn_global_load_lds(g, l, 4, 0, 0); }
+
+template <int... I, class Fn>
+__device__ __forceinline__ void static_for_impl(std::integer_sequence<int, I...>, Fn&& fn) {
+    (fn(std::integral_constant<int, I>{}), ...);
+}
+// fn(integral_constant<int, i>) for i = 0 .. n-1
+template <int n, class Fn>
+__device__ __forceinline__ void static_for(Fn&& fn) {
+    static_for_impl(std::make_integer_sequence<int, n>{}, fn);
+}
+
+template <int RT, int CT, int NW>
+struct WideTile {
+    static constexpr int BM = 16 * RT, BN = 16 * CT * NW, NT = 64 * NW;
+    // DMA instructions of a slot, by kind: activation rows (16 chunks a row,
+    // 64 an instruction), weight blocks (9 chunks a 144-byte block), the rows'
+    // 16-element sums (two chunks a row), their scales (4 bytes a lane)
+    static constexpr int CA = BM / 4, CW = (BN * 9 + 63) / 64, CS = (2 * BM + 63) / 64, CD = (BM + 63) / 64;
+    // every wavefront issues FA + FW + FS + FD of them, then XR "extra" ones
+    // from the remainders (the spare extras repeat the slot's last activation
+    // load: same source, same bytes, same place)
+    static constexpr int FA = CA / NW, FW = CW / NW, FS = CS / NW, FD = CD / NW;
+    static constexpr int RA = CA % NW, RW = CW % NW, RS = CS % NW, RD = CD % NW;
+    static constexpr int E = RA + RW + RS + RD, XR = (E + NW - 1) / NW;
+    static constexpr int NI = FA + FW + FS + FD + XR;  // per wavefront and superblock
+    static_assert(NI <= 63, "vmcnt range");
+    static constexpr int LA = CA * 1024, LW = CW * 1024, LS = CS * 1024, LD = CD * 256;
+    static constexpr int OW = LA, OS = LA + LW, OD = LA + LW + LS, LBUF = LA + LW + LS + LD;
+};
+
+// u16x2{v, v} of byte `sel` of w (a v_perm selector: bytes [b, 0, b, 0])
+__device__ __forceinline__ uint32_t byte_pair(uint32_t w, uint32_t sel) { return __builtin_amdgcn_perm(0u, w, sel); }
+
+__device__ __forceinline__ int bytes_times_p(uint32_t q, uint32_t f2) {
+    const u16x2 p = __builtin_bit_cast(u16x2, q) * __builtin_bit_cast(u16x2, f2);
+    return __builtin_bit_cast(int, p);
+}
+
+template <int RT, int CT, int NW>
+__global__ __launch_bounds__(64 * NW) void mmq_q4k_wide_kernel(const uint8_t* __restrict__ W, ActView act,
+                                                               float* __restrict__ y, int M, int N, int K, int ldy,
+                                                               int mt, int nt, int y_half) {
+    using T = WideTile<RT, CT, NW>;
+    constexpr int BM = T::BM, BN = T::BN;
+    __shared__ __align__(16) uint8_t sB0[T::LBUF], sB1[T::LBUF];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int KB = K / QK_K;
+    const uint32_t row_bytes = (uint32_t)KB * Q4K_BYTES;
+    const int l16 = lane & 15, kb = lane >> 4;
+
+    const int total = mt * nt, L = blockIdx.x;
+    const int x = L & 7, slot = L >> 3, q8 = total >> 3, r8 = total & 7;
+    const int tile = x * q8 + (x < r8 ? x : r8) + slot;  // XCD x's contiguous range of tiles
+    const int mtile = tile % mt, ntile = tile / mt;
+    const int m0 = mtile * BM, n0 = ntile * BN;
+
+    // per-lane source byte offsets (superblock 0) of DMA instruction i of each
+    // kind; rows past M read offset 0 and tail columns column N-1 (valid
+    // addresses; those bytes are never used)
+    auto a_src = [&](int i) {
+        const int q = 64 * i + lane, r = q >> 4, m = m0 + r;
+        return m < M ? (uint32_t)m * (uint32_t)K + 16u * (uint32_t)((q & 15) ^ (r & 15)) : 0u;
+    };
+    auto w_src = [&](int i) {
+        const int q = 64 * i + lane;
+        int n = n0 + q / 9;
+        n = n < N ? n : N - 1;
+        return (uint32_t)n * row_bytes + 16u * (uint32_t)(q % 9);
+    };
+    auto s_src = [&](int i) {
+        const int q = 64 * i + lane, r = q >> 1, m = m0 + r;
+        return r < BM && m < M ? 32u * (uint32_t)m * (uint32_t)KB + 16u * (uint32_t)(q & 1) : 0u;
+    };
+    auto d_src = [&](int i) {
+        const int q = 64 * i + lane, m = m0 + q;
+        return q < BM && m < M ? 4u * (uint32_t)m * (uint32_t)KB : 0u;
+    };
+    uint32_t asrc[T::FA > 0 ? T::FA : 1], wsrc[T::FW > 0 ? T::FW : 1], ssrc[T::FS > 0 ? T::FS : 1],
+        dsrc[T::FD > 0 ? T::FD : 1], xsrc[T::XR > 0 ? T::XR : 1];
+#pragma unroll
+    for (int j = 0; j < T::FA; j++) asrc[j] = a_src(j * NW + wave);
+#pragma unroll
+    for (int j = 0; j < T::FW; j++) wsrc[j] = w_src(j * NW + wave);
+#pragma unroll
+    for (int j = 0; j < T::FS; j++) ssrc[j] = s_src(j * NW + wave);
+#pragma unroll
+    for (int j = 0; j < T::FD; j++) dsrc[j] = d_src(j * NW + wave);
+    // extra x of this wavefront: remainder e = x NW + wave (wave-uniform kind)
+#pragma unroll
+    for (int x = 0; x < T::XR; x++) {
+        const int e = x * NW + wave;
+        if (e < T::RA) xsrc[x] = a_src(T::FA * NW + e);
+        else if (e < T::RA + T::RW) xsrc[x] = w_src(T::FW * NW + e - T::RA);
+        else if (e < T::RA + T::RW + T::RS) xsrc[x] = s_src(T::FS * NW + e - T::RA - T::RW);
+        else if (e < T::E) xsrc[x] = d_src(T::FD * NW + e - T::RA - T::RW - T::RS);
+        else xsrc[x] = a_src(T::CA - 1);
+    }
+    const uint8_t* qbase = reinterpret_cast<const uint8_t*>(act.qs);
+    const uint8_t* sbase = reinterpret_cast<const uint8_t*>(act.bsh);
+    const uint8_t* dbase = reinterpret_cast<const uint8_t*>(act.d);
+    // (each DMA writes at the instruction's LDS base + lane * size)
+    auto issue = [&](int b, lds_u8* buf) __attribute__((always_inline)) {
+        const uint32_t ub = (uint32_t)b;
+#pragma unroll
+        for (int j = 0; j < T::FA; j++) lds_dma16_l(qbase + (asrc[j] + ub * QK_K), buf + 1024 * (j * NW + wave));
+#pragma unroll
+        for (int j = 0; j < T::FW; j++) lds_dma16_l(W + (wsrc[j] + ub * Q4K_BYTES), buf + T::OW + 1024 * (j * NW + wave));
+#pragma unroll
+        for (int j = 0; j < T::FS; j++) lds_dma16_l(sbase + (ssrc[j] + ub * 32u), buf + T::OS + 1024 * (j * NW + wave));
+#pragma unroll
+        for (int j = 0; j < T::FD; j++) lds_dma4_l(dbase + (dsrc[j] + ub * 4u), buf + T::OD + 256 * (j * NW + wave));
+        // the extras: one branch per remainder slot, each with a compile-time
+        // kind and LDS place (wave-uniform conditions)
+        static_for<NW * T::XR>([&](auto ec) __attribute__((always_inline)) {
+            constexpr int e = decltype(ec)::value, x = e / NW;
+            if (wave != e % NW) return;
+            if constexpr (e < T::RA) {
+                lds_dma16_l(qbase + (xsrc[x] + ub * QK_K), buf + 1024 * (T::FA * NW + e));
+            } else if constexpr (e < T::RA + T::RW) {
+                lds_dma16_l(W + (xsrc[x] + ub * Q4K_BYTES), buf + T::OW + 1024 * (T::FW * NW + e - T::RA));
+            } else if constexpr (e < T::RA + T::RW + T::RS) {
+                lds_dma16_l(sbase + (xsrc[x] + ub * 32u), buf + T::OS + 1024 * (T::FS * NW + e - T::RA - T::RW));
+            } else if constexpr (e < T::E) {
+                lds_dma4_l(dbase + (xsrc[x] + ub * 4u), buf + T::OD + 256 * (T::FD * NW + e - T::RA - T::RW - T::RS));
+            } else {  // spare: the slot's last activation-row load again
+                lds_dma16_l(qbase + (xsrc[x] + ub * QK_K), buf + 1024 * (T::CA - 1));
+            }
+        });
+    };
+    // v_perm selectors of scale byte 2 (kb>>1) + (t>>1)
+    const uint32_t sel0 = (uint32_t)(2 * (kb >> 1)) * 0x00010001u | 0x0c000c00u;
+    const uint32_t sel1 = sel0 + 0x00010001u;
+    // msum B operand: bytes 2 (kb&1), 2 (kb&1) + 1 of min word kb>>1
+    const uint32_t msel = (uint32_t)(2 * (kb & 1)) * 0x01010101u + 0x01010000u;
+
+    float facc[RT][CT][4];
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int c = 0; c < CT; c++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) facc[r][c][i] = 0.0f;
+
+    const int b1 = KB;
+    lds_u8* const slot0 = (lds_u8*)sB0;
+    lds_u8* const slot1 = (lds_u8*)sB1;
+    issue(0, slot0);
+
+    auto iter = [&](auto kr, int b) __attribute__((always_inline)) {
+        constexpr int KR = decltype(kr)::value;
+        const uint8_t* A = KR == 0 ? sB0 : sB1;
+        const uint8_t* Wl = A + T::OW;
+        const uint8_t* S = A + T::OS;
+        const float* D = reinterpret_cast<const float*>(A + T::OD);
+        // superblock b landed, in every wavefront
+        __builtin_amdgcn_s_waitcnt(FRQ_VMCNT(0));
+        compiler_fence();
+        __builtin_amdgcn_s_barrier();
+        compiler_fence();
+        // everything this iteration reads from slot KR, into registers first:
+        // the slot's LDS reads all precede the DMA issued below, so no read
+        // can wait on it
+        uint4 hd[CT], raw[CT][2];
+        v4i afr[4][RT];
+        uint2 sv[RT];
+        float4 dx4[RT];
+#pragma unroll
+        for (int c = 0; c < CT; c++) {
+            const uint8_t* col = Wl + (16 * (CT * wave + c) + l16) * Q4K_BYTES;
+            hd[c] = *reinterpret_cast<const uint4*>(col);
+            raw[c][0] = *reinterpret_cast<const uint4*>(col + 16 + 16 * kb);
+            raw[c][1] = *reinterpret_cast<const uint4*>(col + 80 + 16 * kb);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int j = 8 * (t & 1) + 4 * (kb >> 1) + 2 * (t >> 1) + (kb & 1);  // activation chunk
+#pragma unroll
+            for (int r = 0; r < RT; r++)
+                afr[t][r] = *reinterpret_cast<const v4i*>(A + (16 * r + l16) * QK_K + 16 * (j ^ l16));
+        }
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            sv[r] = *reinterpret_cast<const uint2*>(S + (16 * r + l16) * 32 + 8 * kb);
+            dx4[r] = *reinterpret_cast<const float4*>(D + 16 * r + 4 * kb);
+        }
+        // the other slot was read at the top of iteration b-1, which every
+        // wavefront has left: b+1's DMA runs while b is multiplied
+        if (b + 1 < b1) issue(b + 1, KR == 0 ? slot1 : slot0);
+        // column headers: d, dmin, the 6-bit scales split as 8 a + b, the mins
+        float d[CT], dmin[CT];
+        uint32_t aw[CT][2], bw[CT][2], mw[CT];
+#pragma unroll
+        for (int c = 0; c < CT; c++) {
+            const uint32_t sc0 = hd[c].y & 0x3f3f3f3fu;
+            const uint32_t sc1 = (hd[c].w & 0x0f0f0f0fu) | (((hd[c].y >> 6) & 0x03030303u) << 4);
+            const uint32_t mn0 = hd[c].z & 0x3f3f3f3fu;
+            const uint32_t mn1 = ((hd[c].w >> 4) & 0x0f0f0f0fu) | (((hd[c].z >> 6) & 0x03030303u) << 4);
+            d[c] = f16_to_f32(hd[c].x & 0xffffu);
+            dmin[c] = f16_to_f32(hd[c].x >> 16);
+            aw[c][0] = (sc0 >> 3) & 0x07070707u;
+            aw[c][1] = (sc1 >> 3) & 0x07070707u;
+            bw[c][0] = sc0 & 0x07070707u;
+            bw[c][1] = sc1 & 0x07070707u;
+            mw[c] = kb < 2 ? mn0 : mn1;
+        }
+        v4i acc[RT][CT][2];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+#pragma unroll
+            for (int c = 0; c < CT; c++) {
+                const uint4 rw = raw[c][t & 1];
+                const uint32_t sh = t >= 2 ? 4u : 0u;
+                const uint32_t qd[4] = {(rw.x >> sh) & 0x0f0f0f0fu, (rw.y >> sh) & 0x0f0f0f0fu,
+                                        (rw.z >> sh) & 0x0f0f0f0fu, (rw.w >> sh) & 0x0f0f0f0fu};
+                const uint32_t sel = t >= 2 ? sel1 : sel0;
+                const uint32_t pa = byte_pair(aw[c][t & 1], sel), pb = byte_pair(bw[c][t & 1], sel);
+                const v4i ba = v4i{bytes_times_p(qd[0], pa), bytes_times_p(qd[1], pa), bytes_times_p(qd[2], pa),
+                                   bytes_times_p(qd[3], pa)};
+                const v4i bb = v4i{bytes_times_p(qd[0], pb), bytes_times_p(qd[1], pb), bytes_times_p(qd[2], pb),
+                                   bytes_times_p(qd[3], pb)};
+                const v4i zero = v4i{0, 0, 0, 0};
+#pragma unroll
+                for (int r = 0; r < RT; r++) {
+                    acc[r][c][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[t][r], ba, t == 0 ? zero : acc[r][c][0], 0, 0, 0);
+                    acc[r][c][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[t][r], bb, t == 0 ? zero : acc[r][c][1], 0, 0, 0);
+                }
+            }
+        }
+        // msum on f16 MFMA, then the f32 step
+        wh4 mb[CT];
+#pragma unroll
+        for (int c = 0; c < CT; c++) {
+            const uint32_t mm = __builtin_amdgcn_perm(0u, mw[c], msel);  // bytes m_lo, m_lo, m_hi, m_hi
+            mb[c] = wh4{(_Float16)(mm & 0xffu), (_Float16)((mm >> 8) & 0xffu), (_Float16)((mm >> 16) & 0xffu),
+                        (_Float16)(mm >> 24)};
+        }
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            const wh4 sa = __builtin_bit_cast(wh4, sv[r]);  // b_{4kb..4kb+3} as f16
+            const float dxv[4] = {dx4[r].x, dx4[r].y, dx4[r].z, dx4[r].w};
+#pragma unroll
+            for (int c = 0; c < CT; c++) {
+                const wf4 ms = __builtin_amdgcn_mfma_f32_16x16x16f16(sa, mb[c], wf4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int isum = 8 * acc[r][c][0][i] + acc[r][c][1][i];
+                    facc[r][c][i] = fmaf(dxv[i], fmaf(-dmin[c], ms[i], d[c] * (float)isum), facc[r][c][i]);
+                }
+            }
+        }
+    };
+    for (int b = 0; b < b1; b += 2) {
+        iter(std::integral_constant<int, 0>{}, b);
+        if (b + 1 < b1) iter(std::integral_constant<int, 1>{}, b + 1);
+    }
+
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int c = 0; c < CT; c++) {
+            const int n = n0 + 16 * (CT * wave + c) + l16;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = m0 + 16 * r + 4 * kb + i;
+                if (m < M && n < N) {
+                    if (y_half) reinterpret_cast<uint16_t*>(y)[(size_t)m * ldy + n] = f32_to_f16_rne(facc[r][c][i]);
+                    else y[(size_t)m * ldy + n] = facc[r][c][i];
+                }
+            }
+        }
+}
+
+template <int RT, int CT, int NW>
+hipError_t launch_wide(const uint8_t* w, ActView act, float* y, int M, int N, int K, int ldy, hipStream_t s,
+                       bool y_half) {
+    using T = WideTile<RT, CT, NW>;
+    const int mt = (M + T::BM - 1) / T::BM, nt = (N + T::BN - 1) / T::BN;
+    hipLaunchKernelGGL((mmq_q4k_wide_kernel<RT, CT, NW>), dim3(mt * nt), dim3(T::NT), 0, s, w, act, y, M, N, K, ldy,
+                       mt, nt, (int)y_half);
+    return hipGetLastError();
+}
+
 // y[m][n] = sum over splits z (in order) of part[z][m][n]
 __global__ void mmq_reduce_kernel(const float* __restrict__ part, float* __restrict__ y, int M, int N, int ldy,
                                   int nsplit, int y_half) {
@@ -667,6 +990,7 @@ enum MmqKind {
     MMQ_Q6K_32,
     MMQ_Q6K_64,
     MMQ_Q6K_128,
+    MMQ_Q4K_WIDE,      // 64 x 128, eight wavefronts side by side in N (16-byte aligned Q4_K blocks)
 };
 
 #define FRQ_MMQ_KINDS(X)                          \
@@ -700,6 +1024,10 @@ MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus, siz
         default: break;
     }
     while (p.ks > 1 && (size_t)p.ks * M * N > max_part_elems) p.ks--;
+    // from 128 rows, when the tiles fill the chip without a K split, the
+    // wide-tile kernel (two MFMAs per product instead of three; measured 10-17%
+    // faster at M = 512 on the 7B shapes)
+    if (dma && M >= 128 && p.ks == 1) p.kind = MMQ_Q4K_WIDE;
     p.part_elems = p.ks > 1 ? (size_t)p.ks * M * N : 0;
     return p;
 }
@@ -712,6 +1040,7 @@ hipError_t launch_mmq(const MmqPlan& plan, int dtype, const uint8_t* w, ActView 
     case kind: return launch_cfg<F, RT, CT, WM, WN, DMA>(plan, w, act, y, part, M, N, K, ldy, s, y_half);
         FRQ_MMQ_KINDS(FRQ_LAUNCH)
 #undef FRQ_LAUNCH
+        case MMQ_Q4K_WIDE: return launch_wide<4, 1, 8>(w, act, y, M, N, K, ldy, s, y_half);
         default: return hipErrorInvalidValue;
     }
 }

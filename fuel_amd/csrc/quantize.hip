@@ -14,7 +14,10 @@ __global__ __launch_bounds__(64) void quantize_q8k_kernel(const float* __restric
     const int KB = K / QK_K;
     const Q8KWave r = q8k_quantize_wave(x + (size_t)m * K + (size_t)b * QK_K, lane);
     reinterpret_cast<uint32_t*>(act.qs + (size_t)m * K + (size_t)b * QK_K)[lane] = r.packed;
-    if ((lane & 3) == 0) act.bsums[((size_t)m * KB + b) * 16 + (lane >> 2)] = (int16_t)r.bsum;
+    if ((lane & 3) == 0) {
+        act.bsums[((size_t)m * KB + b) * 16 + (lane >> 2)] = (int16_t)r.bsum;
+        if (act.bsh) act.bsh[((size_t)m * KB + b) * 16 + (lane >> 2)] = f32_to_f16_rne((float)r.bsum);
+    }
     if (lane == 0) act.d[(size_t)m * KB + b] = r.d;
     if (aos) {
         uint8_t* blk = aos + ((size_t)m * KB + b) * Q8K_BYTES;
@@ -34,7 +37,10 @@ __global__ __launch_bounds__(64) void quantize_q8k_h_kernel(const uint16_t* __re
                                  f16_to_f32(h.y >> 16));
     const Q8KWave r = q8k_quantize_vals(v, lane);
     reinterpret_cast<uint32_t*>(act.qs + (size_t)m * K + (size_t)b * QK_K)[lane] = r.packed;
-    if ((lane & 3) == 0) act.bsums[((size_t)m * KB + b) * 16 + (lane >> 2)] = (int16_t)r.bsum;
+    if ((lane & 3) == 0) {
+        act.bsums[((size_t)m * KB + b) * 16 + (lane >> 2)] = (int16_t)r.bsum;
+        if (act.bsh) act.bsh[((size_t)m * KB + b) * 16 + (lane >> 2)] = f32_to_f16_rne((float)r.bsum);
+    }
     if (lane == 0) act.d[(size_t)m * KB + b] = r.d;
 }
 
@@ -51,7 +57,10 @@ __global__ __launch_bounds__(64) void quantize_q8k_swiglu_kernel(const float* __
                                  silu_mul(gv.w, uv.w));
     const Q8KWave r = q8k_quantize_vals(h, lane);
     reinterpret_cast<uint32_t*>(act.qs + (size_t)m * K + (size_t)b * QK_K)[lane] = r.packed;
-    if ((lane & 3) == 0) act.bsums[((size_t)m * KB + b) * 16 + (lane >> 2)] = (int16_t)r.bsum;
+    if ((lane & 3) == 0) {
+        act.bsums[((size_t)m * KB + b) * 16 + (lane >> 2)] = (int16_t)r.bsum;
+        if (act.bsh) act.bsh[((size_t)m * KB + b) * 16 + (lane >> 2)] = f32_to_f16_rne((float)r.bsum);
+    }
     if (lane == 0) act.d[(size_t)m * KB + b] = r.d;
 }
 
