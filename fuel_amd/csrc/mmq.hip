@@ -577,10 +577,12 @@ __global__ __launch_bounds__(64 * WM * WN) void mmq_dma_kernel(const uint8_t* __
 // staging registers, no LDS stores): the activation rows (256 bytes each,
 // chunk j of row r at position j ^ (r & 15)), the raw weight blocks of the
 // BN columns (144 bytes apart, in their byte order), the rows' 16-element
-// sums (32 bytes a row) and their scales.  Three slots: superblock b+2 is in
-// flight while b is multiplied; the DMA instructions of a slot are dealt out
+// sums (32 bytes a row) and their scales.  Two slots: superblock b+1 is in
+// flight while b is multiplied (issued right after the barrier that ends
+// everyone's reads of its slot); the DMA instructions of a slot are dealt out
 // round-robin to the wavefronts, each issuing the same count (the spare ones
-// repeat the slot's last instruction: same source, same bytes, same place).
+// repeat the slot's last activation load: same source, same bytes, same
+// place).
 //
 // K order inside a superblock: K step t (64 elements) has lane group kb take
 // the 16 elements of qs bytes 64 (t&1) + 16 kb .. +15, low nibbles for t < 2
@@ -601,13 +603,32 @@ __global__ __launch_bounds__(64 * WM * WN) void mmq_dma_kernel(const uint8_t* __
 typedef _Float16 wh4 __attribute__((ext_vector_type(4)));
 typedef float wf4 __attribute__((ext_vector_type(4)));
 
-// LDS pointers kept in the LDS address space, so that no generic -> LDS
-// conversion (and its null check) sits between a ring slot and its DMA
-typedef __attribute__((address_space(3))) uint8_t lds_u8;
-__device__ __forceinline__ void lds_dma16_l(const uint8_t* g, lds_u8* l) {
-    __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+// LDS DMA through inline assembly: the compiler does not see these loads, so
+// it inserts no waits of its own for them (it cannot tell the ring slot being
+// filled from the slot being read and would wait for every load in flight
+// before the first read); the kernel's explicit waits are the only ones, and
+// they are exact: before a slot is read, s_waitcnt vmcnt(0) and a barrier.
+// The compiler's waits for its own loads stay safe, since vmcnt counts in
+// issue order and hidden loads only make them wait longer.  M0 holds the LDS
+// address of lane 0 (wave-uniform), lane i writes at M0 + i * size, with one
+// wait state between the M0 write and the DMA.  Nothing else in the kernel
+// that issues these uses M0 (no indirect register indexing, no LDS-DMA
+// builtins, no messages), so the clobber the compiler cannot preserve loses
+// nothing.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16_asm(const uint8_t* base, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
+                 : "memory", "m0");
 }
-__device__ __forceinline__ void lds_dma4_l(const uint8_t* g, lds_u8* l) { __builtin_amdgcn_global_load_lds(g, l, 4, 0, 0); }
+__device__ __forceinline__ void dma4_asm(const uint8_t* base, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
+}
 
 template <int... I, class Fn>
 __device__ __forceinline__ void static_for_impl(std::integer_sequence<int, I...>, Fn&& fn) {
@@ -711,31 +732,31 @@ __global__ __launch_bounds__(64 * NW) void mmq_q4k_wide_kernel(const uint8_t* __
     const uint8_t* sbase = reinterpret_cast<const uint8_t*>(act.bsh);
     const uint8_t* dbase = reinterpret_cast<const uint8_t*>(act.d);
     // (each DMA writes at the instruction's LDS base + lane * size)
-    auto issue = [&](int b, lds_u8* buf) __attribute__((always_inline)) {
+    auto issue = [&](int b, uint32_t buf) __attribute__((always_inline)) {
         const uint32_t ub = (uint32_t)b;
 #pragma unroll
-        for (int j = 0; j < T::FA; j++) lds_dma16_l(qbase + (asrc[j] + ub * QK_K), buf + 1024 * (j * NW + wave));
+        for (int j = 0; j < T::FA; j++) dma16_asm(qbase, asrc[j] + ub * QK_K, buf + (uint32_t)(1024 * (j * NW + wave)));
 #pragma unroll
-        for (int j = 0; j < T::FW; j++) lds_dma16_l(W + (wsrc[j] + ub * Q4K_BYTES), buf + T::OW + 1024 * (j * NW + wave));
+        for (int j = 0; j < T::FW; j++) dma16_asm(W, wsrc[j] + ub * Q4K_BYTES, buf + (uint32_t)(T::OW + 1024 * (j * NW + wave)));
 #pragma unroll
-        for (int j = 0; j < T::FS; j++) lds_dma16_l(sbase + (ssrc[j] + ub * 32u), buf + T::OS + 1024 * (j * NW + wave));
+        for (int j = 0; j < T::FS; j++) dma16_asm(sbase, ssrc[j] + ub * 32u, buf + (uint32_t)(T::OS + 1024 * (j * NW + wave)));
 #pragma unroll
-        for (int j = 0; j < T::FD; j++) lds_dma4_l(dbase + (dsrc[j] + ub * 4u), buf + T::OD + 256 * (j * NW + wave));
+        for (int j = 0; j < T::FD; j++) dma4_asm(dbase, dsrc[j] + ub * 4u, buf + (uint32_t)(T::OD + 256 * (j * NW + wave)));
         // the extras: one branch per remainder slot, each with a compile-time
         // kind and LDS place (wave-uniform conditions)
         static_for<NW * T::XR>([&](auto ec) __attribute__((always_inline)) {
             constexpr int e = decltype(ec)::value, x = e / NW;
             if (wave != e % NW) return;
             if constexpr (e < T::RA) {
-                lds_dma16_l(qbase + (xsrc[x] + ub * QK_K), buf + 1024 * (T::FA * NW + e));
+                dma16_asm(qbase, xsrc[x] + ub * QK_K, buf + (uint32_t)(1024 * (T::FA * NW + e)));
             } else if constexpr (e < T::RA + T::RW) {
-                lds_dma16_l(W + (xsrc[x] + ub * Q4K_BYTES), buf + T::OW + 1024 * (T::FW * NW + e - T::RA));
+                dma16_asm(W, xsrc[x] + ub * Q4K_BYTES, buf + (uint32_t)(T::OW + 1024 * (T::FW * NW + e - T::RA)));
             } else if constexpr (e < T::RA + T::RW + T::RS) {
-                lds_dma16_l(sbase + (xsrc[x] + ub * 32u), buf + T::OS + 1024 * (T::FS * NW + e - T::RA - T::RW));
+                dma16_asm(sbase, xsrc[x] + ub * 32u, buf + (uint32_t)(T::OS + 1024 * (T::FS * NW + e - T::RA - T::RW)));
             } else if constexpr (e < T::E) {
-                lds_dma4_l(dbase + (xsrc[x] + ub * 4u), buf + T::OD + 256 * (T::FD * NW + e - T::RA - T::RW - T::RS));
+                dma4_asm(dbase, xsrc[x] + ub * 4u, buf + (uint32_t)(T::OD + 256 * (T::FD * NW + e - T::RA - T::RW - T::RS)));
             } else {  // spare: the slot's last activation-row load again
-                lds_dma16_l(qbase + (xsrc[x] + ub * QK_K), buf + 1024 * (T::CA - 1));
+                dma16_asm(qbase, xsrc[x] + ub * QK_K, buf + (uint32_t)(1024 * (T::CA - 1)));
             }
         });
     };
@@ -754,8 +775,7 @@ __global__ __launch_bounds__(64 * NW) void mmq_q4k_wide_kernel(const uint8_t* __
             for (int i = 0; i < 4; i++) facc[r][c][i] = 0.0f;
 
     const int b1 = KB;
-    lds_u8* const slot0 = (lds_u8*)sB0;
-    lds_u8* const slot1 = (lds_u8*)sB1;
+    const uint32_t slot0 = lds_addr(sB0), slot1 = lds_addr(sB1);
     issue(0, slot0);
 
     auto iter = [&](auto kr, int b) __attribute__((always_inline)) {
@@ -764,45 +784,23 @@ __global__ __launch_bounds__(64 * NW) void mmq_q4k_wide_kernel(const uint8_t* __
         const uint8_t* Wl = A + T::OW;
         const uint8_t* S = A + T::OS;
         const float* D = reinterpret_cast<const float*>(A + T::OD);
-        // superblock b landed, in every wavefront
+        // superblock b landed (the only loads in flight), in every wavefront
         __builtin_amdgcn_s_waitcnt(FRQ_VMCNT(0));
         compiler_fence();
         __builtin_amdgcn_s_barrier();
         compiler_fence();
-        // everything this iteration reads from slot KR, into registers first:
-        // the slot's LDS reads all precede the DMA issued below, so no read
-        // can wait on it
-        uint4 hd[CT], raw[CT][2];
-        v4i afr[4][RT];
-        uint2 sv[RT];
-        float4 dx4[RT];
-#pragma unroll
-        for (int c = 0; c < CT; c++) {
-            const uint8_t* col = Wl + (16 * (CT * wave + c) + l16) * Q4K_BYTES;
-            hd[c] = *reinterpret_cast<const uint4*>(col);
-            raw[c][0] = *reinterpret_cast<const uint4*>(col + 16 + 16 * kb);
-            raw[c][1] = *reinterpret_cast<const uint4*>(col + 80 + 16 * kb);
-        }
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const int j = 8 * (t & 1) + 4 * (kb >> 1) + 2 * (t >> 1) + (kb & 1);  // activation chunk
-#pragma unroll
-            for (int r = 0; r < RT; r++)
-                afr[t][r] = *reinterpret_cast<const v4i*>(A + (16 * r + l16) * QK_K + 16 * (j ^ l16));
-        }
-#pragma unroll
-        for (int r = 0; r < RT; r++) {
-            sv[r] = *reinterpret_cast<const uint2*>(S + (16 * r + l16) * 32 + 8 * kb);
-            dx4[r] = *reinterpret_cast<const float4*>(D + 16 * r + 4 * kb);
-        }
-        // the other slot was read at the top of iteration b-1, which every
-        // wavefront has left: b+1's DMA runs while b is multiplied
+        // the other slot was read in iteration b-1, which every wavefront has
+        // left: b+1's DMA runs while b is multiplied
         if (b + 1 < b1) issue(b + 1, KR == 0 ? slot1 : slot0);
         // column headers: d, dmin, the 6-bit scales split as 8 a + b, the mins
         float d[CT], dmin[CT];
         uint32_t aw[CT][2], bw[CT][2], mw[CT];
+        uint4 hd[CT];
+        const uint8_t* col[CT];
 #pragma unroll
         for (int c = 0; c < CT; c++) {
+            col[c] = Wl + (16 * (CT * wave + c) + l16) * Q4K_BYTES;
+            hd[c] = *reinterpret_cast<const uint4*>(col[c]);
             const uint32_t sc0 = hd[c].y & 0x3f3f3f3fu;
             const uint32_t sc1 = (hd[c].w & 0x0f0f0f0fu) | (((hd[c].y >> 6) & 0x03030303u) << 4);
             const uint32_t mn0 = hd[c].z & 0x3f3f3f3fu;
@@ -818,9 +816,13 @@ __global__ __launch_bounds__(64 * NW) void mmq_q4k_wide_kernel(const uint8_t* __
         v4i acc[RT][CT][2];
 #pragma unroll
         for (int t = 0; t < 4; t++) {
+            const int j = 8 * (t & 1) + 4 * (kb >> 1) + 2 * (t >> 1) + (kb & 1);  // activation chunk
+            v4i afr[RT];
+#pragma unroll
+            for (int r = 0; r < RT; r++) afr[r] = *reinterpret_cast<const v4i*>(A + (16 * r + l16) * QK_K + 16 * (j ^ l16));
 #pragma unroll
             for (int c = 0; c < CT; c++) {
-                const uint4 rw = raw[c][t & 1];
+                const uint4 rw = *reinterpret_cast<const uint4*>(col[c] + 16 + 64 * (t & 1) + 16 * kb);
                 const uint32_t sh = t >= 2 ? 4u : 0u;
                 const uint32_t qd[4] = {(rw.x >> sh) & 0x0f0f0f0fu, (rw.y >> sh) & 0x0f0f0f0fu,
                                         (rw.z >> sh) & 0x0f0f0f0fu, (rw.w >> sh) & 0x0f0f0f0fu};
@@ -833,8 +835,8 @@ __global__ __launch_bounds__(64 * NW) void mmq_q4k_wide_kernel(const uint8_t* __
                 const v4i zero = v4i{0, 0, 0, 0};
 #pragma unroll
                 for (int r = 0; r < RT; r++) {
-                    acc[r][c][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[t][r], ba, t == 0 ? zero : acc[r][c][0], 0, 0, 0);
-                    acc[r][c][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[t][r], bb, t == 0 ? zero : acc[r][c][1], 0, 0, 0);
+                    acc[r][c][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r], ba, t == 0 ? zero : acc[r][c][0], 0, 0, 0);
+                    acc[r][c][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r], bb, t == 0 ? zero : acc[r][c][1], 0, 0, 0);
                 }
             }
         }
@@ -848,8 +850,9 @@ __global__ __launch_bounds__(64 * NW) void mmq_q4k_wide_kernel(const uint8_t* __
         }
 #pragma unroll
         for (int r = 0; r < RT; r++) {
-            const wh4 sa = __builtin_bit_cast(wh4, sv[r]);  // b_{4kb..4kb+3} as f16
-            const float dxv[4] = {dx4[r].x, dx4[r].y, dx4[r].z, dx4[r].w};
+            const wh4 sa = *reinterpret_cast<const wh4*>(S + (16 * r + l16) * 32 + 8 * kb);  // b_{4kb..4kb+3}
+            const float4 dx = *reinterpret_cast<const float4*>(D + 16 * r + 4 * kb);
+            const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
 #pragma unroll
             for (int c = 0; c < CT; c++) {
                 const wf4 ms = __builtin_amdgcn_mfma_f32_16x16x16f16(sa, mb[c], wf4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
@@ -1025,8 +1028,8 @@ MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus, siz
     }
     while (p.ks > 1 && (size_t)p.ks * M * N > max_part_elems) p.ks--;
     // from 128 rows, when the tiles fill the chip without a K split, the
-    // wide-tile kernel (two MFMAs per product instead of three; measured 10-17%
-    // faster at M = 512 on the 7B shapes)
+    // wide-tile kernel (two MFMAs per product instead of three, DMA ring out of
+    // the compiler's sight; measured 19-25% faster at M = 512 on the 7B shapes)
     if (dma && M >= 128 && p.ks == 1) p.kind = MMQ_Q4K_WIDE;
     p.part_elems = p.ks > 1 ? (size_t)p.ks * M * N : 0;
     return p;
