@@ -885,6 +885,194 @@ __global__ __launch_bounds__(64 * NW) void mmq_q4k_wide_kernel(const uint8_t* __
         }
 }
 
+// ---- Q6_K, wide tiles ----
+// The same skeleton for Q6_K: NW wavefronts side by side in N share 16 RT
+// activation rows, one 16-column tile each, so each weight block is turned
+// into its byte planes once per workgroup; activation rows and scales come by
+// DMA (the assembly issue above), two slots.  210-byte blocks are only 2-byte
+// aligned, so the weights are staged through registers instead: the next
+// superblock's 14 chunks per column (MmqQ6K's layout, 224 bytes a column) are
+// loaded right after the barrier and stored to the other slot after the
+// arithmetic.  Products, planes and the f32 step are MmqQ6K's.
+template <int RT, int NW>
+struct WideTile6 {
+    using F = MmqQ6K;
+    static constexpr int BM = 16 * RT, BN = 16 * NW, NT = 64 * NW;
+    static constexpr int CA = BM / 4, CD = (BM + 63) / 64;
+    static constexpr int FA = CA / NW, FD = CD / NW, RA = CA % NW, RD = CD % NW;
+    static constexpr int E = RA + RD, XR = (E + NW - 1) / NW;
+    static constexpr int W_CH = BN * F::CH, W_PT = (W_CH + NT - 1) / NT;
+    static constexpr int LA = CA * 1024, LW = BN * F::STRIDE, LD = CD * 256;
+    static constexpr int OW = LA, OD = LA + LW, LBUF = LA + LW + LD;
+};
+
+template <int RT, int NW>
+__global__ __launch_bounds__(64 * NW) void mmq_q6k_wide_kernel(const uint8_t* __restrict__ W, ActView act,
+                                                               float* __restrict__ y, int M, int N, int K, int ldy,
+                                                               int mt, int nt, int y_half) {
+    using T = WideTile6<RT, NW>;
+    using F = MmqQ6K;
+    constexpr int BM = T::BM, BN = T::BN;
+    __shared__ __align__(16) uint8_t sB0[T::LBUF], sB1[T::LBUF];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int KB = K / QK_K;
+    const uint32_t row_bytes = (uint32_t)KB * Q6K_BYTES;
+    const int l16 = lane & 15, kb = lane >> 4;
+
+    const int total = mt * nt, L = blockIdx.x;
+    const int x = L & 7, slot = L >> 3, q8 = total >> 3, r8 = total & 7;
+    const int tile = x * q8 + (x < r8 ? x : r8) + slot;  // XCD x's contiguous range of tiles
+    const int mtile = tile % mt, ntile = tile / mt;
+    const int m0 = mtile * BM, n0 = ntile * BN;
+
+    auto a_src = [&](int i) {
+        const int q = 64 * i + lane, r = q >> 4, m = m0 + r;
+        return m < M ? (uint32_t)m * (uint32_t)K + 16u * (uint32_t)((q & 15) ^ (r & 15)) : 0u;
+    };
+    auto d_src = [&](int i) {
+        const int q = 64 * i + lane, m = m0 + q;
+        return q < BM && m < M ? 4u * (uint32_t)m * (uint32_t)KB : 0u;
+    };
+    uint32_t asrc[T::FA > 0 ? T::FA : 1], dsrc[T::FD > 0 ? T::FD : 1], xsrc[T::XR > 0 ? T::XR : 1];
+#pragma unroll
+    for (int j = 0; j < T::FA; j++) asrc[j] = a_src(j * NW + wave);
+#pragma unroll
+    for (int j = 0; j < T::FD; j++) dsrc[j] = d_src(j * NW + wave);
+#pragma unroll
+    for (int x = 0; x < T::XR; x++) {
+        const int e = x * NW + wave;
+        if (e < T::RA) xsrc[x] = a_src(T::FA * NW + e);
+        else if (e < T::E) xsrc[x] = d_src(T::FD * NW + e - T::RA);
+        else xsrc[x] = a_src(T::CA - 1);
+    }
+    // weight chunks of this thread: chunk idx = tid + i NT of the tile (column
+    // idx / 14, MmqQ6K chunk idx % 14); tail columns re-read column N-1
+    uint32_t wsrc[T::W_PT], wdst[T::W_PT];
+#pragma unroll
+    for (int i = 0; i < T::W_PT; i++) {
+        const int idx = tid + i * T::NT;
+        const int c = idx < T::W_CH ? idx / F::CH : 0, ch = idx % F::CH;
+        int n = n0 + c;
+        n = n < N ? n : N - 1;
+        wsrc[i] = (uint32_t)n * row_bytes + F::src(ch);
+        wdst[i] = (uint32_t)(T::OW + c * F::STRIDE + 16 * ch);
+    }
+    const uint8_t* qbase = reinterpret_cast<const uint8_t*>(act.qs);
+    const uint8_t* dbase = reinterpret_cast<const uint8_t*>(act.d);
+    auto issue = [&](int b, uint32_t buf) __attribute__((always_inline)) {
+        const uint32_t ub = (uint32_t)b;
+#pragma unroll
+        for (int j = 0; j < T::FA; j++) dma16_asm(qbase, asrc[j] + ub * QK_K, buf + (uint32_t)(1024 * (j * NW + wave)));
+#pragma unroll
+        for (int j = 0; j < T::FD; j++) dma4_asm(dbase, dsrc[j] + ub * 4u, buf + (uint32_t)(T::OD + 256 * (j * NW + wave)));
+        static_for<NW * T::XR>([&](auto ec) __attribute__((always_inline)) {
+            constexpr int e = decltype(ec)::value, x = e / NW;
+            if (wave != e % NW) return;
+            if constexpr (e < T::RA) {
+                dma16_asm(qbase, xsrc[x] + ub * QK_K, buf + (uint32_t)(1024 * (T::FA * NW + e)));
+            } else if constexpr (e < T::E) {
+                dma4_asm(dbase, xsrc[x] + ub * 4u, buf + (uint32_t)(T::OD + 256 * (T::FD * NW + e - T::RA)));
+            } else {  // spare: the slot's last activation-row load again
+                dma16_asm(qbase, xsrc[x] + ub * QK_K, buf + (uint32_t)(1024 * (T::CA - 1)));
+            }
+        });
+    };
+    uint4 wreg[T::W_PT];
+    auto wload = [&](int b) __attribute__((always_inline)) {
+        const uint32_t o = (uint32_t)b * Q6K_BYTES;
+#pragma unroll
+        for (int i = 0; i < T::W_PT; i++) {
+            wreg[i] = uint4{0u, 0u, 0u, 0u};
+            if (tid + i * T::NT < T::W_CH) wreg[i] = load16_u(W + (wsrc[i] + o));
+        }
+    };
+    auto wstore = [&](uint8_t* buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < T::W_PT; i++)
+            if (tid + i * T::NT < T::W_CH) *reinterpret_cast<uint4*>(buf + wdst[i]) = wreg[i];
+    };
+
+    float facc[RT][4];
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) facc[r][i] = 0.0f;
+
+    const int b1 = KB;
+    const uint32_t slot0 = lds_addr(sB0), slot1 = lds_addr(sB1);
+    issue(0, slot0);
+    wload(0);
+    wstore(sB0);
+
+    auto iter = [&](auto kr, int b) __attribute__((always_inline)) {
+        constexpr int KR = decltype(kr)::value;
+        const uint8_t* A = KR == 0 ? sB0 : sB1;
+        const uint8_t* Wl = A + T::OW;
+        const float* D = reinterpret_cast<const float*>(A + T::OD);
+        // superblock b landed (the DMA: vmcnt; this wavefront's weight stores:
+        // lgkmcnt), in every wavefront
+        __builtin_amdgcn_s_waitcnt(FRQ_VMCNT(0) & ~(0xF << 8));
+        compiler_fence();
+        __builtin_amdgcn_s_barrier();
+        compiler_fence();
+        // the other slot was read in iteration b-1: b+1's loads run while b is multiplied
+        const bool more = b + 1 < b1;
+        if (more) {
+            issue(b + 1, KR == 0 ? slot1 : slot0);
+            wload(b + 1);
+        }
+        const uint8_t* col = Wl + (16 * wave + l16) * F::STRIDE;
+        typename F::Hdr hdr;
+        F::header(col, hdr);
+        v4i acc[RT][1][F::NACC];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            v4i afr[RT];
+#pragma unroll
+            for (int r = 0; r < RT; r++)
+                afr[r] = *reinterpret_cast<const v4i*>(A + (16 * r + l16) * QK_K + 16 * ((4 * t + kb) ^ l16));
+            F::template step<RT, 1>(t, kb, 0, col, hdr, afr, acc);
+        }
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            const float4 dx = *reinterpret_cast<const float4*>(D + 16 * r + 4 * kb);
+            const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) facc[r][i] = fmaf(dxv[i], F::finish(acc[r][0], i, hdr), facc[r][i]);
+        }
+        if (more) wstore(KR == 0 ? sB1 : sB0);
+    };
+    for (int b = 0; b < b1; b += 2) {
+        iter(std::integral_constant<int, 0>{}, b);
+        if (b + 1 < b1) iter(std::integral_constant<int, 1>{}, b + 1);
+    }
+    __builtin_amdgcn_s_waitcnt(FRQ_VMCNT(0));
+
+    const int n = n0 + 16 * wave + l16;
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = m0 + 16 * r + 4 * kb + i;
+            if (m < M && n < N) {
+                if (y_half) reinterpret_cast<uint16_t*>(y)[(size_t)m * ldy + n] = f32_to_f16_rne(facc[r][i]);
+                else y[(size_t)m * ldy + n] = facc[r][i];
+            }
+        }
+}
+
+template <int RT, int NW>
+hipError_t launch_wide6(const uint8_t* w, ActView act, float* y, int M, int N, int K, int ldy, hipStream_t s,
+                        bool y_half) {
+    using T = WideTile6<RT, NW>;
+    const int mt = (M + T::BM - 1) / T::BM, nt = (N + T::BN - 1) / T::BN;
+    hipLaunchKernelGGL((mmq_q6k_wide_kernel<RT, NW>), dim3(mt * nt), dim3(T::NT), 0, s, w, act, y, M, N, K, ldy, mt,
+                       nt, (int)y_half);
+    return hipGetLastError();
+}
+
 template <int RT, int CT, int NW>
 hipError_t launch_wide(const uint8_t* w, ActView act, float* y, int M, int N, int K, int ldy, hipStream_t s,
                        bool y_half) {
@@ -994,6 +1182,7 @@ enum MmqKind {
     MMQ_Q6K_64,
     MMQ_Q6K_128,
     MMQ_Q4K_WIDE,      // 64 x 128, eight wavefronts side by side in N (16-byte aligned Q4_K blocks)
+    MMQ_Q6K_WIDE,      // 64 x 128, the same for Q6_K
 };
 
 #define FRQ_MMQ_KINDS(X)                          \
@@ -1028,9 +1217,11 @@ MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus, siz
     }
     while (p.ks > 1 && (size_t)p.ks * M * N > max_part_elems) p.ks--;
     // from 128 rows, when the tiles fill the chip without a K split, the
-    // wide-tile kernel (two MFMAs per product instead of three, DMA ring out of
-    // the compiler's sight; measured 19-25% faster at M = 512 on the 7B shapes)
+    // wide-tile kernels (Q4_K: two MFMAs per product instead of three; both:
+    // the DMA ring out of the compiler's sight; Q4_K measured 19-25% faster at
+    // M = 512 on the 7B shapes)
     if (dma && M >= 128 && p.ks == 1) p.kind = MMQ_Q4K_WIDE;
+    if (dtype == GGML_Q6K && M >= 128 && p.ks == 1) p.kind = MMQ_Q6K_WIDE;
     p.part_elems = p.ks > 1 ? (size_t)p.ks * M * N : 0;
     return p;
 }
@@ -1044,6 +1235,7 @@ hipError_t launch_mmq(const MmqPlan& plan, int dtype, const uint8_t* w, ActView 
         FRQ_MMQ_KINDS(FRQ_LAUNCH)
 #undef FRQ_LAUNCH
         case MMQ_Q4K_WIDE: return launch_wide<4, 1, 8>(w, act, y, M, N, K, ldy, s, y_half);
+        case MMQ_Q6K_WIDE: return launch_wide6<4, 8>(w, act, y, M, N, K, ldy, s, y_half);
         default: return hipErrorInvalidValue;
     }
 }

@@ -399,26 +399,27 @@ def test_qmatmul_mfma_7b_shapes(dev, dt, k, n, m):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("dt", [O.Q4K, O.Q6K])
 @pytest.mark.parametrize("m,n,k", [(130, 8200, 256), (200, 4100, 512), (333, 3000, 768), (129, 9000, 1280)])
-def test_qmatmul_q4k_wide_tiles(dev, m, n, k):
-    """Q4_K from 128 rows when the tiles fill the chip without a K split: the
-    wide-tile kernel (64-row x 128-column workgroups, one to five superblocks
-    through its LDS ring, a ragged last row tile and column tile), f32 and f16
-    outputs, against the oracle."""
-    say("wide q4k", m, n, k)
-    wq = weights(O.Q4K, n, k)
+def test_qmatmul_wide_tiles(dev, dt, m, n, k):
+    """Q4_K / Q6_K from 128 rows when the tiles fill the chip without a K
+    split: the wide-tile kernels (64-row x 128-column workgroups, one to five
+    superblocks through the two-slot LDS ring, a ragged last row tile and
+    column tile), f32 and f16 outputs, against the oracle."""
+    say("wide", dt, m, n, k)
+    wq = weights(dt, n, k)
     x = acts(m, k)
-    want = O.matmul(O.Q4K, x, wq)
+    want = O.matmul(dt, x, wq)
     out = dev.alloc((m, n), np.float32)
     F.qmatmul_f32_rocm_wrapper([dev.from_numpy(x), dev.from_numpy(as_u32(wq))], [out],
-                               F.QMatMulParams(O.Q4K, 1, m, n, k))
+                               F.QMatMulParams(dt, 1, m, n, k))
     err = rel_err(out.numpy(), want)
     say("  rel_err", err)
     assert err <= TOL
-    qs = dev.load_quantized(O.Q4K, wq.tobytes())
+    qs = dev.load_quantized(dt, wq.tobytes())
     x16 = O.f32_to_f16_bits(x)
     y16, _ = qs.fwd((n, k), dev.from_numpy(x16.view(np.float16)))
-    err16 = rel_err(O.f16_bits_to_f32(y16.numpy().view(np.uint16)), O.f16_bits_to_f32(O.matmul_f16(O.Q4K, x16, wq)))
+    err16 = rel_err(O.f16_bits_to_f32(y16.numpy().view(np.uint16)), O.f16_bits_to_f32(O.matmul_f16(dt, x16, wq)))
     say("  f16 rel_err", err16)
     assert err16 <= TOL_F16
 
