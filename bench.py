@@ -381,6 +381,59 @@ def probe_leg(k: int, n: int, dtype: int, m: int, reps_target: int = 200) -> dic
             "calls": reps * R}
 
 
+READ_WGPC = (1, 2, 4, 8, 16)
+READ_UNROLL = (1, 2, 4, 8)
+
+
+def read_ceiling_leg(nbytes: int, shapes=None, reps_target: int = 200) -> dict:
+    """The HBM read ceiling of one launch of `nbytes`: frq_probe_read (a
+    kernel that only streams the bytes in, no arithmetic) over a rotation of
+    >= 1.2 GB of copies, graph-replayed and HIP-event timed like the mat-vec,
+    for each launch shape (workgroups per CU x loads in flight per thread) in
+    `shapes` (default: every one of READ_WGPC x READ_UNROLL); the best is the
+    ceiling the mat-vec's roofline fraction is read against."""
+    import ctypes as C
+
+    import fuel_amd as F
+    from fuel_amd.hiprt import HipRuntime
+
+    hip = HipRuntime()
+    dev = F.RocmDevice(0)
+    stream = hip.stream_create()
+    dev.set_stream(stream)
+    lib = F.lib()
+    R = max(2, math.ceil(ROTATE_BYTES / nbytes))
+    bufs = [F.fill_random_bits(dev, nbytes // 4, 0, SEED, 0, 300 + r) for r in range(R)]
+    sink = dev.alloc((1,), np.int32)
+    dev.synchronize()
+    shapes = shapes or [(w, u) for w in READ_WGPC for u in READ_UNROLL]
+    e0, e1 = hip.event_create(), hip.event_create()
+    res = {}
+    for wgpc, unroll in shapes:
+        def call(i, wgpc=wgpc, unroll=unroll):
+            F._native.check(lib.frq_probe_read(dev.handle, C.c_void_p(bufs[i % R].ptr), nbytes, wgpc, unroll,
+                                               C.c_void_p(sink.ptr)))
+
+        call(0)
+        dev.synchronize()
+        g = hip.capture(stream, lambda: [call(i) for i in range(R)])
+        hip.graph_launch(g, stream)
+        hip.stream_sync(stream)
+        reps = max(2, reps_target // R)
+        hip.event_record(e0, stream)
+        for _ in range(reps):
+            hip.graph_launch(g, stream)
+        hip.event_record(e1, stream)
+        hip.event_sync(e1)
+        us = hip.elapsed_ms(e0, e1) * 1e3 / (reps * R)
+        hip.graph_destroy(g)
+        res[f"wg_per_cu{wgpc}_unroll{unroll}"] = {"us": round(us, 3), "GB_s": round(nbytes / us / 1e3, 1)}
+    dev.close()
+    best = min(res, key=lambda c: res[c]["us"])
+    return {"bytes": nbytes, "best_shape": best, "us": res[best]["us"], "GB_s": res[best]["GB_s"],
+            "hbm_frac": round(res[best]["GB_s"] / HBM_PEAK_GBS, 4), "shapes": res, "launches_per_shape": reps * R}
+
+
 DECODE_PROMPT = 512
 DECODE_NEW = 256
 
@@ -509,8 +562,13 @@ def decode_breakdown_leg(new_tokens: int = 128, prompt_len: int = DECODE_PROMPT)
     hip.graph_destroy(g)
     e0, e1 = hip.event_create(), hip.event_create()
 
-    def timed(parts, reps=20):
-        gg = hip.capture(stream, lambda: dec.enqueue_step(parts))
+    pos0 = dec.pos.numpy().copy()
+
+    def timed(parts, reps=20, inner=1):
+        # `inner` copies of the class per graph, so that a one-launch class is
+        # not timed by the host's graph submissions; the position is put back
+        # after each class (the argmax advances it)
+        gg = hip.capture(stream, lambda: [dec.enqueue_step(parts) for _ in range(inner)])
         hip.graph_launch(gg, stream)
         hip.stream_sync(stream)
         hip.event_record(e0, stream)
@@ -519,12 +577,13 @@ def decode_breakdown_leg(new_tokens: int = 128, prompt_len: int = DECODE_PROMPT)
         hip.event_record(e1, stream)
         hip.event_sync(e1)
         hip.graph_destroy(gg)
-        return hip.elapsed_ms(e0, e1) * 1e3 / reps
+        dec.pos.copy_from(pos0)
+        return hip.elapsed_ms(e0, e1) * 1e3 / (reps * inner)
 
     per_layer = {"qkv": 32, "attention": 32, "gate_up": 32, "down": 32, "logits": 1, "argmax": 1}
     res = {"position": prompt_len - 1 + new_tokens, "max_ctx": cfg.max_ctx, "parts": {}}
     for part in dec.STEP_PARTS:
-        us = timed({part})
+        us = timed({part}, inner=16 if per_layer[part] == 1 else 1)
         res["parts"][part] = {"us_per_token": round(us, 2), "launches": per_layer[part],
                               "us_per_launch": round(us / per_layer[part], 2)}
     full = timed(None)
@@ -670,6 +729,9 @@ def main() -> int:
                     help="time each kernel class of the config-4 decode step (HIP events) and print its JSON line")
     ap.add_argument("--probe", default=None, metavar="K,N,DTYPE,M",
                     help="time one QMatMul configuration alone (profiling runs) and print its JSON line")
+    ap.add_argument("--probe-read", default=None, metavar="BYTES[,WG_PER_CU,UNROLL]",
+                    help="time the streaming-read probe over BYTES (every launch shape, or the one given) "
+                         "and print its JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported "
@@ -682,6 +744,12 @@ def main() -> int:
     if args.probe:
         k, n, dt, m = (int(v) for v in args.probe.split(","))
         print(json.dumps(probe_leg(k, n, dt, m)), flush=True)
+        return 0
+    if args.probe_read:
+        if args.copy_bytes:
+            copy_calibration(args.copy_bytes)
+        v = [int(t) for t in args.probe_read.split(",")]
+        print(json.dumps(read_ceiling_leg(v[0], [tuple(v[1:3])] if len(v) == 3 else None)), flush=True)
         return 0
     global SHAPES
     if args.shape:
@@ -748,6 +816,11 @@ def main() -> int:
             "traffic": traffic,
         },
     }
+    # the read ceiling of a launch that size (pure streaming read, best launch shape)
+    rc = read_ceiling_leg(dom_bytes - dom_bytes % 16)
+    out["roofline"]["read_ceiling"] = {k: rc[k] for k in ("bytes", "best_shape", "us", "GB_s", "hbm_frac")}
+    out["roofline"]["frac_of_read_ceiling"] = round(dom["GB_s"] / rc["GB_s"], 4)
+    say(f"[bench] read ceiling {rc}")
     if batched:
         out["batched"] = batched
     if not args.no_moe:

@@ -17,7 +17,11 @@ mix, MFMA busy and int8 MOPS, LDS conflicts, waits, HBM bytes) over one QMatMul
 configuration (`bench.py --probe K,N,DTYPE,M`) and summarises the kernel whose
 name contains --kernel.
 
-Usage: python bench_profile.py [--shape 4096x32000] [--leg matvec|counters|decode|batched|moe]
+With --leg read it runs a kernel trace and FETCH_SIZE / WRITE_SIZE passes over
+the streaming-read probe (bench.py --probe-read), the read ceiling of one
+launch of the mat-vec's size.
+
+Usage: python bench_profile.py [--shape 4096x32000] [--leg matvec|counters|decode|batched|moe|read]
                                [--probe K,N,DTYPE,M --kernel NAME] [--out DIR]
 """
 from __future__ import annotations
@@ -206,7 +210,9 @@ def breakdown_leg(out: str, summarize_only: bool) -> int:
         f.write("# Config 4: decode step of the 7B-shaped Q4_K_M decoder, per kernel class\n\n")
         f.write(f"Made by `python3 bench_profile.py --leg decode_breakdown` (repository root, one MI355X), which runs "
                 f"`{' '.join(cmd)}`: HIP events around graph replays of each class of the step's launches over all "
-                f"32 layers, at position {res['position']} (max_ctx {res['max_ctx']}).\n\n")
+                f"32 layers (a class of one launch per token captured 16 times per graph, so that the host's "
+                f"graph submissions are not what is timed), at position {res['position']} "
+                f"(max_ctx {res['max_ctx']}).\n\n")
         f.write("| class | launches per token | us per token | us per launch |\n|---|---|---|---|\n")
         for part, v in res["parts"].items():
             f.write(f"| {part} | {v['launches']} | {v['us_per_token']} | {v['us_per_launch']} |\n")
@@ -216,10 +222,74 @@ def breakdown_leg(out: str, summarize_only: bool) -> int:
     return 0
 
 
+def read_leg(nbytes: int, shape: str, out: str, summarize_only: bool) -> int:
+    """The HBM read ceiling behind the mat-vec's roofline fraction: a kernel
+    trace and FETCH_SIZE / WRITE_SIZE passes over the streaming-read probe
+    (bench.py --probe-read BYTES,WG_PER_CU,UNROLL), each after device copies of
+    a known size that calibrate the counters."""
+    name = f"read_ceiling_{nbytes}"
+    base = ["python3", "bench.py", "--probe-read", f"{nbytes},{shape}", "--copy-bytes", str(COPY_BYTES)]
+    cmds = {"trace": ["rocprofv3", "--kernel-trace", "--stats", "--output-format", "csv", "-d", f"{out}/{name}/trace",
+                      "-o", "run", "--"] + base,
+            "fetch": ["rocprofv3", "--pmc", "FETCH_SIZE", "--output-format", "csv", "-d", f"{out}/{name}/fetch", "-o",
+                      "run", "--"] + base,
+            "write": ["rocprofv3", "--pmc", "WRITE_SIZE", "--output-format", "csv", "-d", f"{out}/{name}/write", "-o",
+                      "run", "--"] + base}
+    if not summarize_only:
+        for key, c in cmds.items():
+            run(c, f"{out}/{name}_{key}.log", 240 if key == "trace" else 90)
+    live = None
+    for line in open(os.path.join(ROOT, out, f"{name}_trace.log")):
+        if line.startswith("{"):
+            live = json.loads(line)
+    kname = "probe_read_kernel"
+    durs = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+            for r in rows(f"{out}/{name}/trace", "run_kernel_trace.csv") if kname in r["Kernel_Name"]]
+    avg_us = statistics.mean(durs) / 1e3
+
+    def med(d, cname, pred):
+        v = [float(r["Counter_Value"]) for r in rows(f"{out}/{name}/{d}", "run_counter_collection.csv")
+             if r["Counter_Name"].startswith(cname) and pred(r["Kernel_Name"])]
+        return statistics.median(v) if v else float("nan")
+
+    fetch_kib = med("fetch", "FETCH_SIZE", lambda k: kname in k)
+    write_kib = med("write", "WRITE_SIZE", lambda k: kname in k)
+    copy_fetch = med("fetch", "FETCH_SIZE", lambda k: "copyBuffer" in k)   # the calibration copies
+    copy_write = med("write", "WRITE_SIZE", lambda k: "copyBuffer" in k)
+    f_unit = COPY_BYTES / copy_fetch          # bytes per FETCH_SIZE unit, from a copy of known size
+    w_unit = COPY_BYTES / copy_write
+    res = {"bytes": nbytes, "shape": shape, "dispatches": len(durs), "kernel_avg_us": round(avg_us, 3),
+           "GB_s": round(nbytes / avg_us / 1e3, 1), "hbm_peak_frac": round(nbytes / avg_us / 1e3 / 8000.0, 4),
+           "live_us": live and live["us"], "fetch_bytes": round(fetch_kib * f_unit), "write_bytes": round(write_kib * w_unit),
+           "fetch_unit_bytes": round(f_unit, 1), "write_unit_bytes": round(w_unit, 1),
+           "commands": {k: " ".join(v) for k, v in cmds.items()}}
+    json.dump(res, open(os.path.join(ROOT, out, f"{name}.json"), "w"), indent=1)
+    with open(os.path.join(ROOT, out, f"{name}.md"), "w") as f:
+        f.write(f"# HBM read ceiling: one streaming-read launch of {nbytes} bytes\n\n")
+        f.write(f"The bytes of one Q4_K 4096 x 32000 QMatMul (weights + f32 x and y), read by `probe_read_kernel` "
+                f"(16-byte loads, launch shape {shape} = workgroups per CU, loads in flight per thread) over a "
+                f"rotation of >= 1.2 GB of copies.  Made by `python3 bench_profile.py --leg read` (repository "
+                f"root, one MI355X), which runs:\n\n")
+        for k, v in cmds.items():
+            f.write(f"- {k}: `{' '.join(v)}`\n")
+        f.write(f"\nTrace: {len(durs)} dispatches, average {avg_us:.3f} us -> {res['GB_s']} GB/s = "
+                f"{100 * res['hbm_peak_frac']:.1f}% of 8 TB/s (live, HIP events in the same process: "
+                f"{res['live_us']} us).\n\n")
+        f.write(f"Counters (median per dispatch): FETCH_SIZE {fetch_kib:.0f} -> {res['fetch_bytes'] / 1e6:.2f} MB "
+                f"fetched ({res['fetch_bytes'] / nbytes:.3f}x the bytes), WRITE_SIZE {write_kib:.0f} -> "
+                f"{res['write_bytes']} B written; units from the {COPY_BYTES >> 20} MiB copies of the same run: "
+                f"{res['fetch_unit_bytes']} B per FETCH_SIZE unit, {res['write_unit_bytes']} B per WRITE_SIZE "
+                f"unit.\n")
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--shape", default="4096x32000")
-    ap.add_argument("--leg", default="matvec", choices=["matvec", "counters", "decode_breakdown"] + sorted(LEGS))
+    ap.add_argument("--leg", default="matvec", choices=["matvec", "counters", "decode_breakdown", "read"] + sorted(LEGS))
+    ap.add_argument("--read-bytes", type=int, default=73872384, help="bytes per launch for --leg read")
+    ap.add_argument("--read-shape", default="8,1", help="WG_PER_CU,UNROLL for --leg read")
     ap.add_argument("--probe", default="4096,11008,12,512", help="K,N,DTYPE,M for --leg counters")
     ap.add_argument("--kernel", default="mmq", help="kernel-name substring for --leg counters")
     ap.add_argument("--out", default="gpurun_out/profiles")
@@ -232,6 +302,8 @@ def main() -> int:
         return counters_leg(args.probe, args.kernel, out, args.summarize_only)
     if args.leg == "decode_breakdown":
         return breakdown_leg(out, args.summarize_only)
+    if args.leg == "read":
+        return read_leg(args.read_bytes, args.read_shape, out, args.summarize_only)
     if args.leg != "matvec":
         return trace_leg(args.leg, out, args.summarize_only)
     bench = ["python3", "bench.py", "--shape", args.shape, "--steps", "50", "--warmup", "5", "--no-cpu",

@@ -227,7 +227,12 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restric
 }
 
 constexpr int AM_WG = 1024;
+constexpr int AM_PER = 32;  // logits per thread and round: 32768 in flight at once
 
+// One workgroup.  The logits of a round are all requested before any is
+// compared (positions clamped into the vocabulary, the excess keyed out), and
+// before pos is known, so the whole scan is one memory round trip for
+// vocabularies up to AM_WG * AM_PER (a loop of dependent loads was 13.6 us).
 __global__ __launch_bounds__(AM_WG) void argmax_embed_kernel(const float* __restrict__ logits, int vocab,
                                                             const float* __restrict__ table, int dim, int* tokens,
                                                             int tokens_cap, const int* prompt_len_p, int* pos_p,
@@ -236,6 +241,9 @@ __global__ __launch_bounds__(AM_WG) void argmax_embed_kernel(const float* __rest
     __shared__ int s_i[AM_WG / 64];
     __shared__ int s_tok;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float lv[AM_PER];
+#pragma unroll
+    for (int u = 0; u < AM_PER; u++) lv[u] = attn_load_early(logits + min(tid + u * AM_WG, vocab - 1));
     const int pos = *pos_p;
     const int nxt = pos + 1;
     const bool forced = nxt < *prompt_len_p && nxt < tokens_cap;
@@ -245,13 +253,18 @@ __global__ __launch_bounds__(AM_WG) void argmax_embed_kernel(const float* __rest
     } else {
         float bv = -__builtin_inff();
         int bi = 0x7fffffff;
-        for (int i = tid; i < vocab; i += AM_WG) argmax_merge(bv, bi, scan_key(logits[i], i), i);
+        for (int i0 = 0; i0 < vocab; i0 += AM_WG * AM_PER) {
+            if (i0) {
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            const float ov = __shfl_xor(bv, off);
-            const int oi = __shfl_xor(bi, off);
-            argmax_merge(bv, bi, ov, oi);
+                for (int u = 0; u < AM_PER; u++) lv[u] = logits[min(i0 + tid + u * AM_WG, vocab - 1)];
+            }
+#pragma unroll
+            for (int u = 0; u < AM_PER; u++) {
+                const int i = i0 + tid + u * AM_WG;
+                argmax_merge(bv, bi, i < vocab ? scan_key(lv[u], i) : -__builtin_inff(), i < vocab ? i : 0x7fffffff);
+            }
         }
+        wave_argmax(bv, bi);
         if (lane == 0) {
             s_v[wave] = bv;
             s_i[wave] = bi;
