@@ -327,6 +327,37 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
         }
         return;
     }
+    if constexpr (F::BYTES == Q6K_BYTES) {
+        // Q6_K: a wavefront's last row issues no further loads (a wave-uniform
+        // branch; measured 5-8% faster on the 7B shapes, where the re-issued
+        // row's loads otherwise hold the wave's end; Q4_K measured slower so)
+        while (true) {
+            int nrow = row + nw;
+            if (nrow >= N) {
+                if (row < N) {
+                    const float t = qmv_row<F, SPL>(ra, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
+                    if (lane == 63) store(row, acc_out ? resa + t : t);
+                }
+                return;
+            }
+            if (acc_out) resb = yr[nrow];
+            qmv_load_row<F, SPL>(wrow(nrow), gi, c, KB, rb);
+            float t = qmv_row<F, SPL>(ra, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
+            if (lane == 63) store(row, acc_out ? resa + t : t);
+            row = nrow;
+            nrow = row + nw;
+            if (nrow >= N) {
+                t = qmv_row<F, SPL>(rb, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
+                if (lane == 63) store(row, acc_out ? resb + t : t);
+                return;
+            }
+            if (acc_out) resa = yr[nrow];
+            qmv_load_row<F, SPL>(wrow(nrow), gi, c, KB, ra);
+            t = qmv_row<F, SPL>(rb, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
+            if (lane == 63) store(row, acc_out ? resb + t : t);
+            row = nrow;
+        }
+    }
     // Two-row ring: the next row's loads are in flight while a row is reduced.
     // Past the last row a wave re-issues its current row (cache-resident)
     // rather than branching around the loads.
