@@ -254,6 +254,46 @@ int run_qmatmul(frq_device* dev, int t, const uint8_t* w, const float* x, size_t
     return FRQ_OK;
 }
 
+// The batched paths of a fused QMatMul (rows >= 2 formed by a prologue: the
+// RMS norm x gain, the SwiGLU product, or a strided row): the rows are formed
+// and quantized once (launch_quantize_q8k_src), then the int8-MFMA GEMM (from
+// MMQ_MIN_ROWS rows) or the few-row MFMA kernel, the residual added in their
+// epilogue when asked (OUT_ACC).  false: no batched path applies (Q8_0
+// weights, one row, unsupported K) and the caller runs the fused mat-vec.
+struct FusedBatch {
+    bool mmq = false;
+    MmqPlan plan{};
+    size_t abytes = 0;
+};
+
+bool fused_batch_plan(frq_device* dev, int t, const void* w, const ActSrc& src, size_t rows, size_t n, size_t k,
+                      FusedBatch* fb) {
+    if (rows < 2 || vec_dot_type(t) != GGML_Q8K || k > (size_t)0x7fffffff || !quantize_src_supported(src, (int)k))
+        return false;
+    const bool w32 = n * (k / block_elems(t)) * type_size(t) <= 0xffffffffull;
+    if (rows >= MMQ_MIN_ROWS && mmq_supported(t) && w32) {
+        fb->mmq = true;
+        fb->plan = mmq_plan(t, w, (int)rows, (int)n, (int)k, dev->num_cus);
+    } else if (mmq_skinny_supported(t, (int)k)) {
+        fb->mmq = false;
+        fb->plan = MmqPlan{};
+    } else {
+        return false;
+    }
+    fb->abytes = align256(act_bytes(GGML_Q8K, rows, k));
+    return true;
+}
+
+hipError_t launch_fused_batch(frq_device* dev, const FusedBatch& fb, int t, const void* w, const ActView& act,
+                              size_t rows, size_t n, size_t k, float* y, size_t ldy, int out_mode) {
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+    if (fb.mmq) {
+        float* part = fb.plan.part_elems ? reinterpret_cast<float*>(static_cast<uint8_t*>(dev->ws) + fb.abytes) : nullptr;
+        return launch_mmq(fb.plan, t, wb, act, y, part, (int)rows, (int)n, (int)k, (int)ldy, dev->stream, out_mode);
+    }
+    return launch_mmq_skinny(t, wb, act, y, (int)rows, (int)n, (int)k, (int)ldy, dev->num_cus, dev->stream, out_mode);
+}
+
 // matmul_f16 (k_quants.rs:2333-2374): f16 rows x [rows, k] widened exactly to
 // f32, then the same quantize and block dots as run_qmatmul; each f32 output
 // is rounded to f16 (f16::from_f32, nearest even) as it is stored.
@@ -954,7 +994,6 @@ int frq_qmatmul_fused(frq_device* dev, int dt, size_t m, size_t n, size_t k, con
     if (!is_weight_type(dt)) return fail(FRQ_UNSUPPORTED, "qmatmul_fused: dtype %d", dt);
     if (k == 0 || k % block_elems(dt))
         return fail(FRQ_INVALID, "qmatmul_fused: k=%zu must be a positive multiple of %zu", k, block_elems(dt));
-    if (k > qmv_kmax(dt)) return fail(FRQ_UNSUPPORTED, "qmatmul_fused: k=%zu exceeds %zu", k, qmv_kmax(dt));
     if (m > 65535 || n > (size_t)0x7fffffff) return fail(FRQ_UNSUPPORTED, "qmatmul_fused: m=%zu n=%zu", m, n);
     if (m == 0 || n == 0) return FRQ_OK;
     if (!w || !x || !y) return fail(FRQ_INVALID, "qmatmul_fused: null buffer");
@@ -964,6 +1003,17 @@ int frq_qmatmul_fused(frq_device* dev, int dt, size_t m, size_t n, size_t k, con
     if (!aligned16(x) || (x2 && !aligned16(x2)) || (gain && !aligned16(gain)) || ldx % 4)
         return fail(FRQ_MISALIGNED, "qmatmul_fused: x, x2, gain must be 16-byte aligned and ldx %% 4 == 0");
     if (!aligned4(y) || !aligned4(w)) return fail(FRQ_MISALIGNED, "qmatmul_fused: w / y not 4-byte aligned");
+    const ActSrc src{x, (int)ldx, x2, gain, eps};
+    FusedBatch fb;
+    if (fused_batch_plan(dev, dt, w, src, m, n, k, &fb)) {  // several rows: quantize once, one weight pass
+        rc = ensure_ws(dev, fb.abytes + fb.plan.part_elems * sizeof(float));
+        if (rc) return rc;
+        const ActView act = act_view(dev->ws, GGML_Q8K, m, k);
+        HIP_TRY(launch_quantize_q8k_src(src, (int)m, (int)k, act, dev->stream));
+        HIP_TRY(launch_fused_batch(dev, fb, dt, w, act, m, n, k, y, ldy, accumulate ? OUT_ACC : 0));
+        return FRQ_OK;
+    }
+    if (k > qmv_kmax(dt)) return fail(FRQ_UNSUPPORTED, "qmatmul_fused: k=%zu exceeds %zu", k, qmv_kmax(dt));
     QmvOpts o{};
     o.ldx = (int)ldx;
     o.x2 = x2;
@@ -991,6 +1041,19 @@ int frq_qmatmul_fused_pair(frq_device* dev, size_t m, size_t k, const float* x, 
         return fail(FRQ_MISALIGNED, "qmatmul_fused_pair: x and gain must be 16-byte aligned and ldx %% 4 == 0");
     if (!aligned4(w1) || !aligned4(w2) || !aligned4(y1) || !aligned4(y2))
         return fail(FRQ_MISALIGNED, "qmatmul_fused_pair: weights / outputs not 4-byte aligned");
+    const ActSrc src{x, (int)ldx, nullptr, gain, eps};
+    FusedBatch fb1, fb2;
+    if (fused_batch_plan(dev, dt1, w1, src, m, n1, k, &fb1) && fused_batch_plan(dev, dt2, w2, src, m, n2, k, &fb2)) {
+        // several rows: the normalized rows quantized once for both matrices
+        const size_t parts = fb1.plan.part_elems > fb2.plan.part_elems ? fb1.plan.part_elems : fb2.plan.part_elems;
+        rc = ensure_ws(dev, fb1.abytes + parts * sizeof(float));
+        if (rc) return rc;
+        const ActView act = act_view(dev->ws, GGML_Q8K, m, k);
+        HIP_TRY(launch_quantize_q8k_src(src, (int)m, (int)k, act, dev->stream));
+        HIP_TRY(launch_fused_batch(dev, fb1, dt1, w1, act, m, n1, k, y1, n1, 0));
+        HIP_TRY(launch_fused_batch(dev, fb2, dt2, w2, act, m, n2, k, y2, n2, 0));
+        return FRQ_OK;
+    }
     QmvOpts o{};
     o.ldx = (int)ldx;
     o.rms_gain = gain;

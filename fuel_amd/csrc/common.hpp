@@ -51,6 +51,17 @@ __device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
     return (uint16_t)(sign | q);
 }
 
+// Output modes of the matmul epilogues (the `out_mode` kernel argument):
+// OUT_F16 stores f16 outputs (f16::from_f32 of the f32 sum), OUT_ACC adds
+// the sum to the f32 output already in y (the residual add of a layer:
+// y + v, fuel's x + proj order), neither stores the f32 sum.
+constexpr int OUT_F16 = 1, OUT_ACC = 2;
+__device__ __forceinline__ void store_out(float* y, size_t i, float v, int out_mode) {
+    if (out_mode & OUT_F16) reinterpret_cast<uint16_t*>(y)[i] = f32_to_f16_rne(v);
+    else if (out_mode & OUT_ACC) y[i] = y[i] + v;
+    else y[i] = v;
+}
+
 // Rust `f as i8`: saturating, NaN -> 0.
 __device__ __forceinline__ int sat_i8(float v) {
     if (v != v) return 0;

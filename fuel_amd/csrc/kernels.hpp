@@ -13,6 +13,19 @@ hipError_t launch_quantize_q8k(const float* x, int rows, int K, ActView act, uin
                                hipStream_t s);
 // Q8K rows of silu(g) * u with g = x[m][0, K) and u = x[m][K, 2K) (row stride ldx).
 hipError_t launch_quantize_q8k_swiglu(const float* x, int ldx, int rows, int K, ActView act, hipStream_t s);
+// The activation rows of a fused QMatMul, formed before the Q8K quantize: x
+// (row stride ldx); with x2, silu(x) * x2 (x2 rows of the same stride); with
+// gain, rms_norm(x) * gain (eps inside the root; the fused mat-vec prologue's
+// arithmetic).  x2 and gain are exclusive; gain needs K <= 32768.
+struct ActSrc {
+    const float* x;
+    int ldx;
+    const float* x2;
+    const float* gain;
+    float eps;
+};
+bool quantize_src_supported(const ActSrc& src, int K);
+hipError_t launch_quantize_q8k_src(const ActSrc& src, int rows, int K, ActView act, hipStream_t s);
 hipError_t launch_quantize_q8_0(const float* x, int rows, int K, ActView act, uint8_t* aos,
                                 hipStream_t s);
 // Q8K rows of f16 activations (widened exactly to f32 first).
@@ -124,13 +137,14 @@ hipError_t launch_moe_down_combine(int dtype, const uint8_t* w, size_t expert_by
 // row stride ldy.  K must be a multiple of 256.
 bool mmq_skinny_supported(int dtype, int K);
 hipError_t launch_mmq_skinny(int dtype, const uint8_t* w, ActView act, float* y, int M, int N, int K, int ldy,
-                             int num_cus, hipStream_t s, bool y_half = false);
+                             int num_cus, hipStream_t s, int out_mode = 0);
 // mmq.hip: int8-MFMA matmul for M >= 16 over activations already quantized
 // into the workspace (quantize_q8k), y [M, N] with row stride ldy.
 // mmq_plan picks the kernel (tile shape; the LDS-DMA staging only for 16-byte
 // aligned Q4_K blocks) and the K split on the host; part_elems is the number
 // of f32 split-K partial sums launch_mmq needs in `part` (0 without a split).
-// With y_half set, y holds f16 outputs (round to nearest even of the f32 sums).
+// out_mode (common.hpp): OUT_F16 stores f16 outputs (round to nearest even
+// of the f32 sums), OUT_ACC adds the sums to the f32 values already in y.
 bool mmq_supported(int dtype);
 struct MmqPlan {
     int kind;           // kernel instantiation
@@ -140,7 +154,7 @@ struct MmqPlan {
 // max_part_elems caps the partials: the K split is lowered until they fit.
 MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus, size_t max_part_elems = ~(size_t)0);
 hipError_t launch_mmq(const MmqPlan& plan, int dtype, const uint8_t* w, ActView act, float* y, float* part, int M,
-                      int N, int K, int ldy, hipStream_t s, bool y_half = false);
+                      int N, int K, int ldy, hipStream_t s, int out_mode = 0);
 
 // Grouped (MoE) int8-MFMA matmul: workgroup x takes tile x of the tile table
 // (rows [tile_row0, expert end) of one expert, up to bm of them); its weights

@@ -231,7 +231,7 @@ __device__ __forceinline__ void mmq_stage(uint8_t* buf, int tid, const MmqRegs<F
 template <class F, int RT, int CT, int WM, int WN, bool GROUPED>
 __global__ __launch_bounds__(64 * WM * WN) void mmq_kernel(const uint8_t* __restrict__ W, ActView act,
                                                            float* __restrict__ y, int M, int N, int K, int ldy,
-                                                           int mt, int nt, int nsplit, int y_half, MmqGroup g) {
+                                                           int mt, int nt, int nsplit, int out_mode, MmqGroup g) {
     using T = MmqTile<F, RT, CT, WM, WN>;
     constexpr int BM = T::BM, BN = T::BN;
     __shared__ __align__(16) uint8_t smem[2 * T::LDS_BUF];
@@ -347,7 +347,7 @@ __global__ __launch_bounds__(64 * WM * WN) void mmq_kernel(const uint8_t* __rest
 
     float* out = nsplit > 1 ? y + (size_t)split * M * N : y;  // split partials: [z][M][N]
     const int ld = nsplit > 1 ? N : ldy;
-    const bool half_out = y_half && nsplit == 1;  // (split partials stay f32; the reduce rounds)
+    const int omode = nsplit == 1 ? out_mode : 0;  // (split partials: plain f32; the reduce applies the mode)
 #pragma unroll
     for (int r = 0; r < RT; r++)
 #pragma unroll
@@ -356,13 +356,7 @@ __global__ __launch_bounds__(64 * WM * WN) void mmq_kernel(const uint8_t* __rest
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int m = m0 + wm * RT * 16 + r * 16 + 4 * kb + i;
-                if (m < mend && n < N) {
-                    if (half_out)
-                        reinterpret_cast<uint16_t*>(out)[(size_t)m * ld + n] =
-                            f32_to_f16_rne(facc[r][c][i]);
-                    else
-                        out[(size_t)m * ld + n] = facc[r][c][i];
-                }
+                if (m < mend && n < N) store_out(out, (size_t)m * ld + n, facc[r][c][i], omode);
             }
         }
 }
@@ -409,7 +403,7 @@ __device__ __forceinline__ void lds_dma4(const uint8_t* g, uint8_t* l) { __built
 template <class F, int RT, int CT, int WM, int WN, bool GROUPED>
 __global__ __launch_bounds__(64 * WM * WN) void mmq_dma_kernel(const uint8_t* __restrict__ W, ActView act,
                                                                float* __restrict__ y, int M, int N, int K, int ldy,
-                                                               int mt, int nt, int nsplit, int y_half, MmqGroup g) {
+                                                               int mt, int nt, int nsplit, int out_mode, MmqGroup g) {
     using T = DmaTile<F, RT, CT, WM, WN>;
     constexpr int BM = T::BM, BN = T::BN, NW = T::NW;
     __shared__ __align__(16) uint8_t sA0[T::LA], sA1[T::LA], sA2[T::LA];
@@ -551,7 +545,7 @@ __global__ __launch_bounds__(64 * WM * WN) void mmq_dma_kernel(const uint8_t* __
 
     float* out = nsplit > 1 ? y + (size_t)split * M * N : y;  // split partials: [z][M][N]
     const int ld = nsplit > 1 ? N : ldy;
-    const bool half_out = y_half && nsplit == 1;
+    const int omode = nsplit == 1 ? out_mode : 0;
 #pragma unroll
     for (int r = 0; r < RT; r++)
 #pragma unroll
@@ -560,12 +554,7 @@ __global__ __launch_bounds__(64 * WM * WN) void mmq_dma_kernel(const uint8_t* __
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int m = m0 + wm * RT * 16 + r * 16 + 4 * kb + i;
-                if (m < mend && n < N) {
-                    if (half_out)
-                        reinterpret_cast<uint16_t*>(out)[(size_t)m * ld + n] = f32_to_f16_rne(facc[r][c][i]);
-                    else
-                        out[(size_t)m * ld + n] = facc[r][c][i];
-                }
+                if (m < mend && n < N) store_out(out, (size_t)m * ld + n, facc[r][c][i], omode);
             }
         }
 }
@@ -670,7 +659,7 @@ __device__ __forceinline__ int bytes_times_p(uint32_t q, uint32_t f2) {
 template <int RT, int CT, int NW>
 __global__ __launch_bounds__(64 * NW) void mmq_q4k_wide_kernel(const uint8_t* __restrict__ W, ActView act,
                                                                float* __restrict__ y, int M, int N, int K, int ldy,
-                                                               int mt, int nt, int y_half) {
+                                                               int mt, int nt, int out_mode) {
     using T = WideTile<RT, CT, NW>;
     constexpr int BM = T::BM, BN = T::BN;
     __shared__ __align__(16) uint8_t sB0[T::LBUF], sB1[T::LBUF];
@@ -877,10 +866,7 @@ __global__ __launch_bounds__(64 * NW) void mmq_q4k_wide_kernel(const uint8_t* __
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int m = m0 + 16 * r + 4 * kb + i;
-                if (m < M && n < N) {
-                    if (y_half) reinterpret_cast<uint16_t*>(y)[(size_t)m * ldy + n] = f32_to_f16_rne(facc[r][c][i]);
-                    else y[(size_t)m * ldy + n] = facc[r][c][i];
-                }
+                if (m < M && n < N) store_out(y, (size_t)m * ldy + n, facc[r][c][i], out_mode);
             }
         }
 }
@@ -909,7 +895,7 @@ struct WideTile6 {
 template <int RT, int NW>
 __global__ __launch_bounds__(64 * NW) void mmq_q6k_wide_kernel(const uint8_t* __restrict__ W, ActView act,
                                                                float* __restrict__ y, int M, int N, int K, int ldy,
-                                                               int mt, int nt, int y_half) {
+                                                               int mt, int nt, int out_mode) {
     using T = WideTile6<RT, NW>;
     using F = MmqQ6K;
     constexpr int BM = T::BM, BN = T::BN;
@@ -1056,43 +1042,39 @@ __global__ __launch_bounds__(64 * NW) void mmq_q6k_wide_kernel(const uint8_t* __
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int m = m0 + 16 * r + 4 * kb + i;
-            if (m < M && n < N) {
-                if (y_half) reinterpret_cast<uint16_t*>(y)[(size_t)m * ldy + n] = f32_to_f16_rne(facc[r][i]);
-                else y[(size_t)m * ldy + n] = facc[r][i];
-            }
+            if (m < M && n < N) store_out(y, (size_t)m * ldy + n, facc[r][i], out_mode);
         }
 }
 
 template <int RT, int NW>
 hipError_t launch_wide6(const uint8_t* w, ActView act, float* y, int M, int N, int K, int ldy, hipStream_t s,
-                        bool y_half) {
+                        int out_mode) {
     using T = WideTile6<RT, NW>;
     const int mt = (M + T::BM - 1) / T::BM, nt = (N + T::BN - 1) / T::BN;
     hipLaunchKernelGGL((mmq_q6k_wide_kernel<RT, NW>), dim3(mt * nt), dim3(T::NT), 0, s, w, act, y, M, N, K, ldy, mt,
-                       nt, (int)y_half);
+                       nt, out_mode);
     return hipGetLastError();
 }
 
 template <int RT, int CT, int NW>
 hipError_t launch_wide(const uint8_t* w, ActView act, float* y, int M, int N, int K, int ldy, hipStream_t s,
-                       bool y_half) {
+                       int out_mode) {
     using T = WideTile<RT, CT, NW>;
     const int mt = (M + T::BM - 1) / T::BM, nt = (N + T::BN - 1) / T::BN;
     hipLaunchKernelGGL((mmq_q4k_wide_kernel<RT, CT, NW>), dim3(mt * nt), dim3(T::NT), 0, s, w, act, y, M, N, K, ldy,
-                       mt, nt, (int)y_half);
+                       mt, nt, out_mode);
     return hipGetLastError();
 }
 
 // y[m][n] = sum over splits z (in order) of part[z][m][n]
 __global__ void mmq_reduce_kernel(const float* __restrict__ part, float* __restrict__ y, int M, int N, int ldy,
-                                  int nsplit, int y_half) {
+                                  int nsplit, int out_mode) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (size_t)M * N) return;
     float s = part[i];
     for (int z = 1; z < nsplit; z++) s += part[(size_t)z * M * N + i];
     const size_t o = (i / N) * ldy + i % N;
-    if (y_half) reinterpret_cast<uint16_t*>(y)[o] = f32_to_f16_rne(s);
-    else y[o] = s;
+    store_out(y, o, s, out_mode);
 }
 
 // Resident workgroups per CU of a kernel instantiation (cached per instantiation).
@@ -1133,7 +1115,7 @@ void plan_cfg(int M, int N, int K, int num_cus, MmqPlan& p) {
 
 template <class F, int RT, int CT, int WM, int WN, bool DMA>
 hipError_t launch_cfg(const MmqPlan& p, const uint8_t* w, ActView act, float* y, float* part, int M, int N, int K,
-                      int ldy, hipStream_t s, bool y_half) {
+                      int ldy, hipStream_t s, int out_mode) {
     constexpr int NT = 64 * WM * WN, BM = 16 * RT * WM, BN = 16 * CT * WN;
     const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
     const int ks = p.ks;
@@ -1141,14 +1123,14 @@ hipError_t launch_cfg(const MmqPlan& p, const uint8_t* w, ActView act, float* y,
     float* out = ks > 1 ? part : y;
     if constexpr (DMA)
         hipLaunchKernelGGL((mmq_dma_kernel<F, RT, CT, WM, WN, false>), dim3(mt * nt * ks), dim3(NT), 0, s, w, act, out,
-                           M, N, K, ldy, mt, nt, ks, (int)y_half, MmqGroup{});
+                           M, N, K, ldy, mt, nt, ks, out_mode, MmqGroup{});
     else
         hipLaunchKernelGGL((mmq_kernel<F, RT, CT, WM, WN, false>), dim3(mt * nt * ks), dim3(NT), 0, s, w, act, out, M,
-                           N, K, ldy, mt, nt, ks, (int)y_half, MmqGroup{});
+                           N, K, ldy, mt, nt, ks, out_mode, MmqGroup{});
     if (ks > 1) {
         const size_t total = (size_t)M * N;
         hipLaunchKernelGGL(mmq_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, y, M, N,
-                           ldy, ks, (int)y_half);
+                           ldy, ks, out_mode);
     }
     return hipGetLastError();
 }
@@ -1227,15 +1209,15 @@ MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus, siz
 }
 
 hipError_t launch_mmq(const MmqPlan& plan, int dtype, const uint8_t* w, ActView act, float* y, float* part, int M,
-                      int N, int K, int ldy, hipStream_t s, bool y_half) {
+                      int N, int K, int ldy, hipStream_t s, int out_mode) {
     if (!mmq_supported(dtype)) return hipErrorInvalidValue;
     switch (plan.kind) {
 #define FRQ_LAUNCH(kind, F, RT, CT, WM, WN, DMA) \
-    case kind: return launch_cfg<F, RT, CT, WM, WN, DMA>(plan, w, act, y, part, M, N, K, ldy, s, y_half);
+    case kind: return launch_cfg<F, RT, CT, WM, WN, DMA>(plan, w, act, y, part, M, N, K, ldy, s, out_mode);
         FRQ_MMQ_KINDS(FRQ_LAUNCH)
 #undef FRQ_LAUNCH
-        case MMQ_Q4K_WIDE: return launch_wide<4, 1, 8>(w, act, y, M, N, K, ldy, s, y_half);
-        case MMQ_Q6K_WIDE: return launch_wide6<4, 8>(w, act, y, M, N, K, ldy, s, y_half);
+        case MMQ_Q4K_WIDE: return launch_wide<4, 1, 8>(w, act, y, M, N, K, ldy, s, out_mode);
+        case MMQ_Q6K_WIDE: return launch_wide6<4, 8>(w, act, y, M, N, K, ldy, s, out_mode);
         default: return hipErrorInvalidValue;
     }
 }

@@ -66,7 +66,7 @@ __device__ __forceinline__ void sk_load_a(const int8_t* __restrict__ qs, int K, 
 template <class F, int RT, int NWV>
 __global__ __launch_bounds__(64 * NWV) void mmq_skinny_kernel(const uint8_t* __restrict__ W, ActView act,
                                                                     float* __restrict__ y, int M, int N, int K,
-                                                                    int ldy, int y_half) {
+                                                                    int ldy, int out_mode) {
     __shared__ float red[NWV][RT][4][64];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -153,19 +153,16 @@ __global__ __launch_bounds__(64 * NWV) void mmq_skinny_kernel(const uint8_t* __r
 #pragma unroll
         for (int w = 0; w < NWV; w++) s += red[w][rt][i][l];
         const int m = m0 + 16 * rt + 4 * (l >> 4) + i, nn = n0 + (l & 15);
-        if (m < M && nn < N) {
-            if (y_half) reinterpret_cast<uint16_t*>(y)[(size_t)m * ldy + nn] = f32_to_f16_rne(s);
-            else y[(size_t)m * ldy + nn] = s;
-        }
+        if (m < M && nn < N) store_out(y, (size_t)m * ldy + nn, s, out_mode);
     }
 }
 
 template <class F, int RT, int NWV>
 hipError_t launch_sk(const uint8_t* w, ActView act, float* y, int M, int N, int K, int ldy, hipStream_t s,
-                     bool yh) {
+                     int yh) {
     const dim3 grid((N + SK_COLS - 1) / SK_COLS, (M + 16 * RT - 1) / (16 * RT));
     hipLaunchKernelGGL((mmq_skinny_kernel<F, RT, NWV>), grid, dim3(64 * NWV), 0, s, w, act, y, M, N, K, ldy,
-                       (int)yh);
+                       yh);
     return hipGetLastError();
 }
 
@@ -180,7 +177,7 @@ int sk_split(int tiles, int KU, int num_cus) {
 
 template <class F, int RT>
 hipError_t launch_sk_rt(const uint8_t* w, ActView act, float* y, int M, int N, int K, int ldy, int num_cus,
-                        hipStream_t s, bool yh) {
+                        hipStream_t s, int yh) {
     const int tiles = (N + SK_COLS - 1) / SK_COLS * ((M + 16 * RT - 1) / (16 * RT));
     // (two row tiles: at most 8 wavefronts, 512 threads, for their registers)
     const int nwv = sk_split(tiles, K / SK_UNIT, num_cus);
@@ -194,7 +191,7 @@ hipError_t launch_sk_rt(const uint8_t* w, ActView act, float* y, int M, int N, i
 
 template <class F>
 hipError_t launch_sk_fmt(const uint8_t* w, ActView act, float* y, int M, int N, int K, int ldy, int num_cus,
-                         hipStream_t s, bool yh) {
+                         hipStream_t s, int yh) {
     return M <= 16 ? launch_sk_rt<F, 1>(w, act, y, M, N, K, ldy, num_cus, s, yh)
                    : launch_sk_rt<F, 2>(w, act, y, M, N, K, ldy, num_cus, s, yh);
 }
@@ -206,12 +203,12 @@ bool mmq_skinny_supported(int dtype, int K) {
 }
 
 hipError_t launch_mmq_skinny(int dtype, const uint8_t* w, ActView act, float* y, int M, int N, int K, int ldy,
-                             int num_cus, hipStream_t s, bool y_half) {
+                             int num_cus, hipStream_t s, int out_mode) {
     if (!mmq_skinny_supported(dtype, K) || M < 1 || N < 1) return hipErrorInvalidValue;
     switch (dtype) {
-        case GGML_Q4K: return launch_sk_fmt<SkQ4K>(w, act, y, M, N, K, ldy, num_cus, s, y_half);
-        case GGML_Q6K: return launch_sk_fmt<SkQ6K>(w, act, y, M, N, K, ldy, num_cus, s, y_half);
-        default: return launch_sk_fmt<SkQ80>(w, act, y, M, N, K, ldy, num_cus, s, y_half);
+        case GGML_Q4K: return launch_sk_fmt<SkQ4K>(w, act, y, M, N, K, ldy, num_cus, s, out_mode);
+        case GGML_Q6K: return launch_sk_fmt<SkQ6K>(w, act, y, M, N, K, ldy, num_cus, s, out_mode);
+        default: return launch_sk_fmt<SkQ80>(w, act, y, M, N, K, ldy, num_cus, s, out_mode);
     }
 }
 

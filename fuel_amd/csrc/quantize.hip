@@ -8,11 +8,11 @@ namespace frq {
 
 // One wavefront per 256-element superblock; grid = (K/256, rows).  Writes the
 // SoA workspace and, if aos != nullptr, fuel's BlockQ8K bytes.
-__global__ __launch_bounds__(64) void quantize_q8k_kernel(const float* __restrict__ x, int K,
+__global__ __launch_bounds__(64) void quantize_q8k_kernel(const float* __restrict__ x, int ldx, int K,
                                                           ActView act, uint8_t* __restrict__ aos) {
     const int b = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
     const int KB = K / QK_K;
-    const Q8KWave r = q8k_quantize_wave(x + (size_t)m * K + (size_t)b * QK_K, lane);
+    const Q8KWave r = q8k_quantize_wave(x + (size_t)m * ldx + (size_t)b * QK_K, lane);
     reinterpret_cast<uint32_t*>(act.qs + (size_t)m * K + (size_t)b * QK_K)[lane] = r.packed;
     if ((lane & 3) == 0) {
         act.bsums[((size_t)m * KB + b) * 16 + (lane >> 2)] = (int16_t)r.bsum;
@@ -44,15 +44,16 @@ __global__ __launch_bounds__(64) void quantize_q8k_h_kernel(const uint16_t* __re
     if (lane == 0) act.d[(size_t)m * KB + b] = r.d;
 }
 
-// SwiGLU input of the down projection: rows of silu(g) * u, g and u side by
-// side in one row of stride ldx; grid = (K/256, rows).
-__global__ __launch_bounds__(64) void quantize_q8k_swiglu_kernel(const float* __restrict__ x, int ldx, int K,
+// SwiGLU input of the down projection: rows of silu(g) * u, g rows in x and
+// u rows in x2 (both of row stride ldx); grid = (K/256, rows).
+__global__ __launch_bounds__(64) void quantize_q8k_swiglu_kernel(const float* __restrict__ x,
+                                                                 const float* __restrict__ x2, int ldx, int K,
                                                                  ActView act) {
     const int b = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
     const int KB = K / QK_K;
-    const float* g = x + (size_t)m * ldx + (size_t)b * QK_K;
-    const float4 gv = reinterpret_cast<const float4*>(g)[lane];
-    const float4 uv = reinterpret_cast<const float4*>(g + K)[lane];
+    const size_t o = (size_t)m * ldx + (size_t)b * QK_K;
+    const float4 gv = reinterpret_cast<const float4*>(x + o)[lane];
+    const float4 uv = reinterpret_cast<const float4*>(x2 + o)[lane];
     const float4 h = make_float4(silu_mul(gv.x, uv.x), silu_mul(gv.y, uv.y), silu_mul(gv.z, uv.z),
                                  silu_mul(gv.w, uv.w));
     const Q8KWave r = q8k_quantize_vals(h, lane);
@@ -62,6 +63,44 @@ __global__ __launch_bounds__(64) void quantize_q8k_swiglu_kernel(const float* __
         if (act.bsh) act.bsh[((size_t)m * KB + b) * 16 + (lane >> 2)] = f32_to_f16_rne((float)r.bsum);
     }
     if (lane == 0) act.d[(size_t)m * KB + b] = r.d;
+}
+
+// Rows of rms_norm(x) * gain quantized to Q8K: one workgroup of QR_NW
+// wavefronts per row, the row held in registers (wavefront w owns chunks w,
+// w + QR_NW, ...); the norm is the fused mat-vec prologue's arithmetic
+// (q8.hpp act_row_rms_norm: per-lane sums of squares, DPP wave sums, the
+// wavefronts' sums added in order).  grid = rows.
+constexpr int QR_NW = 16;
+
+template <int MAXQ>
+__global__ __launch_bounds__(64 * QR_NW) void quantize_q8k_rms_kernel(const float* __restrict__ x, int ldx,
+                                                                      const float* __restrict__ gain, float eps,
+                                                                      int K, ActView act) {
+    __shared__ float s_red[QR_NW];
+    const int m = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int KB = K / QK_K;
+    ActRowPre<MAXQ> pre;
+    act_row_load<GGML_Q8K, QR_NW, MAXQ>(x + (size_t)m * ldx, K, w, lane, pre);
+    act_row_rms_norm<GGML_Q8K, QR_NW, MAXQ>(pre, gain, eps, K, w, lane, [&](float v) {
+        if (lane == 63) s_red[w] = v;
+        __syncthreads();
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < QR_NW; i++) t += s_red[i];
+        return t;
+    });
+#pragma unroll
+    for (int i = 0; i < MAXQ; i++) {
+        const int b = w + QR_NW * i;
+        if (b >= KB) break;
+        const Q8KWave r = q8k_quantize_vals(pre.v[i], lane);
+        reinterpret_cast<uint32_t*>(act.qs + (size_t)m * K + (size_t)b * QK_K)[lane] = r.packed;
+        if ((lane & 3) == 0) {
+            act.bsums[((size_t)m * KB + b) * 16 + (lane >> 2)] = (int16_t)r.bsum;
+            if (act.bsh) act.bsh[((size_t)m * KB + b) * 16 + (lane >> 2)] = f32_to_f16_rne((float)r.bsum);
+        }
+        if (lane == 0) act.d[(size_t)m * KB + b] = r.d;
+    }
 }
 
 // Eight 32-element blocks per wavefront; grid = (ceil(K/256), rows).
@@ -112,7 +151,7 @@ hipError_t launch_quantize_q8_0_h(const uint16_t* x, int rows, int K, ActView ac
 hipError_t launch_quantize_q8k(const float* x, int rows, int K, ActView act, uint8_t* aos,
                                hipStream_t s) {
     dim3 grid(K / QK_K, rows);
-    hipLaunchKernelGGL(quantize_q8k_kernel, grid, dim3(64), 0, s, x, K, act, aos);
+    hipLaunchKernelGGL(quantize_q8k_kernel, grid, dim3(64), 0, s, x, K, K, act, aos);
     return hipGetLastError();
 }
 
@@ -124,7 +163,36 @@ hipError_t launch_quantize_q8k_h(const uint16_t* x, int rows, int K, ActView act
 
 hipError_t launch_quantize_q8k_swiglu(const float* x, int ldx, int rows, int K, ActView act, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(quantize_q8k_swiglu_kernel, dim3(K / QK_K, rows), dim3(64), 0, s, x, ldx, K, act);
+    hipLaunchKernelGGL(quantize_q8k_swiglu_kernel, dim3(K / QK_K, rows), dim3(64), 0, s, x, x + K, ldx, K, act);
+    return hipGetLastError();
+}
+
+bool quantize_src_supported(const ActSrc& src, int K) {
+    return K % QK_K == 0 && !(src.x2 && src.gain) && (!src.gain || K <= 8 * QR_NW * QK_K);
+}
+
+hipError_t launch_quantize_q8k_src(const ActSrc& src, int rows, int K, ActView act, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    if (!quantize_src_supported(src, K)) return hipErrorInvalidValue;
+    if (src.x2) {
+        hipLaunchKernelGGL(quantize_q8k_swiglu_kernel, dim3(K / QK_K, rows), dim3(64), 0, s, src.x, src.x2, src.ldx,
+                           K, act);
+    } else if (src.gain) {
+        const int maxq = (K / QK_K + QR_NW - 1) / QR_NW;
+#define FRQ_QR(q)                                                                                                 \
+    case q:                                                                                                       \
+        hipLaunchKernelGGL(quantize_q8k_rms_kernel<q>, dim3(rows), dim3(64 * QR_NW), 0, s, src.x, src.ldx, src.gain, \
+                           src.eps, K, act);                                                                      \
+        break;
+        switch (maxq) {
+            FRQ_QR(1) FRQ_QR(2) FRQ_QR(3) FRQ_QR(4) FRQ_QR(5) FRQ_QR(6) FRQ_QR(7) FRQ_QR(8)
+            default: return hipErrorInvalidValue;
+        }
+#undef FRQ_QR
+    } else {
+        hipLaunchKernelGGL(quantize_q8k_kernel, dim3(K / QK_K, rows), dim3(64), 0, s, src.x, src.ldx, K, act,
+                           (uint8_t*)nullptr);
+    }
     return hipGetLastError();
 }
 

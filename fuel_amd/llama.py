@@ -112,11 +112,12 @@ GGUF_NAMES = {"wq": "attn_q", "wk": "attn_k", "wv": "attn_v", "wo": "attn_output
 
 class LlamaDecoder:
     def __init__(self, dev: RocmDevice, cfg: LlamaConfig, seed: int = 1234, std: float = 0.02, _weights=None,
-                 fuse_oproj: bool = True, fuse_glu: bool = True):
+                 fuse_oproj: bool = True, fuse_glu: bool = True, prefill_fused: bool = True):
         if cfg.head_dim != 128 or cfg.n_heads * cfg.head_dim != cfg.dim:
             raise ValueError("this decoder needs head_dim 128 and n_heads * head_dim == dim")
         self.dev, self.cfg, self.seed, self.std = dev, cfg, seed, std
         self.fuse_oproj, self.fuse_glu = fuse_oproj, fuse_glu
+        self.prefill_fused = prefill_fused
         L = lib()
         self.L = L
         d, f, H, HD, Cx = cfg.dim, cfg.ffn, cfg.n_heads, cfg.head_dim, cfg.max_ctx
@@ -419,16 +420,32 @@ class LlamaDecoder:
         x, xn, qk, v, att, o, gu, hh = (B[k].ptr for k in ("x", "xn", "qk", "v", "att", "o", "gu", "h"))
         check(L.frq_gather_rows(h, vp(self.embed.ptr), cfg.vocab, d, vp(self.tokens.ptr), M, vp(x)))
         for li, lw in enumerate(self.layers):
-            check(L.frq_rms_norm_rows(h, M, d, vp(x), d, vp(self.attn_gain[li].ptr), eps, vp(xn), d))
-            self._mm(lw["dt_qk"], lw["wqk"], 2 * d, d, xn, qk, M)
-            self._mm(lw["dt_v"], lw["wv"], d, d, xn, v, M)
+            ag, fg = vp(self.attn_gain[li].ptr), vp(self.ffn_gain[li].ptr)
+            # (the batched fused QMatMuls take Q4_K / Q6_K weights; others run the separate row kernels)
+            fused = self.prefill_fused and M >= 2 and all(lw[t] in (Q4K, Q6K) for t in
+                                                          ("dt_qk", "dt_v", "dt_o", "dt_gu", "dt_down"))
+            if fused and self._pair(lw):  # RMS norm inside the quantize, once for q|k and v
+                check(L.frq_qmatmul_fused_pair(h, M, d, vp(x), d, ag, eps, lw["dt_qk"], 2 * d, vp(lw["wqk"].ptr),
+                                               vp(qk), lw["dt_v"], d, vp(lw["wv"].ptr), vp(v)))
+            else:
+                check(L.frq_rms_norm_rows(h, M, d, vp(x), d, ag, eps, vp(xn), d))
+                self._mm(lw["dt_qk"], lw["wqk"], 2 * d, d, xn, qk, M)
+                self._mm(lw["dt_v"], lw["wv"], d, d, xn, v, M)
             check(L.frq_rope_append_rows(h, M, H, HD, Cx, vp(qk), 2 * d, vp(v), d, vp(self.rcos.ptr),
                                          vp(self.rsin.ptr), 0, vp(self.kc[li].ptr), vp(self.vc[li].ptr)))
             check(L.frq_attention_prefill(h, M, H, HD, Cx, vp(qk), 2 * d, vp(self.kc[li].ptr), vp(self.vc[li].ptr),
                                           0, self.scale, vp(att), d))
+            if fused:  # residual adds in the matmul epilogues, SwiGLU inside the down projection's quantize
+                check(L.frq_qmatmul_fused(h, lw["dt_o"], M, d, d, vp(lw["wo"].ptr), vp(att), d, None, None, 0.0, 1,
+                                          vp(x), d))
+                check(L.frq_qmatmul_fused(h, lw["dt_gu"], M, 2 * f, d, vp(lw["wgu"].ptr), vp(x), d, None, fg, eps, 0,
+                                          vp(gu), 2 * f))
+                check(L.frq_qmatmul_fused(h, lw["dt_down"], M, d, f, vp(lw["wd"].ptr), vp(gu), 2 * f,
+                                          vp(gu + 4 * f), None, 0.0, 1, vp(x), d))
+                continue
             self._mm(lw["dt_o"], lw["wo"], d, d, att, o, M)
             check(L.frq_add(h, M * d, vp(o), vp(x)))
-            check(L.frq_rms_norm_rows(h, M, d, vp(x), d, vp(self.ffn_gain[li].ptr), eps, vp(xn), d))
+            check(L.frq_rms_norm_rows(h, M, d, vp(x), d, fg, eps, vp(xn), d))
             self._mm(lw["dt_gu"], lw["wgu"], 2 * f, d, xn, gu, M)
             check(L.frq_swiglu_rows(h, M, f, vp(gu), 2 * f, vp(hh), f))
             self._mm(lw["dt_down"], lw["wd"], d, f, hh, o, M)

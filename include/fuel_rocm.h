@@ -205,8 +205,13 @@ int frq_moe_ffn(frq_device *dev, int ggml_dtype, size_t t, size_t d, size_t ffn,
  *   y[r, :] = W a(x[r, :])  or, with accumulate, y[r, :] += W a(x[r, :])
  *       (the residual adds, lazy.rs:7426, 7439).
  * Rows r < m of x (and x2) are ldx floats apart, of y ldy apart.  x, x2 and
- * gain must be 16-byte aligned with ldx % 4 == 0.  Asynchronous; allocates
- * nothing, so it may be captured into a HIP graph. */
+ * gain must be 16-byte aligned with ldx % 4 == 0.  Asynchronous.  With one
+ * row (the decode step) it is one mat-vec launch that allocates nothing, so
+ * it may be captured into a HIP graph; with m >= 2 rows of Q4K / Q6K
+ * weights the rows a(x) are formed and quantized once into the device
+ * workspace (grown on demand, as frq_qmatmul's) and the batched int8-MFMA
+ * kernels read every weight block once, the residual added in their
+ * epilogue (the batched prompt pass). */
 int frq_qmatmul_fused(frq_device *dev, int ggml_dtype, size_t m, size_t n, size_t k, const void *w_dev,
                       const float *x_dev, size_t ldx, const float *x2_dev, const float *rms_gain_dev,
                       float rms_eps, int accumulate, float *y_dev, size_t ldy);
@@ -214,7 +219,9 @@ int frq_qmatmul_fused(frq_device *dev, int ggml_dtype, size_t m, size_t n, size_
  * projections of a layer, lazy.rs:7384-7386): y1[r, :] = W1 a(x[r, :]) and
  * y2[r, :] = W2 a(x[r, :]) with a() the plain or RMS-normalized activation of
  * frq_qmatmul_fused; W1 / W2 are Q4K or Q6K (k % 256 == 0, k <= 16384); y1 /
- * y2 rows are n1 / n2 floats.  Asynchronous, capturable. */
+ * y2 rows are n1 / n2 floats.  Asynchronous; with one row capturable (no
+ * allocation), with m >= 2 the rows are normalized and quantized once into
+ * the device workspace for both batched matmuls. */
 int frq_qmatmul_fused_pair(frq_device *dev, size_t m, size_t k, const float *x_dev, size_t ldx,
                            const float *rms_gain_dev, float rms_eps, int dtype1, size_t n1, const void *w1_dev,
                            float *y1_dev, int dtype2, size_t n2, const void *w2_dev, float *y2_dev);

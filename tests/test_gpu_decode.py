@@ -36,12 +36,12 @@ def say(*a):
     print(*a, flush=True)
 
 
-def fused(dev, dt, w, x, n, k, m=1, ldx=None, x2=None, gain=None, eps=1e-5, acc=0, y=None, ldy=None):
+def fused(dev, dt, w, x, n, k, m=1, ldx=None, x2=None, gain=None, eps=1e-5, acc=0, y=None, ldy=None, x_off=0):
     ldx = ldx or k
     ldy = ldy or n
     if y is None:
         y = dev.alloc((m, ldy), np.float32)
-    F._native.check(L().frq_qmatmul_fused(dev.handle, dt, m, n, k, C.c_void_p(w.ptr), C.c_void_p(x.ptr), ldx,
+    F._native.check(L().frq_qmatmul_fused(dev.handle, dt, m, n, k, C.c_void_p(w.ptr), C.c_void_p(x.ptr + 4 * x_off), ldx,
                                           C.c_void_p(x2) if x2 else None, C.c_void_p(gain.ptr) if gain else None,
                                           eps, acc, C.c_void_p(y.ptr), ldy))
     return y
@@ -92,8 +92,12 @@ def test_qmatmul_fused_glu(dev, dt, n, k, m, rms):
                                               C.c_void_p(xd.ptr), k, C.c_void_p(gd.ptr) if rms else None, 1e-5,
                                               C.c_void_p(y.ptr), n))
     got = y.numpy()
-    sg = fused(dev, dt, wgd, xd, n, k, m=m, gain=gd if rms else None).numpy()
-    su = fused(dev, dt, wud, xd, n, k, m=m, gain=gd if rms else None).numpy()
+    # (row by row: the one-row fused launch is the mat-vec the GLU mode extends;
+    # several rows take the batched MFMA path, whose f32 sums differ in order)
+    sg = np.concatenate([fused(dev, dt, wgd, xd, n, k, m=1, gain=gd if rms else None, x_off=r * k).numpy()
+                         for r in range(m)])
+    su = np.concatenate([fused(dev, dt, wud, xd, n, k, m=1, gain=gd if rms else None, x_off=r * k).numpy()
+                         for r in range(m)])
     host = (sg / (np.float32(1) + np.exp(-sg)) * su).astype(np.float32)
     np.testing.assert_allclose(got, host, rtol=2e-6, atol=0)  # (device expf vs numpy exp: an ulp or two)
     xn = O.rms_norm(x, g, 1e-5) if rms else x
@@ -103,8 +107,65 @@ def test_qmatmul_fused_glu(dev, dt, n, k, m, rms):
         assert rel_err(got[r], want[r]) < TOL, r
 
 
+@pytest.mark.parametrize("dt,n,k,m,mode", [
+    (O.Q4K, 8192, 4096, 2, "rms"), (O.Q6K, 4096, 4096, 17, "rms"), (O.Q4K, 8192, 4096, 128, "rms"),
+    (O.Q6K, 1000, 4096, 33, "rms"), (O.Q4K, 22016, 4096, 512, "rms"),
+    (O.Q4K, 4096, 11008, 3, "swiglu"), (O.Q6K, 4096, 11008, 64, "swiglu"), (O.Q4K, 4096, 11008, 512, "swiglu"),
+    (O.Q6K, 4096, 4096, 40, "plain"), (O.Q4K, 4096, 4096, 512, "plain"), (O.Q4K, 700, 2048, 5, "plain")])
+def test_qmatmul_fused_batched(dev, dt, n, k, m, mode):
+    """Several rows through the fused entry point (the batched prompt pass):
+    the rows formed by the prologue (RMS norm x gain, the SwiGLU product of
+    strided g | u rows, or strided plain rows), quantized once, the int8-MFMA
+    kernels with the residual added in their epilogue -- within 1e-3 of the
+    CPU path (quantize, matmul, then the residual add) row by row."""
+    say("fused batched", dt, n, k, m, mode)
+    w = O.quantize(dt, O.normal((n, k), seed=n + k + m, stream=1, std=0.02))
+    wd = dev.from_numpy(w.view(np.uint8))
+    ldx = 2 * k if mode != "rms" else k + 256  # strided rows
+    xs = O.normal((m, ldx), seed=n + k + m, stream=2, std=2.0)
+    xd = dev.from_numpy(xs)
+    y0 = O.normal((m, n), seed=n + k + m, stream=3)
+    if mode == "rms":
+        g = 1 + O.normal((k,), seed=n + k, stream=4, std=0.2)
+        gd = dev.from_numpy(g)
+        got = fused(dev, dt, wd, xd, n, k, m=m, ldx=ldx, gain=gd).numpy()
+        want = O.matmul(dt, O.rms_norm(np.ascontiguousarray(xs[:, :k]), g, 1e-5), w)
+    elif mode == "swiglu":
+        yd = dev.from_numpy(y0)
+        got = fused(dev, dt, wd, xd, n, k, m=m, ldx=ldx, x2=xd.ptr + 4 * k, acc=1, y=yd).numpy()
+        gg, uu = xs[:, :k], xs[:, k:]
+        h = (gg / (np.float32(1) + np.exp(-gg)) * uu).astype(np.float32)
+        want = y0 + O.matmul(dt, h, w)
+    else:
+        yd = dev.from_numpy(y0)
+        got = fused(dev, dt, wd, xd, n, k, m=m, ldx=ldx, acc=1, y=yd).numpy()
+        want = y0 + O.matmul(dt, np.ascontiguousarray(xs[:, :k]), w)
+    for r in range(m):
+        assert rel_err(got[r], want[r]) < TOL, r
+
+
+@pytest.mark.parametrize("dt,n,k,m", [(O.Q4K, 4096, 4096, 512), (O.Q6K, 4096, 4096, 16), (O.Q4K, 1000, 2048, 40)])
+def test_qmatmul_fused_batched_plain_matches_qmatmul(dev, dt, n, k, m):
+    """Contiguous plain rows through the fused entry point run frq_qmatmul's own
+    quantize and kernels: without accumulate the outputs are bit-identical, with
+    it they are the f32 sum y0 + those outputs."""
+    say("fused batched plain", dt, n, k, m)
+    w = O.quantize(dt, O.normal((n, k), seed=n + k, stream=5, std=0.02))
+    x = O.normal((m, k), seed=n + k, stream=6)
+    y0 = O.normal((m, n), seed=n + k, stream=7)
+    wd, xd = dev.from_numpy(w.view(np.uint8)), dev.from_numpy(x)
+    ref = dev.alloc((m, n), np.float32)
+    F.qmatmul_f32_rocm_wrapper([xd, dev.from_numpy(np.frombuffer(w.tobytes(), np.uint32))], [ref],
+                               F.QMatMulParams(dt, 1, m, n, k))
+    ref = ref.numpy()
+    np.testing.assert_array_equal(fused(dev, dt, wd, xd, n, k, m=m).numpy(), ref)
+    yd = dev.from_numpy(y0)
+    np.testing.assert_array_equal(fused(dev, dt, wd, xd, n, k, m=m, acc=1, y=yd).numpy(), (y0 + ref).astype(np.float32))
+
+
 @pytest.mark.parametrize("dt1,n1,dt2,n2,k,m", [(O.Q4K, 8192, O.Q6K, 4096, 4096, 1), (O.Q6K, 300, O.Q4K, 1000, 2048, 2),
-                                               (O.Q4K, 512, O.Q4K, 768, 11008, 1)])
+                                               (O.Q4K, 512, O.Q4K, 768, 11008, 1), (O.Q4K, 8192, O.Q6K, 4096, 4096, 48),
+                                               (O.Q4K, 8192, O.Q6K, 4096, 4096, 512)])
 def test_qmatmul_fused_pair(dev, dt1, n1, dt2, n2, k, m):
     """[q|k] and v from one launch equal the two single fused launches (same
     kernels, same quantized activation) and the CPU path within 1e-3."""
