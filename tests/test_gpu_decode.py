@@ -262,6 +262,35 @@ def test_attention_decode(dev, H, max_ctx, pos):
     np.testing.assert_array_equal(a.run(qk, v, pos), got)
 
 
+def test_attention_decode_sequence(dev):
+    """64 consecutive steps (positions 600..663, 32 heads, fresh q, k, v each
+    step) reusing one workspace: every step's output within 1e-5 of the CPU
+    attention over the cache as it stands, every appended row bit-exact.  A
+    merge that read a split partial left by the previous step (another q)
+    would miss by far more."""
+    H, max_ctx = 32, 768
+    a = Attn(dev, H, max_ctx)
+    rng = np.random.default_rng(5)
+    kc = rng.standard_normal((H, max_ctx, 128)).astype(np.float16)
+    vc = rng.standard_normal((H, max_ctx, 128)).astype(np.float16)
+    a.kc.copy_from(kc.view(np.uint16))
+    a.vc.copy_from(vc.view(np.uint16))
+    scale = float(np.float32(1 / np.sqrt(128.0)))
+    for pos in range(600, 664):
+        qk = O.normal((2 * H * 128,), seed=pos, stream=11, std=2.0)
+        v = O.normal((H * 128,), seed=pos, stream=12)
+        got = a.run(qk, v, pos)
+        q = O.rope(qk[:H * 128].reshape(H, 1, 128), a.cos[pos:pos + 1], a.sin[pos:pos + 1]).reshape(H, 128)
+        k = O.rope(qk[H * 128:].reshape(H, 1, 128), a.cos[pos:pos + 1], a.sin[pos:pos + 1]).reshape(H, 128)
+        kc[:, pos] = k.astype(np.float16)
+        vc[:, pos] = v.reshape(H, 128).astype(np.float16)
+        want = O.attention_decode(q, kc[:, :pos + 1].astype(np.float32), vc[:, :pos + 1].astype(np.float32), pos + 1,
+                                  scale)
+        assert rel_err(got, want) < 1e-5, pos
+    np.testing.assert_array_equal(a.kc.numpy()[:, 600:664], kc[:, 600:664].view(np.uint16))
+    np.testing.assert_array_equal(a.vc.numpy()[:, 600:664], vc[:, 600:664].view(np.uint16))
+
+
 @pytest.mark.parametrize("H,max_ctx,pos,dt,n", [(32, 768, 700, O.Q4K, 4096), (32, 1024, 0, O.Q6K, 4096),
                                                  (32, 768, 768, O.Q4K, 4096), (2, 64, 0, O.Q6K, 300),
                                                  (2, 2048, 1500, O.Q8_0, 512), (4, 1024, 1023, O.Q4K, 1000),
