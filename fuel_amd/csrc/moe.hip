@@ -153,6 +153,123 @@ __global__ __launch_bounds__(BATCH_WG) void moe_batches_kernel(const int* __rest
     }
 }
 
+// The same batches for E <= 256 experts, ranked with ballots instead of
+// bitmaps (measured: 23-29 us -> a few us for 4096 entries).  The entries go in
+// rounds of BATCH_NW * 64 * BATCH_G; wavefront w of a round takes BATCH_G
+// consecutive 64-entry groups.  Within a group, the lanes holding an entry of
+// the same expert are found by eight ballots over the id's bits (the lanes
+// that agree on every bit), so an entry's rank among them is a popcount below
+// its lane; the wavefront's running count per expert (LDS) turns that into a
+// rank within the wavefront's share of the round.  Then, per expert, an
+// exclusive prefix over the wavefronts (plus the earlier rounds' entries)
+// places every entry: (round, wavefront, group, lane) is entry order, so
+// (token, slot) order within an expert is kept, as build_expert_batches does.
+constexpr int BATCH_NW = BATCH_WG / 64;
+constexpr int BATCH_G = 4;
+constexpr int BALLOT_MAX_EXPERTS = 256;
+
+__global__ __launch_bounds__(BATCH_WG) void moe_batches_ballot_kernel(const int* __restrict__ ids, int P, int E,
+                                                                     int topk, int* __restrict__ offsets,
+                                                                     int* __restrict__ sorted_token,
+                                                                     int* __restrict__ sorted_slot,
+                                                                     int* __restrict__ entry_expert,
+                                                                     int* __restrict__ entry_pos, MoeTiles tiles) {
+    __shared__ int off[BALLOT_MAX_EXPERTS];
+    __shared__ int fill[BALLOT_MAX_EXPERTS];
+    __shared__ int wcnt[BATCH_NW][BALLOT_MAX_EXPERTS];
+    __shared__ int wsum[BATCH_NW];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+    // counts -> expert_offsets (and the tile table), as moe_batches_kernel
+    for (int e = tid; e < E; e += BATCH_WG) {
+        off[e] = 0;
+        fill[e] = 0;
+    }
+    __syncthreads();
+    for (int i = tid; i < P; i += BATCH_WG) {
+        const int e = ids[i];
+        if ((unsigned)e < (unsigned)E) atomicAdd(&off[e], 1);
+    }
+    __syncthreads();
+    const int c = tid < E ? off[tid] : 0;
+    const int incl = wave_incl_scan(c, lane);
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int base = 0;
+    for (int w = 0; w < wave; w++) base += wsum[w];
+    const int excl = base + incl - c;
+    if (tid < E) {
+        off[tid] = excl;
+        offsets[tid] = excl;
+    }
+    if (tid == E - 1) offsets[E] = excl + c;
+    if (tiles.bm > 0) {
+        const int nt = (c + tiles.bm - 1) / tiles.bm;
+        const int tincl = wave_incl_scan(nt, lane);
+        __syncthreads();
+        if (lane == 63) wsum[wave] = tincl;
+        __syncthreads();
+        int tbase = 0;
+        for (int w = 0; w < wave; w++) tbase += wsum[w];
+        const int t0 = tbase + tincl - nt;
+        for (int j = 0; j < nt; j++) {
+            tiles.tile_expert[t0 + j] = tid;
+            tiles.tile_row0[t0 + j] = excl + j * tiles.bm;
+        }
+        if (tid == E - 1) tiles.ntiles[0] = t0 + nt;
+    }
+    __syncthreads();
+
+    const unsigned long long below = (1ull << lane) - 1ull;
+    constexpr int ROUND = BATCH_NW * 64 * BATCH_G;
+    for (int r0 = 0; r0 < P; r0 += ROUND) {
+        for (int e = lane; e < E; e += 64) wcnt[wave][e] = 0;  // (this wavefront's row only)
+        const int g0 = r0 + wave * 64 * BATCH_G;
+        int ee[BATCH_G], rk[BATCH_G];
+#pragma unroll
+        for (int g = 0; g < BATCH_G; g++) {
+            const int i = g0 + 64 * g + lane;
+            const int e = i < P ? ids[i] : -1;
+            const bool valid = (unsigned)e < (unsigned)E;
+            unsigned long long m = __ballot(valid);
+#pragma unroll
+            for (int b = 0; b < 8; b++) {
+                const bool bit = (e >> b) & 1;
+                const unsigned long long v = __ballot(bit);
+                m &= bit ? v : ~v;
+            }
+            const int rank = __popcll(m & below);
+            const int before = valid ? wcnt[wave][e] : 0;
+            if (valid && rank == 0) wcnt[wave][e] = before + __popcll(m);
+            ee[g] = valid ? e : -1;
+            rk[g] = before + rank;
+        }
+        __syncthreads();
+        for (int e = tid; e < E; e += BATCH_WG) {  // prefix over the wavefronts, after the earlier rounds
+            int run = fill[e];
+            for (int w = 0; w < BATCH_NW; w++) {
+                const int cw = wcnt[w][e];
+                wcnt[w][e] = run;
+                run += cw;
+            }
+            fill[e] = run;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int g = 0; g < BATCH_G; g++) {
+            const int e = ee[g];
+            if (e < 0) continue;
+            const int i = g0 + 64 * g + lane;
+            const int pos = off[e] + wcnt[wave][e] + rk[g];
+            sorted_token[pos] = i / topk;
+            if (sorted_slot) sorted_slot[pos] = i;
+            entry_expert[pos] = e;
+            entry_pos[i] = pos;
+        }
+        __syncthreads();
+    }
+}
+
 // ---- combine ----
 
 constexpr int COMBINE_WG = 256;
@@ -458,6 +575,11 @@ hipError_t launch_moe_batches(const int* ids, int P, int E, int topk, int* offse
                               int* sorted_slot, int* entry_expert, int* entry_pos, const MoeTiles& tiles,
                               hipStream_t s) {
     if (E <= 0 || E > MOE_MAX_EXPERTS || topk <= 0) return hipErrorInvalidValue;
+    if (E <= BALLOT_MAX_EXPERTS) {
+        hipLaunchKernelGGL(moe_batches_ballot_kernel, dim3(1), dim3(BATCH_WG), 0, s, ids, P, E, topk, offsets,
+                           sorted_token, sorted_slot, entry_expert, entry_pos, tiles);
+        return hipGetLastError();
+    }
     // words per expert per chunk: enough for all P entries when they fit
     const int need = (P + 31) / 32;
     int wpe = BATCH_WORDS / E;
