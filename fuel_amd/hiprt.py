@@ -63,6 +63,11 @@ class HipRuntime:
         self._chk(self.L.hipGraphDestroy(g), "hipGraphDestroy")
         return ge.value
 
+    def graph_upload(self, ge: int, s: int) -> None:
+        """hipGraphUpload: the executable graph's one-time device set-up, done
+        ahead of its first launch (which otherwise pays for it)."""
+        self._chk(self.L.hipGraphUpload(_vp(ge), _vp(s)), "hipGraphUpload")
+
     def graph_launch(self, ge: int, s: int) -> None:
         self._chk(self.L.hipGraphLaunch(_vp(ge), _vp(s)), "hipGraphLaunch")
 
