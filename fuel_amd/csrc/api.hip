@@ -100,8 +100,19 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Activation rows per call: one row takes the fused quantize + mat-vec; up to
 // MMQ_MIN_ROWS - 1 rows the skinny MFMA kernel (one weight pass per 32-row
-// group); from MMQ_MIN_ROWS rows the tiled int8-MFMA GEMM.
+// group); from MMQ_MIN_ROWS rows the tiled int8-MFMA GEMM -- and from
+// MMQ_WIDE_MIN_ROWS rows already when the matrix has at least MMQ_WIDE_N
+// columns: the skinny kernel's 16-column workgroups each read every quantized
+// row, which costs more than the tiles' partly empty rows once there are many
+// columns (4096x32000: M = 16 36.3 -> 31.1 us, M = 32 56.4 -> 33.6 us;
+// 4096x11008 M = 32 28.3 -> 21.3 us; at N = 4096 the skinny kernel stays
+// faster, 12.7 against 15.0 us at M = 32).
 constexpr size_t MMQ_MIN_ROWS = 33;
+constexpr size_t MMQ_WIDE_MIN_ROWS = 16;
+constexpr size_t MMQ_WIDE_N = 8192;
+bool tiled_rows(size_t rows, size_t n) {
+    return rows >= MMQ_MIN_ROWS || (rows >= MMQ_WIDE_MIN_ROWS && n >= MMQ_WIDE_N);
+}
 
 // Byte size of the quantized-activation workspace for rows x k.
 size_t act_bytes(int vt, size_t rows, size_t k) {
@@ -221,7 +232,7 @@ int run_qmatmul(frq_device* dev, int t, const uint8_t* w, const float* x, size_t
         return fail(FRQ_UNSUPPORTED, "qmatmul: k=%zu exceeds %zu for dtype %d", k, kmax, t);
     // the tiled MFMA kernel addresses the weights with 32-bit offsets
     const bool w32 = n * (k / block_elems(t)) * type_size(t) <= 0xffffffffull;
-    if (rows >= MMQ_MIN_ROWS && mmq_supported(t) && w32) {
+    if (tiled_rows(rows, n) && mmq_supported(t) && w32) {
         // many activation rows: quantize them once, then the int8-MFMA GEMM
         // scratch: quantized rows, then the split-K partial sums the plan needs
         // (a fixed scratch region lowers the split until they fit)
@@ -257,7 +268,7 @@ int run_qmatmul(frq_device* dev, int t, const uint8_t* w, const float* x, size_t
 // The batched paths of a fused QMatMul (rows >= 2 formed by a prologue: the
 // RMS norm x gain, the SwiGLU product, or a strided row): the rows are formed
 // and quantized once (launch_quantize_q8k_src), then the int8-MFMA GEMM (from
-// MMQ_MIN_ROWS rows) or the few-row MFMA kernel, the residual added in their
+// tiled_rows) or the few-row MFMA kernel, the residual added in their
 // epilogue when asked (OUT_ACC).  false: no batched path applies (Q8_0
 // weights, one row, unsupported K) and the caller runs the fused mat-vec.
 struct FusedBatch {
@@ -271,7 +282,7 @@ bool fused_batch_plan(frq_device* dev, int t, const void* w, const ActSrc& src, 
     if (rows < 2 || vec_dot_type(t) != GGML_Q8K || k > (size_t)0x7fffffff || !quantize_src_supported(src, (int)k))
         return false;
     const bool w32 = n * (k / block_elems(t)) * type_size(t) <= 0xffffffffull;
-    if (rows >= MMQ_MIN_ROWS && mmq_supported(t) && w32) {
+    if (tiled_rows(rows, n) && mmq_supported(t) && w32) {
         fb->mmq = true;
         fb->plan = mmq_plan(t, w, (int)rows, (int)n, (int)k, dev->num_cus);
     } else if (mmq_skinny_supported(t, (int)k)) {
@@ -309,7 +320,7 @@ int run_qmatmul_f16(frq_device* dev, int t, const uint8_t* w, const uint16_t* x,
     if (k > kmax && !skinny)
         return fail(FRQ_UNSUPPORTED, "qmatmul_f16: k=%zu exceeds %zu for dtype %d", k, kmax, t);
     const bool w32 = n * (k / block_elems(t)) * type_size(t) <= 0xffffffffull;
-    if (rows >= MMQ_MIN_ROWS && mmq_supported(t) && w32) {
+    if (tiled_rows(rows, n) && mmq_supported(t) && w32) {
         const MmqPlan plan = mmq_plan(t, w, (int)rows, (int)n, (int)k, dev->num_cus);
         const size_t abytes = align256(act_bytes(GGML_Q8K, rows, k));
         int rc = ensure_ws(dev, abytes + plan.part_elems * sizeof(float));
