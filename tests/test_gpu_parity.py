@@ -245,7 +245,8 @@ TOL_F16 = TOL + 2.0 ** -11
 
 
 @pytest.mark.parametrize("dt", [O.Q4K, O.Q6K, O.Q8_0])
-@pytest.mark.parametrize("m,n,k", [(1, 300, 4096), (3, 64, 1024), (32, 1024, 4096), (512, 256, 2048)])
+@pytest.mark.parametrize("m,n,k", [(1, 300, 4096), (3, 64, 1024), (32, 1024, 4096), (512, 256, 2048),
+                                   (16, 8200, 1024)])
 def test_qstorage_fwd_f16(dev, dt, m, n, k):
     """matmul_f16 through fwd: f16 rows in, f16 rows out.  Against the oracle's
     matmul_f16 within the f32 tolerance plus the output rounding, and bit-exact
