@@ -829,6 +829,12 @@ def main() -> int:
         say(f"[bench] read ceiling {rc}")
     if batched:
         out["batched"] = batched
+    if not args.shape:  # BASELINE config 1's QMatMul (Q8_0 [1,4096] x [4096,4096]) on the device
+        c1 = probe_leg(4096, 4096, 8, 1)
+        c1_bytes = algo_bytes(4096, 4096, 34, 32)
+        out["config1_q8_0_4096x4096"] = {"us": c1["us"], "GB_s": round(c1_bytes / c1["us"] / 1e3, 1),
+                                         "hbm_frac": round(c1_bytes / c1["us"] / 1e3 / HBM_PEAK_GBS, 4)}
+        say(f"[bench] config 1 {out['config1_q8_0_4096x4096']}")
     if not args.no_moe:
         out["moe"] = moe_leg()
         say(f"[bench] moe {out['moe']}")
