@@ -249,6 +249,13 @@ int run_qmatmul(frq_device* dev, int t, const uint8_t* w, const float* x, size_t
         HIP_TRY(launch_mmq(plan, t, w, act, y, part, (int)rows, (int)n, (int)k, (int)n, dev->stream));
         return FRQ_OK;
     }
+    if (qmv_multi_supported(t, (int)rows, (int)n, (int)k)) {
+        // a few rows of the k-quants: the mat-vec with every workgroup
+        // quantizing them into LDS, each weight row reduced against all of
+        // them (one weight pass per 2 or 4 rows, no quantize launch)
+        HIP_TRY(launch_qmv_multi(t, w, x, y, (int)rows, (int)n, (int)k, (int)n, dev->stream, dev->num_cus));
+        return FRQ_OK;
+    }
     if (skinny && (rows >= 2 || k > kmax)) {
         // a few rows (and Q8_0 at any row count: it has no tiled MFMA
         // kernel): quantize them once, then one weight pass per 32-row group

@@ -76,9 +76,18 @@ struct QmvOpts {
     const float* route_logits;
     int* route_ids;
     float* route_w;
+    // several activation rows per workgroup (plain mode): the rows in all
+    int rows;
 };
 hipError_t launch_qmv_indexed(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
                               const QmvOpts& ix, hipStream_t s, int num_cus);
+// The plain mat-vec for a few rows of the k-quants: every workgroup quantizes
+// MR (2 or 4) rows into LDS and reduces each weight row against all of them
+// while it is in registers (one weight pass per MR rows, no quantize launch).
+constexpr int QMV_MULTI_MAX_ROWS = 4;
+bool qmv_multi_supported(int dtype, int M, int N, int K);
+hipError_t launch_qmv_multi(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
+                            hipStream_t s, int num_cus);
 hipError_t launch_qmv_indexed_route(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K,
                                     int ldy, const QmvOpts& ix, hipStream_t s, int num_cus);
 constexpr int QMV_ROUTE_MAX_EXPERTS = 128;

@@ -120,13 +120,14 @@ __device__ __forceinline__ float block_sum_waves(float v, float* s_red, int w, i
 // RPW > 1 (rows of at most 16/RPW superblocks, SPL == 1): a wavefront step
 // covers RPW consecutive rows, 16/RPW block slots each, instead of one row
 // with most slots past its end; `row` then counts groups of RPW rows.
-template <class F, int SPL, int WG, int MODE, int RPW = 1>
+template <class F, int SPL, int WG, int MODE, int RPW = 1, int MR = 1>
 __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const float* __restrict__ x,
                                          float* __restrict__ y, int N, int K, int ldy, const QmvOpts& ix, int bx,
                                          int gxn, uint8_t* smem, float* s_red, float* s_rt = nullptr,
                                          int* s_pick = nullptr) {
     constexpr int NW = WG / 64;
-    const int m = blockIdx.y;
+    static_assert(MR == 1 || (MODE == QMV_PLAIN && RPW == 1), "several rows per workgroup: the plain mode");
+    const int m = blockIdx.y * MR;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int gi = lane / F::LPB, c = lane % F::LPB;
     const int KB = K / F::ELEMS;
@@ -184,6 +185,7 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
     constexpr int CHUNKS = SPL * (64 / F::LPB) * F::ELEMS / QK_K;
     constexpr int MAXQ = (CHUNKS + NW - 1) / NW;
     ActRowPre<MAXQ> pre;
+    ActRowPre<(MR > 1 ? MAXQ : 1)> pre_more[(MR > 1 ? MR - 1 : 1)];  // (MR > 1: rows m+1 ..)
     AttnRowPre<MODE == QMV_ATTN ? MAXQ : 1> apre;
     int apos = 0;
     if constexpr (MODE == QMV_HALF)
@@ -195,6 +197,13 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
         act_row_load_swiglu<F::ACT, NW, MAXQ>(xr, xr2, K, w, lane, pre);
     else
         act_row_load<F::ACT, NW, MAXQ>(xr, K, w, lane, pre);
+    if constexpr (MR > 1) {  // the workgroup's other rows (clamped into the rows; the extra ones never stored)
+#pragma unroll
+        for (int i = 1; i < MR; i++) {
+            const int mi = m + i < ix.rows ? m + i : ix.rows - 1;
+            act_row_load<F::ACT, NW, MAXQ>(x + (size_t)mi * K, K, w, lane, pre_more[i - 1]);
+        }
+    }
     __builtin_amdgcn_sched_barrier(0);  // the activation loads go out ahead of the weight loads
     if constexpr (MODE == QMV_INDEXED_ROUTE) {
         // wavefront 0 runs the token's routing rounds (a serial chain: copies
@@ -253,7 +262,32 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
                                            [&](float v) { return block_sum_waves<NW>(v, s_red, w, lane); });
     }
     act_row_quantize<F::ACT, NW, MAXQ>(pre, K, s_qs, lay.qstride, s_d, s_bs, w, lane);
+    if constexpr (MR > 1) {
+#pragma unroll
+        for (int i = 1; i < MR; i++) {
+            uint8_t* b = smem + (size_t)i * lay.bytes;
+            act_row_quantize<F::ACT, NW, MAXQ>(pre_more[i - 1], K, reinterpret_cast<int8_t*>(b), lay.qstride,
+                                               reinterpret_cast<float*>(b + lay.off_d),
+                                               reinterpret_cast<int16_t*>(b + lay.off_bs), w, lane);
+        }
+    }
     __syncthreads();
+    // a row's sums against every activation row of the workgroup, stored
+    auto emit = [&](const typename F::Raw(&r)[SPL], int row, float res) __attribute__((always_inline)) {
+        if constexpr (MR == 1) {
+            const float t = qmv_row<F, SPL>(r, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
+            if (lane == 63) store(row, acc_out ? res + t : t);
+        } else {
+#pragma unroll
+            for (int i = 0; i < MR; i++) {
+                const uint8_t* b = smem + (size_t)i * lay.bytes;
+                const float t = qmv_row<F, SPL>(r, reinterpret_cast<const int8_t*>(b), lay.qstride,
+                                                reinterpret_cast<const float*>(b + lay.off_d),
+                                                reinterpret_cast<const int16_t*>(b + lay.off_bs), gi, c, KB);
+                if (lane == 63 && m + i < ix.rows) y[(size_t)(m + i) * ldy + row] = t;
+            }
+        }
+    };
 
     if constexpr (MODE == QMV_GLU && SPL <= 2) {
         // Two output rows in flight: the gate and up rows of the wavefront's
@@ -334,27 +368,21 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
         while (true) {
             int nrow = row + nw;
             if (nrow >= N) {
-                if (row < N) {
-                    const float t = qmv_row<F, SPL>(ra, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
-                    if (lane == 63) store(row, acc_out ? resa + t : t);
-                }
+                if (row < N) emit(ra, row, resa);
                 return;
             }
             if (acc_out) resb = yr[nrow];
             qmv_load_row<F, SPL>(wrow(nrow), gi, c, KB, rb);
-            float t = qmv_row<F, SPL>(ra, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
-            if (lane == 63) store(row, acc_out ? resa + t : t);
+            emit(ra, row, resa);
             row = nrow;
             nrow = row + nw;
             if (nrow >= N) {
-                t = qmv_row<F, SPL>(rb, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
-                if (lane == 63) store(row, acc_out ? resb + t : t);
+                emit(rb, row, resb);
                 return;
             }
             if (acc_out) resa = yr[nrow];
             qmv_load_row<F, SPL>(wrow(nrow), gi, c, KB, ra);
-            t = qmv_row<F, SPL>(rb, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
-            if (lane == 63) store(row, acc_out ? resb + t : t);
+            emit(rb, row, resb);
             row = nrow;
         }
     }
@@ -366,21 +394,19 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
         int lrow = nrow < N ? nrow : row;
         if (acc_out) resb = yr[lrow];
         qmv_load_row<F, SPL>(wrow(lrow), gi, c, KB, rb);
-        float t = qmv_row<F, SPL>(ra, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
-        if (lane == 63) store(row, acc_out ? resa + t : t);
+        emit(ra, row, resa);
         row = nrow;
         if (row >= N) break;
         nrow = row + nw;
         lrow = nrow < N ? nrow : row;
         if (acc_out) resa = yr[lrow];
         qmv_load_row<F, SPL>(wrow(lrow), gi, c, KB, ra);
-        t = qmv_row<F, SPL>(rb, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
-        if (lane == 63) store(row, acc_out ? resb + t : t);
+        emit(rb, row, resb);
         row = nrow;
     }
 }
 
-template <class F, int SPL, int WG, int MODE, int RPW = 1>
+template <class F, int SPL, int WG, int MODE, int RPW = 1, int MR = 1>
 __global__ __launch_bounds__(WG) void qmv_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
                                                  float* __restrict__ y, int N, int K, int ldy, QmvOpts ix) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -390,7 +416,7 @@ __global__ __launch_bounds__(WG) void qmv_kernel(const uint8_t* __restrict__ W, 
         __shared__ int s_pick[QMV_ROUTE_MAX_EXPERTS];
         qmv_body<F, SPL, WG, MODE, RPW>(W, x, y, N, K, ldy, ix, blockIdx.x, gridDim.x, smem, s_red, s_rt, s_pick);
     } else {
-        qmv_body<F, SPL, WG, MODE, RPW>(W, x, y, N, K, ldy, ix, blockIdx.x, gridDim.x, smem, s_red);
+        qmv_body<F, SPL, WG, MODE, RPW, MR>(W, x, y, N, K, ldy, ix, blockIdx.x, gridDim.x, smem, s_red);
     }
 }
 
@@ -410,27 +436,30 @@ __global__ __launch_bounds__(WG) void qmv_pair_kernel(const uint8_t* __restrict_
 
 namespace {
 
-template <class F, int SPL, int WG, int MODE, int RPW = 1>
+template <class F, int SPL, int WG, int MODE, int RPW = 1, int MR = 1>
 hipError_t launch_qmv_wg(const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy, const QmvOpts& ix,
                          hipStream_t s, int num_cus) {
     constexpr int NW = WG / 64;
     static int occ = -1;  // resident workgroups per CU for this instantiation
     if (occ < 0) {
         int o = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, qmv_kernel<F, SPL, WG, MODE, RPW>, WG, 16384) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, qmv_kernel<F, SPL, WG, MODE, RPW, MR>, WG, 16384 * MR) !=
                 hipSuccess ||
             o < 1)
             o = 1;
         occ = o;
     }
-    const size_t lds = (size_t)act_lds_layout(F::ACT, K).bytes;
+    const size_t lds = (size_t)MR * act_lds_layout(F::ACT, K).bytes;
     if (lds > 65536) return hipErrorInvalidValue;
     const int groups = (N + RPW - 1) / RPW;  // (rows, or groups of RPW rows)
     const int need = (groups + NW - 1) / NW;
-    int cap = num_cus * occ / (M > 0 ? M : 1);
+    const int gy = (M + MR - 1) / MR;  // (MR activation rows per workgroup)
+    int cap = num_cus * occ / (gy > 0 ? gy : 1);
     if (cap < 1) cap = 1;
     const int gx = need < cap ? need : cap;
-    hipLaunchKernelGGL((qmv_kernel<F, SPL, WG, MODE, RPW>), dim3(gx, M), dim3(WG), lds, s, w, x, y, N, K, ldy, ix);
+    QmvOpts o = ix;
+    o.rows = M;
+    hipLaunchKernelGGL((qmv_kernel<F, SPL, WG, MODE, RPW, MR>), dim3(gx, gy), dim3(WG), lds, s, w, x, y, N, K, ldy, o);
     return hipGetLastError();
 }
 
@@ -469,6 +498,26 @@ hipError_t launch_fmt(const uint8_t* w, const float* x, float* y, int M, int N, 
         case 8: return launch_qmv<F, 8, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
         default: return hipErrorInvalidValue;  // K beyond 8 slots: rejected by the host check
     }
+}
+
+// Plain mode with MR activation rows per workgroup (each weight row reduced
+// against all of them while it is in registers).
+template <class F, int MR>
+hipError_t launch_multi_fmt(const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy, hipStream_t s,
+                            int num_cus) {
+    constexpr int BPW = 64 / F::LPB;
+    const int spl = (K / F::ELEMS + BPW - 1) / BPW;
+    const QmvOpts o{};
+#define FRQ_MR(S)                                                                                                  \
+    case S: {                                                                                                      \
+        constexpr int WG = qmv_wg_big<F, S>();                                                                     \
+        return launch_qmv_wg<F, S, WG, QMV_PLAIN, 1, MR>(w, x, y, M, N, K, ldy, o, s, num_cus);                     \
+    }
+    switch (spl) {  // (K <= 4096: one slot; qmv_multi_supported)
+        FRQ_MR(1)
+        default: return hipErrorInvalidValue;
+    }
+#undef FRQ_MR
 }
 
 template <int MODE>
@@ -548,6 +597,26 @@ hipError_t launch_qmv_pair(int dt1, const uint8_t* w1, float* y1, int n1, int dt
 hipError_t launch_qmv(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
                       hipStream_t s, int num_cus) {
     return launch_dtype<QMV_PLAIN>(dtype, w, x, y, M, N, K, ldy, QmvOpts{}, s, num_cus);
+}
+
+bool qmv_multi_supported(int dtype, int M, int N, int K) {
+    // measured against the skinny MFMA kernel (Q4_K / Q6_K): two rows win at
+    // K = 4096 (4096x4096 7.5 -> 6.2 us, 4096x32000 25.7 -> 18.2 us), three or
+    // four only on wide matrices (4096x32000 M = 4 27.2 -> 25.4 us, 4096x11008
+    // 17.1 -> 13.1 us; at N = 4096 7.6 against 8.6 us); longer rows (one
+    // register slot no longer holds a lane's blocks) and more rows lose
+    if (!(dtype == GGML_Q4K || dtype == GGML_Q6K) || K % QK_K || K > 16 * QK_K) return false;
+    return M == 2 || (M >= 3 && M <= QMV_MULTI_MAX_ROWS && N >= 8192);
+}
+
+hipError_t launch_qmv_multi(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
+                            hipStream_t s, int num_cus) {
+    if (!qmv_multi_supported(dtype, M, N, K)) return hipErrorInvalidValue;
+    if (dtype == GGML_Q4K)
+        return M <= 2 ? launch_multi_fmt<Q4K, 2>(w, x, y, M, N, K, ldy, s, num_cus)
+                      : launch_multi_fmt<Q4K, 4>(w, x, y, M, N, K, ldy, s, num_cus);
+    return M <= 2 ? launch_multi_fmt<Q6K, 2>(w, x, y, M, N, K, ldy, s, num_cus)
+                  : launch_multi_fmt<Q6K, 4>(w, x, y, M, N, K, ldy, s, num_cus);
 }
 
 hipError_t launch_qmv_indexed(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,

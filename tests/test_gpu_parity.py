@@ -117,14 +117,16 @@ def test_qmatmul_m1_7b_shapes(dev, dt, k, n):
 @pytest.mark.parametrize("dt", [O.Q4K, O.Q6K, O.Q8_0])
 @pytest.mark.parametrize("m,k,n", [(2, 4096, 4096), (3, 4096, 1000), (8, 4096, 4096), (15, 11008, 4096),
                                    (5, 11008, 776), (9, 2048, 300), (16, 256, 40), (24, 4096, 1000),
-                                   (32, 11008, 4096)])
+                                   (32, 11008, 4096), (2, 1024, 333), (3, 4096, 8200), (4, 2048, 9001),
+                                   (2, 4096, 32000)])
 def test_qmatmul_small_batch(dev, dt, m, k, n):
-    """2 <= M <= 32 rows (and Q8_0 at any M) take the skinny int8-MFMA kernel
-    (rows quantized once, each weight block read once per 32-row group, K
-    split over the workgroup's wavefronts): within the tolerance of the
-    oracle, and independent of the other rows of the batch: every row
-    computed beside a single other row (a two-row call; 16-row tiles up to 16
-    rows, two tiles up to 32) gives the same bits."""
+    """2 <= M <= 32 rows: the skinny int8-MFMA kernel (rows quantized once,
+    each weight block read once per 32-row group, K split over the
+    workgroup's wavefronts; Q8_0 at any M) or, for 2 rows of the k-quants
+    with K <= 4096 and 3-4 rows of wide ones, the mat-vec with several rows
+    per workgroup (the 8200- and 9001-column cases): within the tolerance of
+    the oracle, and independent of the other rows of the batch: the same
+    rows in another order give every row the same bits."""
     say("small batch", dt, m, k, n)
     wq = weights(dt, n, k)
     x = acts(m, k, seed=m)
@@ -137,13 +139,17 @@ def test_qmatmul_small_batch(dev, dt, m, k, n):
     err = rel_err(got, want)
     say("  rel_err", err)
     assert err <= TOL
-    if m > 16:
-        return  # (a two-row call takes the one-tile kernel; its split of K differs)
-    two = dev.alloc((2, n), np.float32)
-    for r in range(m):
-        pair = np.ascontiguousarray(x[[r, (r + 1) % m]])
-        F.qmatmul_f32_rocm_wrapper([dev.from_numpy(pair), w], [two], F.QMatMulParams(dt, 1, 2, n, k))
-        assert np.array_equal(two.numpy()[0].view(np.uint32), got[r].view(np.uint32)), r
+    rolled = np.ascontiguousarray(np.roll(x, 1, axis=0))
+    out2 = dev.alloc((m, n), np.float32)
+    F.qmatmul_f32_rocm_wrapper([dev.from_numpy(rolled), w], [out2], F.QMatMulParams(dt, 1, m, n, k))
+    np.testing.assert_array_equal(np.roll(out2.numpy(), -1, axis=0).view(np.uint32), got.view(np.uint32))
+    if m == 2 and dt != O.Q8_0 and k <= 4096:
+        # (two rows of the mat-vec: each row is the one-row call's, bit for bit)
+        one = dev.alloc((1, n), np.float32)
+        for r in range(2):
+            F.qmatmul_f32_rocm_wrapper([dev.from_numpy(np.ascontiguousarray(x[r:r + 1])), w], [one],
+                                       F.QMatMulParams(dt, 1, 1, n, k))
+            np.testing.assert_array_equal(one.numpy()[0].view(np.uint32), got[r].view(np.uint32))
 
 
 @pytest.mark.parametrize("m", [16, 32, 100])
