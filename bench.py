@@ -386,15 +386,17 @@ def probe_leg(k: int, n: int, dtype: int, m: int, reps_target: int = 200) -> dic
 
 READ_WGPC = (1, 2, 4, 8, 16)
 READ_UNROLL = (1, 2, 4, 8)
+READ_NT = (0, 1)  # plain loads, non-temporal (streaming) loads
 
 
 def read_ceiling_leg(nbytes: int, shapes=None, reps_target: int = 200) -> dict:
     """The HBM read ceiling of one launch of `nbytes`: frq_probe_read (a
     kernel that only streams the bytes in, no arithmetic) over a rotation of
     >= 1.2 GB of copies, graph-replayed and HIP-event timed like the mat-vec,
-    for each launch shape (workgroups per CU x loads in flight per thread) in
-    `shapes` (default: every one of READ_WGPC x READ_UNROLL); the best is the
-    ceiling the mat-vec's roofline fraction is read against."""
+    for each launch shape (workgroups per CU x loads in flight per thread x
+    cache policy) in `shapes` (default: every one of READ_WGPC x READ_UNROLL x
+    READ_NT); the best is the ceiling the mat-vec's roofline fraction is read
+    against."""
     import ctypes as C
 
     import fuel_amd as F
@@ -409,12 +411,12 @@ def read_ceiling_leg(nbytes: int, shapes=None, reps_target: int = 200) -> dict:
     bufs = [F.fill_random_bits(dev, nbytes // 4, 0, SEED, 0, 300 + r) for r in range(R)]
     sink = dev.alloc((1,), np.int32)
     dev.synchronize()
-    shapes = shapes or [(w, u) for w in READ_WGPC for u in READ_UNROLL]
+    shapes = shapes or [(w, u, nt) for w in READ_WGPC for u in READ_UNROLL for nt in READ_NT]
     e0, e1 = hip.event_create(), hip.event_create()
     res = {}
-    for wgpc, unroll in shapes:
-        def call(i, wgpc=wgpc, unroll=unroll):
-            F._native.check(lib.frq_probe_read(dev.handle, C.c_void_p(bufs[i % R].ptr), nbytes, wgpc, unroll,
+    for wgpc, unroll, nt in shapes:
+        def call(i, wgpc=wgpc, unroll=unroll, nt=nt):
+            F._native.check(lib.frq_probe_read(dev.handle, C.c_void_p(bufs[i % R].ptr), nbytes, wgpc, unroll, nt,
                                                C.c_void_p(sink.ptr)))
 
         call(0)
@@ -430,7 +432,8 @@ def read_ceiling_leg(nbytes: int, shapes=None, reps_target: int = 200) -> dict:
         hip.event_sync(e1)
         us = hip.elapsed_ms(e0, e1) * 1e3 / (reps * R)
         hip.graph_destroy(g)
-        res[f"wg_per_cu{wgpc}_unroll{unroll}"] = {"us": round(us, 3), "GB_s": round(nbytes / us / 1e3, 1)}
+        res[f"wg_per_cu{wgpc}_unroll{unroll}" + ("_nt" if nt else "")] = {"us": round(us, 3),
+                                                                         "GB_s": round(nbytes / us / 1e3, 1)}
     dev.close()
     best = min(res, key=lambda c: res[c]["us"])
     return {"bytes": nbytes, "best_shape": best, "us": res[best]["us"], "GB_s": res[best]["GB_s"],
@@ -735,7 +738,7 @@ def main() -> int:
                     help="time each kernel class of the config-4 decode step (HIP events) and print its JSON line")
     ap.add_argument("--probe", default=None, metavar="K,N,DTYPE,M",
                     help="time one QMatMul configuration alone (profiling runs) and print its JSON line")
-    ap.add_argument("--probe-read", default=None, metavar="BYTES[,WG_PER_CU,UNROLL]",
+    ap.add_argument("--probe-read", default=None, metavar="BYTES[,WG_PER_CU,UNROLL[,NT]]",
                     help="time the streaming-read probe over BYTES (every launch shape, or the one given) "
                          "and print its JSON line")
     args = ap.parse_args()
@@ -755,7 +758,8 @@ def main() -> int:
         if args.copy_bytes:
             copy_calibration(args.copy_bytes)
         v = [int(t) for t in args.probe_read.split(",")]
-        print(json.dumps(read_ceiling_leg(v[0], [tuple(v[1:3])] if len(v) == 3 else None)), flush=True)
+        shape = [(v[1], v[2], v[3] if len(v) > 3 else 0)] if len(v) >= 3 else None
+        print(json.dumps(read_ceiling_leg(v[0], shape)), flush=True)
         return 0
     global SHAPES
     if args.shape:

@@ -225,7 +225,7 @@ def breakdown_leg(out: str, summarize_only: bool) -> int:
 def read_leg(nbytes: int, shape: str, out: str, summarize_only: bool) -> int:
     """The HBM read ceiling behind the mat-vec's roofline fraction: a kernel
     trace and FETCH_SIZE / WRITE_SIZE passes over the streaming-read probe
-    (bench.py --probe-read BYTES,WG_PER_CU,UNROLL), each after device copies of
+    (bench.py --probe-read BYTES,WG_PER_CU,UNROLL,NT), each after device copies of
     a known size that calibrate the counters."""
     name = f"read_ceiling_{nbytes}"
     base = ["python3", "bench.py", "--probe-read", f"{nbytes},{shape}", "--copy-bytes", str(COPY_BYTES)]
@@ -267,7 +267,8 @@ def read_leg(nbytes: int, shape: str, out: str, summarize_only: bool) -> int:
     with open(os.path.join(ROOT, out, f"{name}.md"), "w") as f:
         f.write(f"# HBM read ceiling: one streaming-read launch of {nbytes} bytes\n\n")
         f.write(f"The bytes of one Q4_K 4096 x 32000 QMatMul (weights + f32 x and y), read by `probe_read_kernel` "
-                f"(16-byte loads, launch shape {shape} = workgroups per CU, loads in flight per thread) over a "
+                f"(16-byte loads, launch shape {shape} = workgroups per CU, loads in flight per thread, non-temporal "
+                f"loads if 1) over a "
                 f"rotation of >= 1.2 GB of copies.  Made by `python3 bench_profile.py --leg read` (repository "
                 f"root, one MI355X), which runs:\n\n")
         for k, v in cmds.items():
@@ -289,7 +290,7 @@ def main() -> int:
     ap.add_argument("--shape", default="4096x32000")
     ap.add_argument("--leg", default="matvec", choices=["matvec", "counters", "decode_breakdown", "read"] + sorted(LEGS))
     ap.add_argument("--read-bytes", type=int, default=73872384, help="bytes per launch for --leg read")
-    ap.add_argument("--read-shape", default="8,1", help="WG_PER_CU,UNROLL for --leg read")
+    ap.add_argument("--read-shape", default="8,1,1", help="WG_PER_CU,UNROLL,NT for --leg read (NT 1: non-temporal loads)")
     ap.add_argument("--probe", default="4096,11008,12,512", help="K,N,DTYPE,M for --leg counters")
     ap.add_argument("--kernel", default="mmq", help="kernel-name substring for --leg counters")
     ap.add_argument("--out", default="gpurun_out/profiles")

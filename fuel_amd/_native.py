@@ -92,7 +92,7 @@ SIGNATURES = {
     "frq_block_isums": (_i32, [_vp, _i32, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
     "frq_fill_random_bits": (_i32, [_vp, _vp, _sz, C.c_uint64, C.c_uint64, C.c_uint32, C.c_uint32]),
     "frq_fill_normal": (_i32, [_vp, _vp, _sz, C.c_uint64, C.c_uint32, C.c_float, C.c_float]),
-    "frq_probe_read": (_i32, [_vp, _vp, _sz, _i32, _i32, _vp]),
+    "frq_probe_read": (_i32, [_vp, _vp, _sz, _i32, _i32, _i32, _vp]),
     "frq_gguf_open": (_i32, [C.c_char_p, _vp]),
     "frq_gguf_close": (_i32, [_vp]),
     "frq_gguf_version": (_i32, [_vp]),

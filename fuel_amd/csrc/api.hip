@@ -1299,14 +1299,15 @@ int frq_fill_normal(frq_device* dev, float* y, size_t n, uint64_t seed, uint32_t
     return FRQ_OK;
 }
 
-int frq_probe_read(frq_device* dev, const void* src, size_t bytes, int wg_per_cu, int unroll, uint32_t* sink) {
+int frq_probe_read(frq_device* dev, const void* src, size_t bytes, int wg_per_cu, int unroll, int nontemporal,
+                   uint32_t* sink) {
     int rc = use_device(dev);
     if (rc) return rc;
     if (!src || !sink) return fail(FRQ_INVALID, "probe_read: null buffer");
     if (!aligned16(src) || bytes % 16 || !bytes) return fail(FRQ_MISALIGNED, "probe_read: 16-byte aligned, whole 16-byte words");
     if (wg_per_cu < 1 || wg_per_cu > 32 || (unroll != 1 && unroll != 2 && unroll != 4 && unroll != 8))
         return fail(FRQ_INVALID, "probe_read: wg_per_cu %d (1..32), unroll %d (1, 2, 4, 8)", wg_per_cu, unroll);
-    HIP_TRY(launch_probe_read(src, bytes, wg_per_cu * dev->num_cus, unroll, sink, dev->stream));
+    HIP_TRY(launch_probe_read(src, bytes, wg_per_cu * dev->num_cus, unroll, nontemporal, sink, dev->stream));
     return FRQ_OK;
 }
 

@@ -205,7 +205,8 @@ hipError_t launch_normal(float* y, size_t n, unsigned long long seed, uint32_t s
 // probe.hip: a read-only streaming kernel over `bytes` (a multiple of 16) with
 // `grid` workgroups of 256 threads and `unroll` (1, 2, 4, 8) loads in flight
 // per thread; the HBM read ceiling of a launch that size.
-hipError_t launch_probe_read(const void* src, size_t bytes, int grid, int unroll, uint32_t* sink, hipStream_t s);
+hipError_t launch_probe_read(const void* src, size_t bytes, int grid, int unroll, int nontemporal, uint32_t* sink,
+                             hipStream_t s);
 
 // decode.hip: attention of one new token per head over an f16 KV cache with
 // RoPE and the cache append fused (head_dim ATTN_HEAD_DIM): a split kernel

@@ -1,9 +1,10 @@
 // Streaming-read probe: the HBM read ceiling that the mat-vec's roofline
 // fraction is read against.  A kernel that only reads (16-byte loads, a
 // grid-stride loop with `U` loads of each thread in flight per step, all of
-// them issued before any is used) moves the bytes a QMatMul of the same size
-// must read, with no arithmetic, no activation row and nothing written but a
-// word that keeps the loads alive.  Measurement helper: nothing in the
+// them issued before any is used; NT: non-temporal loads, the streaming
+// cache policy) moves the bytes a QMatMul of the same size must read, with no
+// arithmetic, no activation row and nothing written but a word that keeps the
+// loads alive.  Measurement helper: nothing in the
 // reference corresponds to it and no product path calls it.
 #include <hip/hip_runtime.h>
 
@@ -15,7 +16,9 @@ namespace {
 
 constexpr int PR_WG = 256;
 
-template <int U>
+typedef unsigned int pr_u4 __attribute__((ext_vector_type(4)));
+
+template <int U, bool NT>
 __global__ __launch_bounds__(PR_WG) void probe_read_kernel(const uint4* __restrict__ src, size_t n16,
                                                            uint32_t* __restrict__ sink) {
     const size_t stride = (size_t)gridDim.x * PR_WG * U;
@@ -25,7 +28,13 @@ __global__ __launch_bounds__(PR_WG) void probe_read_kernel(const uint4* __restri
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const size_t j = i + (size_t)u * PR_WG;
-            v[u] = src[j < n16 ? j : n16 - 1];  // clamped, not predicated: every load goes out at once
+            const uint4* p = src + (j < n16 ? j : n16 - 1);  // clamped, not predicated: every load goes out at once
+            if constexpr (NT) {
+                const pr_u4 t = __builtin_nontemporal_load(reinterpret_cast<const pr_u4*>(p));
+                v[u] = make_uint4(t.x, t.y, t.z, t.w);
+            } else {
+                v[u] = *p;
+            }
         }
 #pragma unroll
         for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
@@ -33,19 +42,26 @@ __global__ __launch_bounds__(PR_WG) void probe_read_kernel(const uint4* __restri
     if (acc == 0x9e3779b9u) sink[0] = acc;  // (keeps the loads; almost never taken)
 }
 
-}  // namespace
-
-hipError_t launch_probe_read(const void* src, size_t bytes, int grid, int unroll, uint32_t* sink, hipStream_t s) {
-    const uint4* p = reinterpret_cast<const uint4*>(src);
-    const size_t n16 = bytes / 16;
+template <bool NT>
+hipError_t launch_probe_nt(const uint4* p, size_t n16, int grid, int unroll, uint32_t* sink, hipStream_t s) {
     switch (unroll) {
-        case 1: hipLaunchKernelGGL(probe_read_kernel<1>, dim3(grid), dim3(PR_WG), 0, s, p, n16, sink); break;
-        case 2: hipLaunchKernelGGL(probe_read_kernel<2>, dim3(grid), dim3(PR_WG), 0, s, p, n16, sink); break;
-        case 4: hipLaunchKernelGGL(probe_read_kernel<4>, dim3(grid), dim3(PR_WG), 0, s, p, n16, sink); break;
-        case 8: hipLaunchKernelGGL(probe_read_kernel<8>, dim3(grid), dim3(PR_WG), 0, s, p, n16, sink); break;
+        case 1: hipLaunchKernelGGL((probe_read_kernel<1, NT>), dim3(grid), dim3(PR_WG), 0, s, p, n16, sink); break;
+        case 2: hipLaunchKernelGGL((probe_read_kernel<2, NT>), dim3(grid), dim3(PR_WG), 0, s, p, n16, sink); break;
+        case 4: hipLaunchKernelGGL((probe_read_kernel<4, NT>), dim3(grid), dim3(PR_WG), 0, s, p, n16, sink); break;
+        case 8: hipLaunchKernelGGL((probe_read_kernel<8, NT>), dim3(grid), dim3(PR_WG), 0, s, p, n16, sink); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_probe_read(const void* src, size_t bytes, int grid, int unroll, int nontemporal, uint32_t* sink,
+                             hipStream_t s) {
+    const uint4* p = reinterpret_cast<const uint4*>(src);
+    const size_t n16 = bytes / 16;
+    return nontemporal ? launch_probe_nt<true>(p, n16, grid, unroll, sink, s)
+                       : launch_probe_nt<false>(p, n16, grid, unroll, sink, s);
 }
 
 }  // namespace frq

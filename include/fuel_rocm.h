@@ -344,11 +344,12 @@ int frq_fill_normal(frq_device *dev, float *y_dev, size_t n, uint64_t seed, uint
 /* ---- measurement helper (no reference counterpart) ----
  * A read-only streaming kernel over `bytes` of device memory (16-byte aligned,
  * a multiple of 16): wg_per_cu * CUs workgroups of 256 threads, `unroll`
- * (1, 2, 4 or 8) 16-byte loads per thread in flight, nothing written but
- * sink[0] in the rare case the loaded words XOR to a fixed constant.  Times
- * the HBM read ceiling of one launch of that size, the bound the mat-vec's
- * roofline fraction is read against. */
-int frq_probe_read(frq_device *dev, const void *src_dev, size_t bytes, int wg_per_cu, int unroll,
+ * (1, 2, 4 or 8) 16-byte loads per thread in flight (non-temporal loads when
+ * `nontemporal` is nonzero), nothing written but sink[0] in the rare case the
+ * loaded words XOR to a fixed constant.  Times the HBM read ceiling of one
+ * launch of that size, the bound the mat-vec's roofline fraction is read
+ * against. */
+int frq_probe_read(frq_device *dev, const void *src_dev, size_t bytes, int wg_per_cu, int unroll, int nontemporal,
                    uint32_t *sink_dev);
 
 /* ---- GGUF files (host-side reader + upload) ----
