@@ -132,10 +132,16 @@ struct SkQ6K {
 };
 
 // Q8_0: a unit is eight 34-byte blocks; lane group c holds bytes 8c..8c+7 of
-// each block's quants (one 8-byte load per block) and the block's f16 d.
+// each block's quants and the block's f16 d.  The unit starts on a 16-byte
+// boundary (rows of K/32 blocks with K a multiple of 256, weights 4-byte
+// aligned), so the pieces of the even blocks start 2 bytes past a dword
+// boundary: those load the dword-aligned 8 bytes below plus the 2 bytes after
+// them and funnel-shift (an 8-byte load 2 bytes off a dword boundary runs far
+// slower than an aligned one).
 struct SkQ80 {
     struct Raw {
         uint2 q[8];
+        uint32_t tail[4];  // even blocks: bytes 6, 7 of the piece
         uint32_t dbits[8];
     };
     static constexpr int BYTES = 8 * Q8_0_BYTES;
@@ -145,7 +151,13 @@ struct SkQ80 {
         const uint8_t* b = row + (size_t)u * BYTES;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            r.q[j] = load8_u(b + j * Q8_0_BYTES + 2 + 8 * c);
+            const uint8_t* p = b + j * Q8_0_BYTES + 2 + 8 * c;
+            if (j & 1) {
+                r.q[j] = *reinterpret_cast<const uint2*>(p);
+            } else {
+                r.q[j] = *reinterpret_cast<const uint2*>(p - 2);
+                r.tail[j >> 1] = load_u16(p + 6);
+            }
             r.dbits[j] = load_u16(b + j * Q8_0_BYTES);
         }
     }
@@ -161,7 +173,12 @@ struct SkQ80 {
         const v4i zero = v4i{0, 0, 0, 0};
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const i64 bq = (i64)(((unsigned long long)r.q[j].y << 32) | r.q[j].x);
+            uint32_t lo = r.q[j].x, hi = r.q[j].y;
+            if (!(j & 1)) {
+                lo = __builtin_amdgcn_alignbyte(r.q[j].y, r.q[j].x, 2);
+                hi = __builtin_amdgcn_alignbyte(r.tail[j >> 1], r.q[j].y, 2);
+            }
+            const i64 bq = (i64)(((unsigned long long)hi << 32) | lo);
             const float dw = f16_to_f32(r.dbits[j]);
 #pragma unroll
             for (int rt = 0; rt < RT; rt++) {
