@@ -513,9 +513,16 @@ hipError_t launch_multi_fmt(const uint8_t* w, const float* x, float* y, int M, i
         constexpr int WG = qmv_wg_big<F, S>();                                                                     \
         return launch_qmv_wg<F, S, WG, QMV_PLAIN, 1, MR>(w, x, y, M, N, K, ldy, o, s, num_cus);                     \
     }
-    switch (spl) {  // (K <= 4096: one slot; qmv_multi_supported)
-        FRQ_MR(1)
-        default: return hipErrorInvalidValue;
+    if constexpr (F::LPB == 2) {  // Q8_0 (K <= 4096: four slots; qmv_multi_supported)
+        switch (spl) {
+            FRQ_MR(4)
+            default: return hipErrorInvalidValue;
+        }
+    } else {
+        switch (spl) {  // (K <= 4096: one slot; qmv_multi_supported)
+            FRQ_MR(1)
+            default: return hipErrorInvalidValue;
+        }
     }
 #undef FRQ_MR
 }
@@ -605,13 +612,18 @@ bool qmv_multi_supported(int dtype, int M, int N, int K) {
     // four only on wide matrices (4096x32000 M = 4 27.2 -> 25.4 us, 4096x11008
     // 17.1 -> 13.1 us; at N = 4096 7.6 against 8.6 us); longer rows (one
     // register slot no longer holds a lane's blocks) and more rows lose
-    if (!(dtype == GGML_Q4K || dtype == GGML_Q6K) || K % QK_K || K > 16 * QK_K) return false;
+    if (!(dtype == GGML_Q4K || dtype == GGML_Q6K || dtype == GGML_Q8_0) || K % QK_K || K > 16 * QK_K) return false;
+    if (dtype == GGML_Q8_0)  // (four slots exactly; 5-8 rows: two row groups, each reading the weights)
+        return K == 16 * QK_K && M >= 2 && (M <= QMV_MULTI_MAX_ROWS || (M <= 2 * QMV_MULTI_MAX_ROWS && N >= 8192));
     return M == 2 || (M >= 3 && M <= QMV_MULTI_MAX_ROWS && N >= 8192);
 }
 
 hipError_t launch_qmv_multi(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
                             hipStream_t s, int num_cus) {
     if (!qmv_multi_supported(dtype, M, N, K)) return hipErrorInvalidValue;
+    if (dtype == GGML_Q8_0)
+        return M <= 2 ? launch_multi_fmt<Q80, 2>(w, x, y, M, N, K, ldy, s, num_cus)
+                      : launch_multi_fmt<Q80, 4>(w, x, y, M, N, K, ldy, s, num_cus);
     if (dtype == GGML_Q4K)
         return M <= 2 ? launch_multi_fmt<Q4K, 2>(w, x, y, M, N, K, ldy, s, num_cus)
                       : launch_multi_fmt<Q4K, 4>(w, x, y, M, N, K, ldy, s, num_cus);

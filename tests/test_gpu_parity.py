@@ -118,15 +118,16 @@ def test_qmatmul_m1_7b_shapes(dev, dt, k, n):
 @pytest.mark.parametrize("m,k,n", [(2, 4096, 4096), (3, 4096, 1000), (8, 4096, 4096), (15, 11008, 4096),
                                    (5, 11008, 776), (9, 2048, 300), (16, 256, 40), (24, 4096, 1000),
                                    (32, 11008, 4096), (2, 1024, 333), (3, 4096, 8200), (4, 2048, 9001),
-                                   (2, 4096, 32000)])
+                                   (2, 4096, 32000), (6, 4096, 8200), (4, 4096, 1000)])
 def test_qmatmul_small_batch(dev, dt, m, k, n):
     """2 <= M <= 32 rows: the skinny int8-MFMA kernel (rows quantized once,
     each weight block read once per 32-row group, K split over the
-    workgroup's wavefronts; Q8_0 at any M) or, for 2 rows of the k-quants
-    with K <= 4096 and 3-4 rows of wide ones, the mat-vec with several rows
-    per workgroup (the 8200- and 9001-column cases): within the tolerance of
-    the oracle, and independent of the other rows of the batch: the same
-    rows in another order give every row the same bits."""
+    workgroup's wavefronts) or the mat-vec with several rows per workgroup —
+    2 rows of the k-quants with K <= 4096 and 3-4 rows of wide ones (the
+    8200- and 9001-column cases); Q8_0 at K = 4096 with 2-4 rows, and 5-8 rows
+    of wide matrices in two row groups: within the tolerance of the oracle,
+    and independent of the other rows of the batch: the same rows in another
+    order give every row the same bits."""
     say("small batch", dt, m, k, n)
     wq = weights(dt, n, k)
     x = acts(m, k, seed=m)
@@ -143,7 +144,7 @@ def test_qmatmul_small_batch(dev, dt, m, k, n):
     out2 = dev.alloc((m, n), np.float32)
     F.qmatmul_f32_rocm_wrapper([dev.from_numpy(rolled), w], [out2], F.QMatMulParams(dt, 1, m, n, k))
     np.testing.assert_array_equal(np.roll(out2.numpy(), -1, axis=0).view(np.uint32), got.view(np.uint32))
-    if m == 2 and dt != O.Q8_0 and k <= 4096:
+    if m == 2 and k <= 4096 and (dt != O.Q8_0 or k == 4096):
         # (two rows of the mat-vec: each row is the one-row call's, bit for bit)
         one = dev.alloc((1, n), np.float32)
         for r in range(2):
@@ -154,8 +155,9 @@ def test_qmatmul_small_batch(dev, dt, m, k, n):
 
 @pytest.mark.parametrize("m", [16, 32, 100])
 def test_qmatmul_q8_0_batched(dev, m):
-    """Q8_0 (no MFMA kernel) at 16 or more rows: the small-batch mat-vec in
-    groups of 8 rows, against the oracle at 4096 x 4096."""
+    """Q8_0 (no tiled MFMA kernel) at 16 or more rows: the skinny int8-MFMA
+    kernel, one weight pass per 32-row group, against the oracle at
+    4096 x 4096."""
     say("q8_0 batched", m)
     k = n = 4096
     wq = weights(O.Q8_0, n, k)
