@@ -79,9 +79,10 @@ __global__ __launch_bounds__(HD) void rope_append_rows_kernel(float* __restrict_
     vc[crow + tid] = __float2half(v[(size_t)m * ldv + (size_t)h * HD + tid]);
 }
 
-// Attention of a query tile on f16 MFMA.  A wavefront owns 16 query rows of
-// one head and walks the cache rows 0 .. its last row's position 16 at a time
-// with a running maximum (flash attention):
+// Attention of a query tile on f16 MFMA.  A workgroup owns 16 query rows of
+// one head; its AF_WAVES wavefronts split the tile's cache rows 0 .. its last
+// row's position into contiguous ranges of 16-row blocks, and each walks its
+// range with a running maximum (flash attention):
 //   S^T (16 keys x 16 queries) = K_blk (16 x 128) . Q^T (128 x 16) on
 //     v_mfma_f32_16x16x32_f16, four 32-dim steps; K rows are f16 already and
 //     each q value is split exactly into f16 hi + lo (hi = f16(q), lo =
@@ -97,11 +98,16 @@ __global__ __launch_bounds__(HD) void rope_append_rows_kernel(float* __restrict_
 // (row = dim, k = key): tile t takes the dims 8 * row + t, so lane l's four
 // 16-byte loads of rows 4g + i (dims 8r .. 8r+7) hold its A values for all
 // eight tiles.  Output: the C layout of tile t leaves lane l dims
-// 8 (4g + i) + t of query r, eight consecutive floats per i.
+// 8 (4g + i) + t of query r, eight consecutive floats per i.  The wavefronts'
+// (max, sum, output) triples are merged through LDS in wavefront order:
+// M = max m_w, out = sum_w e^(m_w - M) o_w / sum_w e^(m_w - M) l_w.  Under a
+// causal mask the tiles of late rows walk many more blocks than early ones;
+// split over four wavefronts the longest chain is a quarter as long and four
+// times as many wavefronts share the chip.
 typedef _Float16 af_h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 af_h4 __attribute__((ext_vector_type(4)));
 typedef float af_f4 __attribute__((ext_vector_type(4)));
-constexpr int AF_WAVES = 4;  // query tiles (16 rows each) per workgroup
+constexpr int AF_WAVES = 4;  // wavefronts per query tile (key-range split)
 
 __device__ __forceinline__ void split_f16(float v, _Float16& hi, _Float16& lo) {
     hi = (_Float16)v;
@@ -113,9 +119,11 @@ __global__ __launch_bounds__(64 * AF_WAVES) void attention_prefill_kernel(const 
                                                                           const uint16_t* __restrict__ vc, int pos0,
                                                                           int M, int max_ctx, float scale,
                                                                           float* __restrict__ out, int ldo) {
+    __shared__ float s_o[AF_WAVES - 1][32][64];  // (wavefronts 1..: wavefront 0 keeps its own)
+    __shared__ float s_m[AF_WAVES][16], s_l[AF_WAVES][16];
     const int h = blockIdx.x, lane = threadIdx.x & 63;
-    const int m0 = 16 * ((int)blockIdx.y * AF_WAVES + (int)(threadIdx.x >> 6));
-    if (m0 >= M) return;  // (the whole wavefront)
+    const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int m0 = 16 * (int)blockIdx.y;  // (< M: the grid has ceil(M / 16) tiles)
     const int r = lane & 15, g = lane >> 4;
     const int m = m0 + r;
     const int mq = m < M ? m : M - 1;
@@ -156,7 +164,10 @@ __global__ __launch_bounds__(64 * AF_WAVES) void attention_prefill_kernel(const 
     af_f4 o[8];
 #pragma unroll
     for (int t = 0; t < 8; t++) o[t] = af_f4{0.f, 0.f, 0.f, 0.f};
-    float mrun = -__builtin_inff(), lrun = 0.0f;
+    // (a finite floor: a range whose blocks are all past a row's position
+    // keeps m = -1e30, l = 0, o = 0 and weighs 0 in the merge; block 0, live
+    // for every row, is in wavefront 0's range)
+    float mrun = -1e30f, lrun = 0.0f;
     auto block = [&](int j0, const uint4 (&kf)[4], const uint4 (&vf)[4]) {
         af_f4 st = af_f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -173,8 +184,8 @@ __global__ __launch_bounds__(64 * AF_WAVES) void attention_prefill_kernel(const 
         }
         bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
         bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-        const float mnew = fmaxf(mrun, bmax);  // finite: cache row 0 is live for every query
-        const float c = expf(mrun - mnew);     // (0 on the first block, where lrun = o = 0)
+        const float mnew = fmaxf(mrun, bmax);  // finite (>= the floor)
+        const float c = expf(mrun - mnew);     // (0 on the first live block, where lrun = o = 0)
         float p[4], psum = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -209,26 +220,61 @@ __global__ __launch_bounds__(64 * AF_WAVES) void attention_prefill_kernel(const 
     };
     // two-block register ring: the next block's loads are in flight while a
     // block is computed (past the last block the ring re-reads its last one)
-    uint4 ka[4], va[4], kb[4], vb[4];
-    load_blk(0, ka, va);
-    int j0 = 0;
-    while (j0 <= jmax) {
-        load_blk(j0 + 16 <= jmax ? j0 + 16 : j0, kb, vb);
-        block(j0, ka, va);
-        j0 += 16;
-        if (j0 > jmax) break;
-        load_blk(j0 + 16 <= jmax ? j0 + 16 : j0, ka, va);
-        block(j0, kb, vb);
-        j0 += 16;
+    // this wavefront's blocks [b0, b1) of the tile's nblk
+    const int nblk = jmax / 16 + 1, per = (nblk + AF_WAVES - 1) / AF_WAVES;
+    const int b0 = w * per, b1 = min(nblk, b0 + per);
+    if (b0 < b1) {  // (wave-uniform)
+        const int jlast = 16 * (b1 - 1);
+        uint4 ka[4], va[4], kb[4], vb[4];
+        int j0 = 16 * b0;
+        load_blk(j0, ka, va);
+        while (true) {
+            load_blk(j0 + 16 <= jlast ? j0 + 16 : j0, kb, vb);
+            block(j0, ka, va);
+            j0 += 16;
+            if (j0 > jlast) break;
+            load_blk(j0 + 16 <= jlast ? j0 + 16 : j0, ka, va);
+            block(j0, kb, vb);
+            j0 += 16;
+            if (j0 > jlast) break;
+        }
     }
-    if (m < M) {
-        const float inv = 1.0f / lrun;
+    if (w > 0) {
+#pragma unroll
+        for (int t = 0; t < 8; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) s_o[w - 1][4 * t + i][lane] = o[t][i];
+    }
+    if (g == 0) {
+        s_m[w][r] = mrun;
+        s_l[w][r] = lrun;
+    }
+    __syncthreads();
+    if (w == 0 && m < M) {
+        float mx = s_m[0][r];
+#pragma unroll
+        for (int v = 1; v < AF_WAVES; v++) mx = fmaxf(mx, s_m[v][r]);
+        float wt[AF_WAVES], l = 0.0f;
+#pragma unroll
+        for (int v = 0; v < AF_WAVES; v++) {
+            wt[v] = expf(s_m[v][r] - mx);
+            l += s_l[v][r] * wt[v];
+        }
+        const float inv = 1.0f / l;
+        float res[32];
+#pragma unroll
+        for (int k = 0; k < 32; k++) {
+            float a = o[k >> 2][k & 3] * wt[0];
+#pragma unroll
+            for (int v = 1; v < AF_WAVES; v++) a = fmaf(s_o[v - 1][k][lane], wt[v], a);
+            res[k] = a * inv;
+        }
         float* orow = out + (size_t)m * ldo + (size_t)h * HD;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             float4* dst = reinterpret_cast<float4*>(orow + 8 * (4 * g + i));
-            dst[0] = make_float4(o[0][i] * inv, o[1][i] * inv, o[2][i] * inv, o[3][i] * inv);
-            dst[1] = make_float4(o[4][i] * inv, o[5][i] * inv, o[6][i] * inv, o[7][i] * inv);
+            dst[0] = make_float4(res[i], res[4 + i], res[8 + i], res[12 + i]);
+            dst[1] = make_float4(res[16 + i], res[20 + i], res[24 + i], res[28 + i]);
         }
     }
 }
@@ -272,7 +318,7 @@ hipError_t launch_rope_append_rows(float* qk, int ldqk, const float* v, int ldv,
 hipError_t launch_attention_prefill(const float* q, int ldq, const uint16_t* kc, const uint16_t* vc, int pos0, int M,
                                     int n_heads, int max_ctx, float scale, float* out, int ldo, hipStream_t s) {
     if (M <= 0) return hipSuccess;
-    hipLaunchKernelGGL(attention_prefill_kernel, dim3(n_heads, (M + 16 * AF_WAVES - 1) / (16 * AF_WAVES)),
+    hipLaunchKernelGGL(attention_prefill_kernel, dim3(n_heads, (M + 15) / 16),
                        dim3(64 * AF_WAVES), 0, s, q, ldq, kc, vc, pos0, M, max_ctx, scale, out, ldo);
     return hipGetLastError();
 }
