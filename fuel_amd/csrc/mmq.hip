@@ -659,7 +659,7 @@ __device__ __forceinline__ int bytes_times_p(uint32_t q, uint32_t f2) {
 template <int RT, int CT, int NW>
 __global__ __launch_bounds__(64 * NW) void mmq_q4k_wide_kernel(const uint8_t* __restrict__ W, ActView act,
                                                                float* __restrict__ y, int M, int N, int K, int ldy,
-                                                               int mt, int nt, int out_mode) {
+                                                               int mt, int nt, int ks, int out_mode) {
     using T = WideTile<RT, CT, NW>;
     constexpr int BM = T::BM, BN = T::BN;
     __shared__ __align__(16) uint8_t sB0[T::LBUF], sB1[T::LBUF];
@@ -670,11 +670,15 @@ __global__ __launch_bounds__(64 * NW) void mmq_q4k_wide_kernel(const uint8_t* __
     const uint32_t row_bytes = (uint32_t)KB * Q4K_BYTES;
     const int l16 = lane & 15, kb = lane >> 4;
 
-    const int total = mt * nt, L = blockIdx.x;
+    const int total = mt * nt, z = blockIdx.x / total, L = blockIdx.x - z * total;
     const int x = L & 7, slot = L >> 3, q8 = total >> 3, r8 = total & 7;
     const int tile = x * q8 + (x < r8 ? x : r8) + slot;  // XCD x's contiguous range of tiles
     const int mtile = tile % mt, ntile = tile / mt;
     const int m0 = mtile * BM, n0 = ntile * BN;
+    // K split z of ks: superblocks [bs, be) into partial z (y then points at
+    // the partials, ldy = N)
+    const int per = (KB + ks - 1) / ks, bs = z * per, be = min(KB, bs + per);
+    y += (size_t)z * M * ldy;
 
     // per-lane source byte offsets (superblock 0) of DMA instruction i of each
     // kind; rows past M read offset 0 and tail columns column N-1 (valid
@@ -763,9 +767,9 @@ __global__ __launch_bounds__(64 * NW) void mmq_q4k_wide_kernel(const uint8_t* __
 #pragma unroll
             for (int i = 0; i < 4; i++) facc[r][c][i] = 0.0f;
 
-    const int b1 = KB;
+    const int b1 = be;
     const uint32_t slot0 = lds_addr(sB0), slot1 = lds_addr(sB1);
-    issue(0, slot0);
+    if (bs < be) issue(bs, slot0);
 
     auto iter = [&](auto kr, int b) __attribute__((always_inline)) {
         constexpr int KR = decltype(kr)::value;
@@ -853,7 +857,7 @@ __global__ __launch_bounds__(64 * NW) void mmq_q4k_wide_kernel(const uint8_t* __
             }
         }
     };
-    for (int b = 0; b < b1; b += 2) {
+    for (int b = bs; b < b1; b += 2) {
         iter(std::integral_constant<int, 0>{}, b);
         if (b + 1 < b1) iter(std::integral_constant<int, 1>{}, b + 1);
     }
@@ -1056,15 +1060,6 @@ hipError_t launch_wide6(const uint8_t* w, ActView act, float* y, int M, int N, i
     return hipGetLastError();
 }
 
-template <int RT, int CT, int NW>
-hipError_t launch_wide(const uint8_t* w, ActView act, float* y, int M, int N, int K, int ldy, hipStream_t s,
-                       int out_mode) {
-    using T = WideTile<RT, CT, NW>;
-    const int mt = (M + T::BM - 1) / T::BM, nt = (N + T::BN - 1) / T::BN;
-    hipLaunchKernelGGL((mmq_q4k_wide_kernel<RT, CT, NW>), dim3(mt * nt), dim3(T::NT), 0, s, w, act, y, M, N, K, ldy,
-                       mt, nt, out_mode);
-    return hipGetLastError();
-}
 
 // y[m][n] = sum over splits z (in order) of part[z][m][n]
 __global__ void mmq_reduce_kernel(const float* __restrict__ part, float* __restrict__ y, int M, int N, int ldy,
@@ -1075,6 +1070,28 @@ __global__ void mmq_reduce_kernel(const float* __restrict__ part, float* __restr
     for (int z = 1; z < nsplit; z++) s += part[(size_t)z * M * N + i];
     const size_t o = (i / N) * ldy + i % N;
     store_out(y, o, s, out_mode);
+}
+
+// The wide Q4_K kernel, over ks K splits (ks > 1: into part[ks][M][N], then
+// mmq_reduce_kernel adds them in split order into y).
+template <int RT, int CT, int NW>
+hipError_t launch_wide(const uint8_t* w, ActView act, float* y, int M, int N, int K, int ldy, hipStream_t s,
+                       int out_mode, int ks = 1, float* part = nullptr) {
+    using T = WideTile<RT, CT, NW>;
+    const int mt = (M + T::BM - 1) / T::BM, nt = (N + T::BN - 1) / T::BN;
+    if (ks > 1 && !part) return hipErrorInvalidValue;
+    if (ks > 1)
+        hipLaunchKernelGGL((mmq_q4k_wide_kernel<RT, CT, NW>), dim3(mt * nt * ks), dim3(T::NT), 0, s, w, act, part, M,
+                           N, K, N, mt, nt, ks, 0);
+    else
+        hipLaunchKernelGGL((mmq_q4k_wide_kernel<RT, CT, NW>), dim3(mt * nt), dim3(T::NT), 0, s, w, act, y, M, N, K,
+                           ldy, mt, nt, 1, out_mode);
+    if (ks > 1) {
+        const size_t total = (size_t)M * N;
+        hipLaunchKernelGGL(mmq_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, y, M, N,
+                           ldy, ks, out_mode);
+    }
+    return hipGetLastError();
 }
 
 // Resident workgroups per CU of a kernel instantiation (cached per instantiation).
@@ -1207,7 +1224,22 @@ MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus, siz
     // wide-tile kernels (Q4_K: two MFMAs per product instead of three; both:
     // the DMA ring out of the compiler's sight; Q4_K measured 19-25% faster at
     // M = 512 on the 7B shapes)
-    if (dma && M >= 128 && p.ks == 1) p.kind = MMQ_Q4K_WIDE;
+    // (and for 128-255 rows of long rows, K >= 8192, K-split like the plane
+    // kernels: 11008x4096 at M = 128 36.9 -> 34.9 us, M = 160 57.6 -> 42.9,
+    // M = 250 61.4 -> 53.9; at K = 4096 the plane kernels' split stays
+    // faster, 23.1 against 26.0 us at 4096x4096 M = 128)
+    const bool wide_split = dma && M >= 128 && M < 256 && K >= 32 * QK_K;
+    if (dma && M >= 128 && (p.ks == 1 || wide_split)) {
+        using T = WideTile<4, 1, 8>;
+        p.kind = MMQ_Q4K_WIDE;
+        p.ks = 1;
+        if (wide_split) {
+            const int tiles = ((M + T::BM - 1) / T::BM) * ((N + T::BN - 1) / T::BN);
+            const int occ = kernel_occupancy(mmq_q4k_wide_kernel<4, 1, 8>, T::NT);
+            p.ks = mmq_ksplit(tiles, occ, num_cus, K / QK_K);
+            while (p.ks > 1 && (size_t)p.ks * M * N > max_part_elems) p.ks--;
+        }
+    }
     if (dtype == GGML_Q6K && M >= 128 && p.ks == 1) p.kind = MMQ_Q6K_WIDE;
     p.part_elems = p.ks > 1 ? (size_t)p.ks * M * N : 0;
     return p;
@@ -1221,7 +1253,7 @@ hipError_t launch_mmq(const MmqPlan& plan, int dtype, const uint8_t* w, ActView 
     case kind: return launch_cfg<F, RT, CT, WM, WN, DMA>(plan, w, act, y, part, M, N, K, ldy, s, out_mode);
         FRQ_MMQ_KINDS(FRQ_LAUNCH)
 #undef FRQ_LAUNCH
-        case MMQ_Q4K_WIDE: return launch_wide<4, 1, 8>(w, act, y, M, N, K, ldy, s, out_mode);
+        case MMQ_Q4K_WIDE: return launch_wide<4, 1, 8>(w, act, y, M, N, K, ldy, s, out_mode, plan.ks, part);
         case MMQ_Q6K_WIDE: return launch_wide6<4, 8>(w, act, y, M, N, K, ldy, s, out_mode);
         default: return hipErrorInvalidValue;
     }
