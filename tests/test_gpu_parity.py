@@ -391,12 +391,13 @@ def test_qmatmul_mfma_rows(dev, dt, m):
 
 @pytest.mark.parametrize("dt", [O.Q4K, O.Q6K])
 @pytest.mark.parametrize("k,n", SHAPES_7B)
-@pytest.mark.parametrize("m", [16, 24, 32, 128, 512])
+@pytest.mark.parametrize("m", [16, 24, 32, 48, 128, 200, 512])
 def test_qmatmul_mfma_7b_shapes(dev, dt, k, n, m):
     """M = 32 / 128 / 512 rows at the four 7B shapes (the
     43-superblock rows of K = 11008, split K, the 128 x 64 tiles, the LDS-DMA
-    staging), and 16 / 24 rows (the tiled kernel's partly empty 32-row tiles
-    for the wide matrices, the skinny kernel at N = 4096), against the oracle."""
+    staging), 16 / 24 rows (the tiled kernel's partly empty 32-row tiles
+    for the wide matrices, the skinny kernel at N = 4096) and 48 / 200 rows
+    (the wide tiles with a K split at K = 11008), against the oracle."""
     say("mfma", dt, "m", m, k, n)
     wq = weights(dt, n, k)
     x = acts(m, k)
