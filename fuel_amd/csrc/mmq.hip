@@ -899,7 +899,7 @@ struct WideTile6 {
 template <int RT, int NW>
 __global__ __launch_bounds__(64 * NW) void mmq_q6k_wide_kernel(const uint8_t* __restrict__ W, ActView act,
                                                                float* __restrict__ y, int M, int N, int K, int ldy,
-                                                               int mt, int nt, int ks, int out_mode) {
+                                                               int mt, int nt, int out_mode) {
     using T = WideTile6<RT, NW>;
     using F = MmqQ6K;
     constexpr int BM = T::BM, BN = T::BN;
@@ -911,15 +911,11 @@ __global__ __launch_bounds__(64 * NW) void mmq_q6k_wide_kernel(const uint8_t* __
     const uint32_t row_bytes = (uint32_t)KB * Q6K_BYTES;
     const int l16 = lane & 15, kb = lane >> 4;
 
-    const int total = mt * nt, z = blockIdx.x / total, L = blockIdx.x - z * total;
+    const int total = mt * nt, L = blockIdx.x;
     const int x = L & 7, slot = L >> 3, q8 = total >> 3, r8 = total & 7;
     const int tile = x * q8 + (x < r8 ? x : r8) + slot;  // XCD x's contiguous range of tiles
     const int mtile = tile % mt, ntile = tile / mt;
     const int m0 = mtile * BM, n0 = ntile * BN;
-    // K split z of ks: superblocks [bs, be) into partial z (y then points at
-    // the partials, ldy = N)
-    const int per = (KB + ks - 1) / ks, bs = z * per, be = min(KB, bs + per);
-    y += (size_t)z * M * ldy;
 
     auto a_src = [&](int i) {
         const int q = 64 * i + lane, r = q >> 4, m = m0 + r;
@@ -994,13 +990,11 @@ __global__ __launch_bounds__(64 * NW) void mmq_q6k_wide_kernel(const uint8_t* __
 #pragma unroll
         for (int i = 0; i < 4; i++) facc[r][i] = 0.0f;
 
-    const int b1 = be;
+    const int b1 = KB;
     const uint32_t slot0 = lds_addr(sB0), slot1 = lds_addr(sB1);
-    if (bs < be) {  // (workgroup-uniform)
-        issue(bs, slot0);
-        wload(bs);
-        wstore(sB0);
-    }
+    issue(0, slot0);
+    wload(0);
+    wstore(sB0);
 
     auto iter = [&](auto kr, int b) __attribute__((always_inline)) {
         constexpr int KR = decltype(kr)::value;
@@ -1040,7 +1034,7 @@ __global__ __launch_bounds__(64 * NW) void mmq_q6k_wide_kernel(const uint8_t* __
         }
         if (more) wstore(KR == 0 ? sB1 : sB0);
     };
-    for (int b = bs; b < b1; b += 2) {
+    for (int b = 0; b < b1; b += 2) {
         iter(std::integral_constant<int, 0>{}, b);
         if (b + 1 < b1) iter(std::integral_constant<int, 1>{}, b + 1);
     }
@@ -1058,7 +1052,13 @@ __global__ __launch_bounds__(64 * NW) void mmq_q6k_wide_kernel(const uint8_t* __
 
 template <int RT, int NW>
 hipError_t launch_wide6(const uint8_t* w, ActView act, float* y, int M, int N, int K, int ldy, hipStream_t s,
-                        int out_mode, int ks = 1, float* part = nullptr);
+                        int out_mode) {
+    using T = WideTile6<RT, NW>;
+    const int mt = (M + T::BM - 1) / T::BM, nt = (N + T::BN - 1) / T::BN;
+    hipLaunchKernelGGL((mmq_q6k_wide_kernel<RT, NW>), dim3(mt * nt), dim3(T::NT), 0, s, w, act, y, M, N, K, ldy, mt,
+                       nt, out_mode);
+    return hipGetLastError();
+}
 
 
 // y[m][n] = sum over splits z (in order) of part[z][m][n]
@@ -1086,27 +1086,6 @@ hipError_t launch_wide(const uint8_t* w, ActView act, float* y, int M, int N, in
     else
         hipLaunchKernelGGL((mmq_q4k_wide_kernel<RT, CT, NW>), dim3(mt * nt), dim3(T::NT), 0, s, w, act, y, M, N, K,
                            ldy, mt, nt, 1, out_mode);
-    if (ks > 1) {
-        const size_t total = (size_t)M * N;
-        hipLaunchKernelGGL(mmq_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, y, M, N,
-                           ldy, ks, out_mode);
-    }
-    return hipGetLastError();
-}
-
-// The wide Q6_K kernel, over ks K splits (as launch_wide).
-template <int RT, int NW>
-hipError_t launch_wide6(const uint8_t* w, ActView act, float* y, int M, int N, int K, int ldy, hipStream_t s,
-                        int out_mode, int ks, float* part) {
-    using T = WideTile6<RT, NW>;
-    const int mt = (M + T::BM - 1) / T::BM, nt = (N + T::BN - 1) / T::BN;
-    if (ks > 1 && !part) return hipErrorInvalidValue;
-    if (ks > 1)
-        hipLaunchKernelGGL((mmq_q6k_wide_kernel<RT, NW>), dim3(mt * nt * ks), dim3(T::NT), 0, s, w, act, part, M, N,
-                           K, N, mt, nt, ks, 0);
-    else
-        hipLaunchKernelGGL((mmq_q6k_wide_kernel<RT, NW>), dim3(mt * nt), dim3(T::NT), 0, s, w, act, y, M, N, K, ldy,
-                           mt, nt, 1, out_mode);
     if (ks > 1) {
         const size_t total = (size_t)M * N;
         hipLaunchKernelGGL(mmq_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, y, M, N,
@@ -1263,20 +1242,7 @@ MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus, siz
             while (p.ks > 1 && (size_t)p.ks * M * N > max_part_elems) p.ks--;
         }
     }
-    // (Q6_K likewise: 11008x4096 M = 48 33.3 -> 27.1 us, M = 96 54.6 -> 37.9,
-    // M = 128 52.0 -> 41.6, M = 200 76.3 -> 66.3, 11008x8192 M = 64 57.8 -> 44.0)
-    const bool wide6_split = dtype == GGML_Q6K && M >= 33 && M < 256 && K >= 32 * QK_K;
-    if (dtype == GGML_Q6K && ((M >= 128 && p.ks == 1) || wide6_split)) {
-        using T = WideTile6<4, 8>;
-        p.kind = MMQ_Q6K_WIDE;
-        p.ks = 1;
-        if (wide6_split) {
-            const int tiles = ((M + T::BM - 1) / T::BM) * ((N + T::BN - 1) / T::BN);
-            const int occ = kernel_occupancy(mmq_q6k_wide_kernel<4, 8>, T::NT);
-            p.ks = mmq_ksplit(tiles, occ, num_cus, K / QK_K);
-            while (p.ks > 1 && (size_t)p.ks * M * N > max_part_elems) p.ks--;
-        }
-    }
+    if (dtype == GGML_Q6K && M >= 128 && p.ks == 1) p.kind = MMQ_Q6K_WIDE;
     p.part_elems = p.ks > 1 ? (size_t)p.ks * M * N : 0;
     return p;
 }
@@ -1290,7 +1256,7 @@ hipError_t launch_mmq(const MmqPlan& plan, int dtype, const uint8_t* w, ActView 
         FRQ_MMQ_KINDS(FRQ_LAUNCH)
 #undef FRQ_LAUNCH
         case MMQ_Q4K_WIDE: return launch_wide<4, 1, 8>(w, act, y, M, N, K, ldy, s, out_mode, plan.ks, part);
-        case MMQ_Q6K_WIDE: return launch_wide6<4, 8>(w, act, y, M, N, K, ldy, s, out_mode, plan.ks, part);
+        case MMQ_Q6K_WIDE: return launch_wide6<4, 8>(w, act, y, M, N, K, ldy, s, out_mode);
         default: return hipErrorInvalidValue;
     }
 }
