@@ -1224,13 +1224,15 @@ MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus, siz
     // wide-tile kernels (Q4_K: two MFMAs per product instead of three; both:
     // the DMA ring out of the compiler's sight; Q4_K measured 19-25% faster at
     // M = 512 on the 7B shapes)
-    // (and for 33-255 rows of long rows, K >= 8192, K-split like the plane
+    // (and for 33-384 rows of long rows, K >= 8192, K-split like the plane
     // kernels: 11008x4096 at M = 33 26.2 -> 24.3 us, M = 96 41.5 -> 33.3,
     // M = 128 36.9 -> 34.9, M = 160 57.6 -> 42.9, M = 250 61.4 -> 53.9,
+    // M = 256 61.3 -> 52.0, M = 384 75.6 -> 71.2 (at 511 rows two splits
+    // lose: 79.1 against 81.3 us),
     // 11008x8192 M = 40 42.9 -> 33.8, M = 64 44.3 -> 35.2; at K = 4096 the
     // plane kernels' split stays faster, 23.1 against 26.0 us at 4096x4096
     // M = 128, and below 33 rows it is no faster)
-    const bool wide_split = dma && M >= 33 && M < 256 && K >= 32 * QK_K;
+    const bool wide_split = dma && M >= 33 && M <= 384 && K >= 32 * QK_K;
     if ((dma && M >= 128 && p.ks == 1) || wide_split) {
         using T = WideTile<4, 1, 8>;
         p.kind = MMQ_Q4K_WIDE;
