@@ -71,3 +71,17 @@ def test_device_quantize_imatrix_errors(dev):
         assert e.value.status == FRQ_INVALID
     with pytest.raises(F.FuelRocmError):  # source size mismatch
         q4.quantize_imatrix(dev.from_numpy(O.normal((1, 256), seed=1, stream=1)), w, 256)
+
+
+def test_device_quantize_imatrix_importance_formula(dev):
+    """The importance-formula known answer (weight_kat.q4k_imatrix_formula_case:
+    dmin is the float64 least-squares fit over sw_j = sum imatrix *
+    sqrt(2 sum(x^2)/256 + x^2)) through frq_qstorage_quantize_imatrix."""
+    from weight_kat import q4k_imatrix_formula_case
+
+    x, qw, want = q4k_imatrix_formula_case()
+    say("device from_float_imatrix, importance-formula block")
+    assert device_imatrix(dev, O.Q4K, x.reshape(1, 256), qw, 256) == want.tobytes()
+    # the same block repeated over a 4-superblock row, the importance matrix tiled per row
+    x4 = np.tile(x, 4).reshape(1, 1024)
+    assert device_imatrix(dev, O.Q4K, x4, np.tile(qw, 4), 1024) == want.tobytes() * 4

@@ -21,7 +21,15 @@ What pins them:
   leaves every byte unchanged: every sum doubles exactly), and
   sqrt(sigma2 + x^2) is homogeneous in x (doubling x doubles d and dmin and
   keeps every scale and code), and column blocks repeat per n_per_row.
+* The importance formula itself (sigma2 = 2 sum(x^2) / 256 and the square
+  root in w = imatrix * sqrt(sigma2 + x^2), k_quants.rs:1539-1548): a block
+  whose dmin is a weighted least-squares fit over the sub-block weights sw_j,
+  worked out in float64 with its rounding margins (weight_kat); dropping the
+  factor 2 or the square root moves dmin's f16 bits, and copies of the oracle
+  with either slip planted fail it.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -159,3 +167,78 @@ def test_imatrix_types_and_row_sizes():
         O.quantize_imatrix(O.Q8_0, x, w, 256)
     with pytest.raises(ValueError):
         O.quantize_imatrix(O.Q4K, x, w, 100)
+
+
+def test_q4k_imatrix_importance_formula_known_answer():
+    """The block of weight_kat.q4k_imatrix_formula_case: its dmin is the
+    weighted least-squares fit over sw_j = sum imatrix * sqrt(sigma2 + x^2),
+    sigma2 = 2 sum(x^2) / 256, worked out in float64; the margins show that
+    neither the f16 rounding of dmin nor a code of the search sits near a
+    boundary."""
+    from weight_kat import code_margin, imatrix_margins, q4k_imatrix_formula_case
+
+    x, qw, want = q4k_imatrix_formula_case()
+    f16_margin, descent_margin = imatrix_margins(x, qw)
+    assert f16_margin > 0.3 and descent_margin > 0.15, (f16_margin, descent_margin)
+    assert code_margin(O.Q4K, x, want) < 0.1
+    got = O.quantize_imatrix(O.Q4K, x.reshape(1, 256), qw, 256)
+    assert got.tobytes() == want.tobytes(), (got, want)
+
+
+def test_q4k_imatrix_formula_slips_change_the_known_answer():
+    """Each plausible slip of the importance formula moves dmin's f16 bits in
+    the closed form, by more than one unit."""
+    from weight_kat import imatrix_formula_dmin, imatrix_formula_inputs
+
+    x, qw = imatrix_formula_inputs()
+    bits = lambda v: int(np.float16(v).view(np.uint16))
+    right = bits(imatrix_formula_dmin(x, qw))
+    for slip in ({"sigma2_factor": 1.0}, {"sqrt": False}, {"sigma2_factor": 1.0, "sqrt": False}):
+        assert abs(bits(imatrix_formula_dmin(x, qw, **slip)) - right) >= 2, slip
+
+
+MUTATIONS = {
+    "sigma2 without the factor 2": ("float sigma2 = 2.0f * sum_x2 / (float)FO_QK_K;",
+                                    "float sigma2 = sum_x2 / (float)FO_QK_K;"),
+    "weights without the square root": ("weights[l] = qw[32 * j + l] * sqrtf(sigma2 + xe * xe);",
+                                        "weights[l] = qw[32 * j + l] * (sigma2 + xe * xe);"),
+}
+
+
+@pytest.mark.parametrize("name", [None] + sorted(MUTATIONS))
+def test_q4k_imatrix_known_answer_catches_a_planted_slip(tmp_path, name):
+    """The known answer fails a copy of the oracle with the slip planted in its
+    Q4K from_float_imatrix (built here with the oracle's own flags), and passes
+    the unmodified copy built the same way."""
+    import ctypes
+    import shutil
+    import subprocess
+
+    from weight_kat import q4k_imatrix_formula_case
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    src = open(os.path.join(os.path.dirname(O.__file__), "fuel_oracle.c")).read()
+    if name is not None:
+        old, new = MUTATIONS[name]
+        assert src.count(old) == 1, f"the line to mutate is not in the oracle: {old}"
+        src = src.replace(old, new)
+    d = tmp_path / "mut"
+    d.mkdir()
+    shutil.copy(os.path.join(os.path.dirname(O.__file__), "fuel_oracle.h"), d / "fuel_oracle.h")
+    (d / "fuel_oracle.c").write_text(src)
+    so = d / "libmut.so"
+    subprocess.run([cc, "-O2", "-std=c11", "-fPIC", "-fopenmp", "-ffp-contract=off", "-fno-fast-math", "-shared",
+                    "-o", str(so), str(d / "fuel_oracle.c"), "-lm"], check=True)
+    lib = ctypes.CDLL(str(so))
+    lib.fo_quantize_imatrix.restype = ctypes.c_int
+    lib.fo_quantize_imatrix.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                        ctypes.c_size_t, ctypes.c_void_p]
+    x, qw, want = q4k_imatrix_formula_case()
+    got = np.zeros(1, O.BLOCK_Q4K)
+    assert lib.fo_quantize_imatrix(O.Q4K, x.ctypes.data, 256, qw.ctypes.data, 256, got.ctypes.data) == 0
+    if name is None:
+        assert got.tobytes() == want.tobytes()
+    else:
+        assert got.tobytes() != want.tobytes(), name

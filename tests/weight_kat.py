@@ -320,6 +320,121 @@ def q6k_zero_case():
     return np.zeros(256, np.float32), b
 
 
+# ---------------------------------------------------------------------------
+# Q4K from_float_imatrix: the importance formula
+# ---------------------------------------------------------------------------
+
+IMX_QB = 3.0  # importance of the zero elements of sub-blocks 4..7
+
+
+def q4k_imatrix_formula_case():
+    """A block whose bytes depend on the importance formula of
+    BlockQ4K::from_float_imatrix (k_quants.rs:1539-1548):
+
+      sigma2 = 2 * sum(x^2) / 256,   w_l = imatrix_l * sqrt(sigma2 + x_l^2),
+      sw_j = sum over sub-block j of w_l.
+
+    Sub-blocks 0..3 ("A"): x = -15 at element 0, 0 elsewhere (a grid with step
+    1 from min -15, codes 0 and 15): make_qkx3_quants (utils.rs:358-469) fits
+    it with zero error at its first pass, so it returns (1, 15) for any
+    weights.  Sub-blocks 4..7 ("B"): x = -1, 14, then 30 zeros (grid from min
+    -1, codes 0, 15, 1): (1, 1).  sum(x^2) = 4*225 + 4*197 = 1688, sigma2 =
+    13.1875 exactly.
+
+    Importance: 1 on each A sub-block's -15 (x^2 = 225 >> sigma2), IMX_QB on
+    each B sub-block's 30 zeros (x^2 = 0 << sigma2), 1e-3 elsewhere.  So sw_A
+    follows |x| and barely sigma2, sw_B follows sqrt(sigma2): the factor 2 and
+    the square root set the ratio sw_B / sw_A.
+
+    make_qp_quants (utils.rs:472-563) over the eight scales (all 1) gives codes
+    63 and d = 1/63 -> f16 bits 9232.  Over the mins (15 x 4, 1 x 4): max 15,
+    iscale 63/15 = 4.2, codes 63 and round(4.2) = 4 for every candidate
+    iscale of the search ((63 + 0.1 is) and (4.2 + is/150) round to 63 and 4
+    for |is| <= 4), and the coordinate descent keeps them (its proposals
+    m_j * sl2 / slx stay inside (62.5, 63.5] and (3.5, 4.5): `imatrix_margins`).
+    The result is the weighted least-squares fit
+
+      dmin = (945 W_A + 4 W_B) / (3969 W_A + 16 W_B),  W_A = sum_{j<4} sw_j,
+                                                      W_B = sum_{j>=4} sw_j,
+
+    evaluated in float64 and rounded to f16 (its distance from the f16
+    rounding boundary is checked by `imatrix_margins`).  Codes: A -> 0 at the
+    -15 and 15 elsewhere, B -> 0, 15, then 1 ((x + dmin*m) / (d*sc) with d*sc
+    ~ 1 and dmin*m ~ 15.06 / 0.956).
+
+    With sigma2 = sum(x^2)/256 the same closed form gives dmin bits 2 below,
+    without the square root 6 below: either slip changes the bytes.
+    """
+    x, qw = imatrix_formula_inputs()
+    dmin = imatrix_formula_dmin(x, qw)
+    ls = [63] * 8
+    lm = [63, 63, 63, 63, 4, 4, 4, 4]
+    codes = np.full(256, 15, np.int64)
+    for j in range(4):
+        codes[32 * j] = 0
+    for j in range(4, 8):
+        codes[32 * j:32 * j + 32] = 1
+        codes[32 * j] = 0
+        codes[32 * j + 1] = 15
+    d_bits = f16_bits(np.float32(1.0) / np.float32(63))
+    return x, qw, _q4k_block(d_bits, int(np.float16(dmin).view(np.uint16)), ls, lm, codes)
+
+
+def imatrix_formula_inputs():
+    x = np.zeros(256, np.float32)
+    qw = np.full(256, 1e-3, np.float32)
+    for j in range(4):
+        x[32 * j] = -15.0
+        qw[32 * j] = 1.0
+    for j in range(4, 8):
+        x[32 * j] = -1.0
+        x[32 * j + 1] = 14.0
+        qw[32 * j + 2:32 * j + 32] = IMX_QB
+    return x, qw
+
+
+def imatrix_formula_sw(x, qw, sigma2_factor=2.0, sqrt=True):
+    """sw_j of the block in float64; the keyword arguments give the slips."""
+    x = x.astype(np.float64)
+    sigma2 = sigma2_factor * float(np.sum(x * x)) / 256.0
+    t = sigma2 + x * x
+    return (qw.astype(np.float64) * (np.sqrt(t) if sqrt else t)).reshape(8, 32).sum(1)
+
+
+IMX_MINS = np.array([15, 15, 15, 15, 1, 1, 1, 1], np.float64)
+IMX_LM = np.array([63, 63, 63, 63, 4, 4, 4, 4], np.float64)
+
+
+def imatrix_formula_dmin(x, qw, **slip):
+    sw = imatrix_formula_sw(x, qw, **slip)
+    wa, wb = sw[:4].sum(), sw[4:].sum()
+    return (945.0 * wa + 4.0 * wb) / (3969.0 * wa + 16.0 * wb)
+
+
+def imatrix_margins(x, qw):
+    """(f16 margin of dmin in ulps, worst descent-proposal margin): the first
+    is the distance of the float64 dmin from the nearest f16 rounding boundary
+    (0.5 = on an f16 value), the second the smallest distance of a proposal
+    m_j * sl2 / slx (the fit without element j, utils.rs:540-553) from the
+    boundary that would change its code."""
+    dmin = imatrix_formula_dmin(x, qw)
+    ulp = 2.0 ** (np.floor(np.log2(dmin)) - 10)
+    u = dmin / ulp
+    f16_margin = abs((u - np.floor(u)) - 0.5)
+    sw = imatrix_formula_sw(x, qw)
+    worst = 1.0
+    for j in range(8):
+        keep = np.arange(8) != j
+        slx = float((sw * IMX_MINS * IMX_LM)[keep].sum())
+        sl2 = float((sw * IMX_LM * IMX_LM)[keep].sum())
+        p = IMX_MINS[j] * sl2 / slx
+        if j < 4:
+            worst = min(worst, p - 62.5)  # anything above rounds to 63 or is clamped to it
+        else:
+            worst = min(worst, p - 3.5, 4.5 - p)
+    return f16_margin, worst
+
+
 CASES = {
     "q4k_grid": (O.Q4K, q4k_grid_case),
     "q4k_edge": (O.Q4K, q4k_edge_case),
