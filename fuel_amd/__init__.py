@@ -18,6 +18,7 @@ from .backend import (
     moe_ffn,
     moe_route,
     qmatmul_f32_rocm_wrapper,
+    qmatmul_plan,
     quantize_q8_0,
     quantize_q8k,
     type_size,
@@ -28,5 +29,5 @@ __all__ = [
     "F16", "F32", "Q4K", "Q6K", "Q8K", "Q8_0", "FuelRocmError", "LIB_PATH", "SIGNATURES", "lib",
     "QMatMulParams", "RocmDevice", "RocmQStorage", "RocmStorage", "block_isums", "block_size",
     "device_count", "fill_normal", "fill_random_bits", "moe_ffn", "moe_route",
-    "qmatmul_f32_rocm_wrapper", "quantize_q8_0", "quantize_q8k", "type_size", "GgufFile",
+    "qmatmul_f32_rocm_wrapper", "qmatmul_plan", "quantize_q8_0", "quantize_q8k", "type_size", "GgufFile",
 ]

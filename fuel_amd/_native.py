@@ -68,6 +68,8 @@ SIGNATURES = {
     "frq_qstorage_fwd_f16": (_i32, [_vp, _sz, _sz, _vp, _sz, _vp]),
     "frq_qmatmul": (_i32, [_vp, _i32, _sz, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz]),
     "frq_qmatmul_noalloc": (_i32, [_vp, _i32, _sz, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz]),
+    "frq_qmatmul_plan": (_i32, [_vp, _i32, _sz, _sz, _sz, _vp, _i32, C.POINTER(C.c_int), C.POINTER(C.c_int),
+                                C.POINTER(C.c_int)]),
     "frq_quantize_q8k": (_i32, [_vp, _vp, _sz, _sz, _vp]),
     "frq_quantize_q8_0": (_i32, [_vp, _vp, _sz, _sz, _vp]),
     "frq_moe_route": (_i32, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp]),

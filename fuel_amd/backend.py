@@ -301,6 +301,18 @@ def fill_random_bits(dev: RocmDevice, n: int, start: int, seed: int, base: int, 
 
 # ---- parity taps ----
 
+QMM_PATHS = ("matvec", "matvec_multi", "skinny_mfma", "tiled_mfma")
+
+
+def qmatmul_plan(dev: RocmDevice, ggml_dtype: int, rows: int, n: int, k: int, w_ptr: int, noalloc: bool = False):
+    """The kernels frq_qmatmul (or frq_qmatmul_noalloc) runs for this call:
+    (path name, tile kernel kind or -1, K splits)."""
+    path, kind, ks = C.c_int(), C.c_int(), C.c_int()
+    check(lib().frq_qmatmul_plan(dev.handle, ggml_dtype, rows, n, k, C.c_void_p(w_ptr), int(noalloc), C.byref(path),
+                                 C.byref(kind), C.byref(ks)))
+    return QMM_PATHS[path.value], kind.value, ks.value
+
+
 def quantize_q8k(dev: RocmDevice, x: RocmStorage, rows: int, k: int) -> np.ndarray:
     """Device BlockQ8K quantization of x [rows, k]; returns the block bytes."""
     out = dev.alloc((rows * (k // 256) * 292,), np.uint8)

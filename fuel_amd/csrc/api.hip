@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <mutex>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -36,6 +37,12 @@ struct frq_device {
     // references: the open handle plus one per live storage; the struct is
     // deleted when the last one is dropped (a storage may outlive close)
     std::atomic<int> refs{1};
+    // held by every entry point that enqueues work on the device or touches
+    // its stream or workspace: calls from several threads (on the handle or
+    // on storages of the device) take turns on the host, and their work runs
+    // in call order on the one stream, so a workspace grown by one call is
+    // never freed under another's kernels (hipFree waits for them)
+    std::recursive_mutex mu;
 };
 
 struct frq_gguf {
@@ -161,6 +168,20 @@ int use_device(frq_device* dev) {
     return FRQ_OK;
 }
 
+// The device lock for the duration of an entry point (no-op for a null
+// handle, which use_device then rejects).
+struct DevGuard {
+    frq_device* d;
+    explicit DevGuard(frq_device* dev) : d(dev) {
+        if (d) d->mu.lock();
+    }
+    ~DevGuard() {
+        if (d) d->mu.unlock();
+    }
+    DevGuard(const DevGuard&) = delete;
+    DevGuard& operator=(const DevGuard&) = delete;
+};
+
 void release_device(frq_device* dev) {
     if (dev->refs.fetch_sub(1) == 1) delete dev;
 }
@@ -215,14 +236,23 @@ int quantize_rows(frq_device* dev, int vt, const float* x, size_t rows, size_t k
     return FRQ_OK;
 }
 
-// y[rows, n] = x[rows, k] @ dequant(W[n, k])^T through the int8 path, with
-// its scratch (quantized rows, split-K partials) from `fx` when that is set.
-int run_qmatmul(frq_device* dev, int t, const uint8_t* w, const float* x, size_t rows, size_t n,
-                size_t k, float* y, const Scratch& fx = Scratch{}) {
-    if (rows == 0 || n == 0) return FRQ_OK;
+// Which kernels a QMatMul of `rows` activation rows runs (frq_qmatmul_plan
+// reports it): a pure function of the call's shape, weight type, the weight
+// base's 16-byte alignment, the device's CU count and whether the scratch is
+// the allocation-free entry point's fixed array -- never of earlier calls.
+enum QmmPath { QMM_MATVEC = 0, QMM_MULTI = 1, QMM_SKINNY = 2, QMM_TILED = 3 };
+
+struct QmmPlan {
+    int path = QMM_MATVEC;
+    MmqPlan mmq{};        // QMM_TILED: kernel kind and K split
+    size_t abytes = 0;    // QMM_TILED / QMM_SKINNY: quantized-row scratch bytes
+};
+
+int plan_qmatmul(const frq_device* dev, int t, const uint8_t* w, size_t rows, size_t n, size_t k, const Scratch& fx,
+                 QmmPlan* p) {
+    *p = QmmPlan{};
     if (k > (size_t)0x7fffffff || n > (size_t)0x7fffffff || rows > 65535)
-        return fail(FRQ_UNSUPPORTED, "qmatmul: rows=%zu n=%zu k=%zu exceed the launch limits", rows,
-                    n, k);
+        return fail(FRQ_UNSUPPORTED, "qmatmul: rows=%zu n=%zu k=%zu exceed the launch limits", rows, n, k);
     // each lane of the mat-vec holds at most 8 blocks of a row: K <= 8 * 16 * 256
     // for the k-quants (4 lanes per superblock), K <= 8 * 32 * 32 for Q8_0;
     // longer rows (K a multiple of 256) take the skinny MFMA kernel, any K
@@ -233,43 +263,67 @@ int run_qmatmul(frq_device* dev, int t, const uint8_t* w, const float* x, size_t
     // the tiled MFMA kernel addresses the weights with 32-bit offsets
     const bool w32 = n * (k / block_elems(t)) * type_size(t) <= 0xffffffffull;
     if (tiled_rows(rows, n) && mmq_supported(t) && w32) {
-        // many activation rows: quantize them once, then the int8-MFMA GEMM
-        // scratch: quantized rows, then the split-K partial sums the plan needs
-        // (a fixed scratch region lowers the split until they fit)
-        const size_t abytes = align256(act_bytes(vec_dot_type(t), rows, k));
-        const size_t pcap = !fx.base ? ~(size_t)0 : fx.bytes > abytes ? (fx.bytes - abytes) / sizeof(float) : 0;
-        const MmqPlan plan = mmq_plan(t, w, (int)rows, (int)n, (int)k, dev->num_cus, pcap);
-        uint8_t* base = nullptr;
-        int rc = scratch_at_least(dev, fx, abytes + plan.part_elems * sizeof(float), &base, "qmatmul");
-        if (rc) return rc;
-        ActView act;
-        rc = quantize_rows_at(dev, vec_dot_type(t), x, rows, k, nullptr, base, &act);
-        if (rc) return rc;
-        float* part = plan.part_elems ? reinterpret_cast<float*>(base + abytes) : nullptr;
-        HIP_TRY(launch_mmq(plan, t, w, act, y, part, (int)rows, (int)n, (int)k, (int)n, dev->stream));
-        return FRQ_OK;
-    }
-    if (qmv_multi_supported(t, (int)rows, (int)n, (int)k)) {
+        // many activation rows: quantize them once, then the int8-MFMA GEMM;
+        // scratch: quantized rows, then the split-K partial sums the plan
+        // needs (a fixed scratch region lowers the split until they fit)
+        p->path = QMM_TILED;
+        p->abytes = align256(act_bytes(vec_dot_type(t), rows, k));
+        const size_t pcap =
+            !fx.base ? ~(size_t)0 : fx.bytes > p->abytes ? (fx.bytes - p->abytes) / sizeof(float) : 0;
+        p->mmq = mmq_plan(t, w, (int)rows, (int)n, (int)k, dev->num_cus, pcap);
+    } else if (qmv_multi_supported(t, (int)rows, (int)n, (int)k)) {
         // a few rows of the k-quants: the mat-vec with every workgroup
         // quantizing them into LDS, each weight row reduced against all of
         // them (one weight pass per 2 or 4 rows, no quantize launch)
-        HIP_TRY(launch_qmv_multi(t, w, x, y, (int)rows, (int)n, (int)k, (int)n, dev->stream, dev->num_cus));
-        return FRQ_OK;
-    }
-    if (skinny && (rows >= 2 || k > kmax)) {
+        p->path = QMM_MULTI;
+    } else if (skinny && (rows >= 2 || k > kmax)) {
         // a few rows (and Q8_0 at any row count: it has no tiled MFMA
         // kernel): quantize them once, then one weight pass per 32-row group
-        uint8_t* base = nullptr;
-        int rc = scratch_at_least(dev, fx, act_bytes(vec_dot_type(t), rows, k), &base, "qmatmul");
-        if (rc) return rc;
-        ActView act;
-        rc = quantize_rows_at(dev, vec_dot_type(t), x, rows, k, nullptr, base, &act);
-        if (rc) return rc;
-        HIP_TRY(launch_mmq_skinny(t, w, act, y, (int)rows, (int)n, (int)k, (int)n, dev->num_cus, dev->stream));
-        return FRQ_OK;
+        p->path = QMM_SKINNY;
+        p->abytes = act_bytes(vec_dot_type(t), rows, k);
+    } else {
+        p->path = QMM_MATVEC;
     }
-    HIP_TRY(launch_qmv(t, w, x, y, (int)rows, (int)n, (int)k, (int)n, dev->stream, dev->num_cus));
     return FRQ_OK;
+}
+
+// y[rows, n] = x[rows, k] @ dequant(W[n, k])^T through the int8 path, with
+// its scratch (quantized rows, split-K partials) from `fx` when that is set.
+int run_qmatmul(frq_device* dev, int t, const uint8_t* w, const float* x, size_t rows, size_t n,
+                size_t k, float* y, const Scratch& fx = Scratch{}) {
+    if (rows == 0 || n == 0) return FRQ_OK;
+    QmmPlan plan;
+    int rc = plan_qmatmul(dev, t, w, rows, n, k, fx, &plan);
+    if (rc) return rc;
+    switch (plan.path) {
+        case QMM_TILED: {
+            uint8_t* base = nullptr;
+            rc = scratch_at_least(dev, fx, plan.abytes + plan.mmq.part_elems * sizeof(float), &base, "qmatmul");
+            if (rc) return rc;
+            ActView act;
+            rc = quantize_rows_at(dev, vec_dot_type(t), x, rows, k, nullptr, base, &act);
+            if (rc) return rc;
+            float* part = plan.mmq.part_elems ? reinterpret_cast<float*>(base + plan.abytes) : nullptr;
+            HIP_TRY(launch_mmq(plan.mmq, t, w, act, y, part, (int)rows, (int)n, (int)k, (int)n, dev->stream));
+            return FRQ_OK;
+        }
+        case QMM_MULTI:
+            HIP_TRY(launch_qmv_multi(t, w, x, y, (int)rows, (int)n, (int)k, (int)n, dev->stream, dev->num_cus));
+            return FRQ_OK;
+        case QMM_SKINNY: {
+            uint8_t* base = nullptr;
+            rc = scratch_at_least(dev, fx, plan.abytes, &base, "qmatmul");
+            if (rc) return rc;
+            ActView act;
+            rc = quantize_rows_at(dev, vec_dot_type(t), x, rows, k, nullptr, base, &act);
+            if (rc) return rc;
+            HIP_TRY(launch_mmq_skinny(t, w, act, y, (int)rows, (int)n, (int)k, (int)n, dev->num_cus, dev->stream));
+            return FRQ_OK;
+        }
+        default:
+            HIP_TRY(launch_qmv(t, w, x, y, (int)rows, (int)n, (int)k, (int)n, dev->stream, dev->num_cus));
+            return FRQ_OK;
+    }
 }
 
 // The batched paths of a fused QMatMul (rows >= 2 formed by a prologue: the
@@ -468,25 +522,30 @@ int frq_device_open(int ordinal, frq_device** out) {
 
 int frq_device_close(frq_device* dev) {
     if (!dev) return FRQ_OK;
-    (void)hipSetDevice(dev->ordinal);
-    (void)hipStreamSynchronize(dev->stream);
-    if (dev->ws) (void)hipFree(dev->ws);
-    dev->ws = nullptr;
-    dev->ws_bytes = 0;
-    if (dev->own_stream) (void)hipStreamDestroy(dev->own_stream);
-    dev->own_stream = dev->stream = nullptr;
-    (void)hipGetLastError();
+    {
+        DevGuard guard(dev);
+        (void)hipSetDevice(dev->ordinal);
+        (void)hipStreamSynchronize(dev->stream);
+        if (dev->ws) (void)hipFree(dev->ws);
+        dev->ws = nullptr;
+        dev->ws_bytes = 0;
+        if (dev->own_stream) (void)hipStreamDestroy(dev->own_stream);
+        dev->own_stream = dev->stream = nullptr;
+        (void)hipGetLastError();
+    }
     release_device(dev);  // storages still alive keep the struct until they are freed
     return FRQ_OK;
 }
 
 int frq_device_set_stream(frq_device* dev, void* s) {
     if (!dev) return fail(FRQ_INVALID, "null device");
+    DevGuard guard(dev);
     dev->stream = s ? static_cast<hipStream_t>(s) : dev->own_stream;
     return FRQ_OK;
 }
 
 int frq_sync(frq_device* dev) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     HIP_TRY(hipStreamSynchronize(dev->stream));
@@ -501,11 +560,13 @@ int frq_device_cu_count(const frq_device* dev, int* cus) {
 
 int frq_device_workspace_bytes(const frq_device* dev, size_t* bytes) {
     if (!dev || !bytes) return fail(FRQ_INVALID, "null argument");
+    DevGuard guard(const_cast<frq_device*>(dev));
     *bytes = dev->ws_bytes;
     return FRQ_OK;
 }
 
 int frq_malloc(frq_device* dev, size_t bytes, void** dptr) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (!dptr) return fail(FRQ_INVALID, "null out");
@@ -517,6 +578,7 @@ int frq_malloc(frq_device* dev, size_t bytes, void** dptr) {
 }
 
 int frq_free(frq_device* dev, void* p) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (p) HIP_TRY(hipFree(p));
@@ -524,6 +586,7 @@ int frq_free(frq_device* dev, void* p) {
 }
 
 int frq_memcpy_htod(frq_device* dev, void* dst, const void* src, size_t bytes) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (!bytes) return FRQ_OK;
@@ -533,6 +596,7 @@ int frq_memcpy_htod(frq_device* dev, void* dst, const void* src, size_t bytes) {
 }
 
 int frq_memcpy_dtoh(frq_device* dev, void* dst, const void* src, size_t bytes) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (!bytes) return FRQ_OK;
@@ -542,6 +606,7 @@ int frq_memcpy_dtoh(frq_device* dev, void* dst, const void* src, size_t bytes) {
 }
 
 int frq_memcpy_dtod(frq_device* dev, void* dst, const void* src, size_t bytes) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (!bytes) return FRQ_OK;
@@ -550,6 +615,7 @@ int frq_memcpy_dtod(frq_device* dev, void* dst, const void* src, size_t bytes) {
 }
 
 int frq_memset(frq_device* dev, void* dst, int value, size_t bytes) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (!bytes) return FRQ_OK;
@@ -577,6 +643,7 @@ static int new_storage(frq_device* dev, int t, size_t nbytes, frq_qstorage** out
 }
 
 int frq_qstorage_zeros(frq_device* dev, int t, size_t elem_count, frq_qstorage** out) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (!out) return fail(FRQ_INVALID, "null out");
@@ -593,6 +660,7 @@ int frq_qstorage_zeros(frq_device* dev, int t, size_t elem_count, frq_qstorage**
 }
 
 int frq_qstorage_load(frq_device* dev, int t, const void* host, size_t nbytes, frq_qstorage** out) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (!out) return fail(FRQ_INVALID, "null out");
@@ -642,6 +710,7 @@ int frq_qstorage_device_ptr(const frq_qstorage* q, const void** out) {
 
 static int dequant_common(const frq_qstorage* q, size_t elem_count, void* y, bool f16) {
     if (!q) return fail(FRQ_INVALID, "null storage");
+    DevGuard guard(q->dev);
     int rc = use_device(q->dev);
     if (rc) return rc;
     if (!is_weight_type(q->dtype)) return fail(FRQ_UNSUPPORTED, "dequantize: dtype %d", q->dtype);
@@ -664,6 +733,7 @@ int frq_qstorage_dequantize_f16(const frq_qstorage* q, size_t elem_count, uint16
 
 int frq_qstorage_quantize(frq_qstorage* q, const float* src, size_t elem_count) {
     if (!q) return fail(FRQ_INVALID, "null storage");
+    DevGuard guard(q->dev);
     int rc = use_device(q->dev);
     if (rc) return rc;
     if (!is_weight_type(q->dtype)) return fail(FRQ_UNSUPPORTED, "quantize: dtype %d", q->dtype);
@@ -679,6 +749,7 @@ int frq_qstorage_quantize(frq_qstorage* q, const float* src, size_t elem_count) 
 int frq_qstorage_quantize_imatrix(frq_qstorage* q, const float* src, size_t elem_count, const float* imatrix,
                                   size_t n_per_row) {
     if (!q) return fail(FRQ_INVALID, "null storage");
+    DevGuard guard(q->dev);
     int rc = use_device(q->dev);
     if (rc) return rc;
     if (q->dtype != GGML_Q4K && q->dtype != GGML_Q6K)
@@ -705,6 +776,7 @@ int frq_qstorage_quantize_imatrix(frq_qstorage* q, const float* src, size_t elem
 
 int frq_qstorage_fwd(const frq_qstorage* q, size_t n, size_t k, const float* x, size_t m, float* y) {
     if (!q) return fail(FRQ_INVALID, "null storage");
+    DevGuard guard(q->dev);
     int rc = use_device(q->dev);
     if (rc) return rc;
     if (!is_weight_type(q->dtype)) return fail(FRQ_UNSUPPORTED, "fwd: dtype %d", q->dtype);
@@ -719,6 +791,7 @@ int frq_qstorage_fwd(const frq_qstorage* q, size_t n, size_t k, const float* x, 
 
 int frq_qstorage_fwd_f16(const frq_qstorage* q, size_t n, size_t k, const uint16_t* x, size_t m, uint16_t* y) {
     if (!q) return fail(FRQ_INVALID, "null storage");
+    DevGuard guard(q->dev);
     int rc = use_device(q->dev);
     if (rc) return rc;
     if (!is_weight_type(q->dtype)) return fail(FRQ_UNSUPPORTED, "fwd_f16: dtype %d", q->dtype);
@@ -740,6 +813,7 @@ namespace {
 // the matmul with its scratch from `fx` when set.
 int qmatmul_checked(frq_device* dev, int t, size_t batch, size_t m, size_t n, size_t k, const float* act,
                     size_t act_b, const uint32_t* w, size_t w_b, float* out, size_t out_b, const Scratch& fx) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (!is_weight_type(t)) return fail(FRQ_UNSUPPORTED, "qmatmul: unsupported quant_type %d", t);
@@ -780,9 +854,31 @@ int frq_qmatmul_noalloc(frq_device* dev, int t, size_t batch, size_t m, size_t n
     return qmatmul_checked(dev, t, batch, m, n, k, act, act_b, w, w_b, out, out_b, fx);
 }
 
+int frq_qmatmul_plan(frq_device* dev, int t, size_t rows, size_t n, size_t k, const void* w, int noalloc, int* path,
+                     int* kind, int* ksplit) {
+    DevGuard guard(dev);
+    int rc = use_device(dev);
+    if (rc) return rc;
+    if (!path || !kind || !ksplit) return fail(FRQ_INVALID, "qmatmul_plan: null output");
+    if (!is_weight_type(t)) return fail(FRQ_UNSUPPORTED, "qmatmul_plan: unsupported quant_type %d", t);
+    if (k % block_elems(t)) return fail(FRQ_INVALID, "qmatmul_plan: k=%zu must be a multiple of %zu", k, block_elems(t));
+    Scratch fx;
+    if (noalloc) {
+        fx.base = static_cast<uint8_t*>(dev->scratch);
+        fx.bytes = FRQ_NOALLOC_SCRATCH_BYTES;
+    }
+    QmmPlan p;
+    if ((rc = plan_qmatmul(dev, t, static_cast<const uint8_t*>(w), rows, n, k, fx, &p))) return rc;
+    *path = p.path;
+    *kind = p.path == QMM_TILED ? p.mmq.kind : -1;
+    *ksplit = p.path == QMM_TILED ? (p.mmq.ks > 1 ? p.mmq.ks : 1) : 1;
+    return FRQ_OK;
+}
+
 // ---- taps ----
 
 int frq_quantize_q8k(frq_device* dev, const float* x, size_t rows, size_t k, void* blocks) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (k % QK_K) return fail(FRQ_INVALID, "quantize_q8k: k=%zu not a multiple of 256", k);
@@ -792,6 +888,7 @@ int frq_quantize_q8k(frq_device* dev, const float* x, size_t rows, size_t k, voi
 }
 
 int frq_quantize_q8_0(frq_device* dev, const float* x, size_t rows, size_t k, void* blocks) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (k % QK8_0) return fail(FRQ_INVALID, "quantize_q8_0: k=%zu not a multiple of 32", k);
@@ -802,6 +899,7 @@ int frq_quantize_q8_0(frq_device* dev, const float* x, size_t rows, size_t k, vo
 
 int frq_block_isums(frq_device* dev, int t, size_t m, size_t n, size_t k, const void* w,
                     const float* x, int32_t* isum, int32_t* msum) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (!is_weight_type(t)) return fail(FRQ_UNSUPPORTED, "block_isums: dtype %d", t);
@@ -819,6 +917,7 @@ int frq_block_isums(frq_device* dev, int t, size_t m, size_t n, size_t k, const 
 
 int frq_moe_route(frq_device* dev, const float* logits, size_t t, size_t e, size_t topk, int32_t* ids, float* w,
                   int32_t* offsets, int32_t* sorted_token, int32_t* sorted_slot) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if ((rc = check_moe_dims("moe_route", e, topk))) return rc;
@@ -839,6 +938,7 @@ int frq_moe_route(frq_device* dev, const float* logits, size_t t, size_t e, size
 int frq_indexed_moe_forward(const frq_qstorage* q, size_t e, size_t n, size_t k, const float* x, size_t t,
                             size_t x_slots, const int32_t* ids, size_t topk, float* y) {
     if (!q) return fail(FRQ_INVALID, "null storage");
+    DevGuard guard(q->dev);
     int rc = use_device(q->dev);
     if (rc) return rc;
     const int dt = q->dtype;
@@ -871,6 +971,7 @@ int frq_indexed_moe_forward(const frq_qstorage* q, size_t e, size_t n, size_t k,
 
 int frq_moe_ffn(frq_device* dev, int dt, size_t t, size_t d, size_t ffn, size_t e, size_t topk, const float* x,
                 const float* logits, const void* w_gate, const void* w_up, const void* w_down, float* out) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (!is_weight_type(dt)) return fail(FRQ_UNSUPPORTED, "moe_ffn: dtype %d", dt);
@@ -1007,6 +1108,7 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 int frq_qmatmul_fused(frq_device* dev, int dt, size_t m, size_t n, size_t k, const void* w, const float* x, size_t ldx,
                       const float* x2, const float* gain, float eps, int accumulate, float* y, size_t ldy) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (!is_weight_type(dt)) return fail(FRQ_UNSUPPORTED, "qmatmul_fused: dtype %d", dt);
@@ -1046,6 +1148,7 @@ int frq_qmatmul_fused(frq_device* dev, int dt, size_t m, size_t n, size_t k, con
 int frq_qmatmul_fused_pair(frq_device* dev, size_t m, size_t k, const float* x, size_t ldx, const float* gain,
                            float eps, int dt1, size_t n1, const void* w1, float* y1, int dt2, size_t n2, const void* w2,
                            float* y2) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (!qmv_pair_supported(dt1, dt2, (int)(k > 0x7fffffff ? 0 : k)) || k == 0)
@@ -1090,6 +1193,7 @@ size_t frq_attention_decode_workspace(size_t n_heads, size_t max_ctx) {
 int frq_attention_decode(frq_device* dev, size_t n_heads, size_t head_dim, size_t max_ctx, const float* qk,
                          const float* v, const float* rcos, const float* rsin, uint16_t* kc, uint16_t* vc,
                          const int32_t* pos, float scale, void* work, size_t work_bytes, float* out) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (head_dim != (size_t)ATTN_HEAD_DIM)
@@ -1108,6 +1212,7 @@ int frq_attention_decode(frq_device* dev, size_t n_heads, size_t head_dim, size_
 
 int frq_qmatmul_fused_glu(frq_device* dev, int dt, size_t m, size_t n, size_t k, const void* w_gate, const void* w_up,
                           const float* x, size_t ldx, const float* gain, float eps, float* y, size_t ldy) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (!is_weight_type(dt)) return fail(FRQ_UNSUPPORTED, "qmatmul_fused_glu: dtype %d", dt);
@@ -1137,6 +1242,7 @@ int frq_attention_decode_oproj(frq_device* dev, size_t n_heads, size_t head_dim,
                                const float* v, const float* rcos, const float* rsin, uint16_t* kc, uint16_t* vc,
                                const int32_t* pos, float scale, void* work, size_t work_bytes, int o_dtype,
                                const void* w_o, size_t n_out, float* y) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (head_dim != (size_t)ATTN_HEAD_DIM)
@@ -1183,6 +1289,7 @@ int frq_attention_decode_oproj(frq_device* dev, size_t n_heads, size_t head_dim,
 
 int frq_rms_norm_rows(frq_device* dev, size_t m, size_t k, const float* x, size_t ldx, const float* gain, float eps,
                       float* y, size_t ldy) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (m > 0x7fffffff || k == 0 || k > 0x7fffffff || ldx < k || ldy < k || ldx > 0x7fffffff || ldy > 0x7fffffff)
@@ -1196,6 +1303,7 @@ int frq_rms_norm_rows(frq_device* dev, size_t m, size_t k, const float* x, size_
 int frq_rope_append_rows(frq_device* dev, size_t m, size_t n_heads, size_t head_dim, size_t max_ctx, float* qk,
                          size_t ldqk, const float* v, size_t ldv, const float* rcos, const float* rsin, size_t pos0,
                          uint16_t* kc, uint16_t* vc) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (head_dim != (size_t)ATTN_HEAD_DIM)
@@ -1217,6 +1325,7 @@ int frq_rope_append_rows(frq_device* dev, size_t m, size_t n_heads, size_t head_
 int frq_attention_prefill(frq_device* dev, size_t m, size_t n_heads, size_t head_dim, size_t max_ctx, const float* q,
                           size_t ldq, const uint16_t* kc, const uint16_t* vc, size_t pos0, float scale, float* out,
                           size_t ldo) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (head_dim != (size_t)ATTN_HEAD_DIM)
@@ -1236,6 +1345,7 @@ int frq_attention_prefill(frq_device* dev, size_t m, size_t n_heads, size_t head
 }
 
 int frq_swiglu_rows(frq_device* dev, size_t m, size_t f, const float* gu, size_t ldgu, float* h, size_t ldh) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (m > 65535 || f == 0 || f > 0x7fffffff || ldgu < 2 * f || ldh < f || ldgu > 0x7fffffff || ldh > 0x7fffffff)
@@ -1247,6 +1357,7 @@ int frq_swiglu_rows(frq_device* dev, size_t m, size_t f, const float* gu, size_t
 }
 
 int frq_add(frq_device* dev, size_t n, const float* x, float* y) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (n == 0) return FRQ_OK;
@@ -1258,6 +1369,7 @@ int frq_add(frq_device* dev, size_t n, const float* x, float* y) {
 
 int frq_gather_rows(frq_device* dev, const float* table, size_t rows, size_t dim, const int32_t* ids, size_t m,
                     float* out) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (rows == 0 || rows > 0x7fffffff || dim == 0 || dim > 0x7fffffff || m > 65535)
@@ -1270,6 +1382,7 @@ int frq_gather_rows(frq_device* dev, const float* table, size_t rows, size_t dim
 
 int frq_argmax_embed(frq_device* dev, const float* logits, size_t vocab, const float* table, size_t dim, int32_t* tokens,
                      size_t tokens_cap, const int32_t* prompt_len, int32_t* pos, float* x) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (vocab == 0 || vocab > (size_t)0x7fffffff || dim == 0 || dim % 4 || tokens_cap > (size_t)0x7fffffff)
@@ -1283,6 +1396,7 @@ int frq_argmax_embed(frq_device* dev, const float* logits, size_t vocab, const f
 
 int frq_fill_random_bits(frq_device* dev, uint32_t* y, size_t n, uint64_t start, uint64_t seed, uint32_t base,
                          uint32_t stream) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (n && !y) return fail(FRQ_INVALID, "null output");
@@ -1291,6 +1405,7 @@ int frq_fill_random_bits(frq_device* dev, uint32_t* y, size_t n, uint64_t start,
 }
 
 int frq_fill_normal(frq_device* dev, float* y, size_t n, uint64_t seed, uint32_t stream, float mean, float stdv) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (n && !y) return fail(FRQ_INVALID, "null output");
@@ -1301,6 +1416,7 @@ int frq_fill_normal(frq_device* dev, float* y, size_t n, uint64_t seed, uint32_t
 
 int frq_probe_read(frq_device* dev, const void* src, size_t bytes, int wg_per_cu, int unroll, int nontemporal,
                    uint32_t* sink) {
+    DevGuard guard(dev);
     int rc = use_device(dev);
     if (rc) return rc;
     if (!src || !sink) return fail(FRQ_INVALID, "probe_read: null buffer");

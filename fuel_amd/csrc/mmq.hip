@@ -1094,15 +1094,18 @@ hipError_t launch_wide(const uint8_t* w, ActView act, float* y, int M, int N, in
     return hipGetLastError();
 }
 
-// Resident workgroups per CU of a kernel instantiation (cached per instantiation).
-template <class Kern>
-int kernel_occupancy(Kern kern, int threads) {
-    static int occ = -1;
-    if (occ < 0) {
+// Resident workgroups per CU of one kernel instantiation at `Threads` threads
+// per workgroup.  The template parameter is the kernel itself, so every
+// instantiation has its own cache (kernels of one signature do not share it):
+// a plan is a function of its call alone, never of which kernels were planned
+// before in the process.  The first query initialises the static (thread-safe).
+template <auto Kern, int Threads>
+int kernel_occupancy() {
+    static const int occ = [] {
         int o = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, kern, threads, 0) != hipSuccess || o < 1) o = 1;
-        occ = o;
-    }
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, Kern, Threads, 0) != hipSuccess || o < 1) o = 1;
+        return o;
+    }();
     return occ;
 }
 
@@ -1124,8 +1127,8 @@ void plan_cfg(int M, int N, int K, int num_cus, MmqPlan& p) {
     constexpr int NT = 64 * WM * WN, BM = 16 * RT * WM, BN = 16 * CT * WN;
     const int mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
     int occ;
-    if constexpr (DMA) occ = kernel_occupancy(mmq_dma_kernel<F, RT, CT, WM, WN, false>, NT);
-    else occ = kernel_occupancy(mmq_kernel<F, RT, CT, WM, WN, false>, NT);
+    if constexpr (DMA) occ = kernel_occupancy<mmq_dma_kernel<F, RT, CT, WM, WN, false>, NT>();
+    else occ = kernel_occupancy<mmq_kernel<F, RT, CT, WM, WN, false>, NT>();
     p.ks = mmq_ksplit(mt * nt, occ, num_cus, K / QK_K);
     p.part_elems = p.ks > 1 ? (size_t)p.ks * M * N : 0;
 }
@@ -1239,7 +1242,7 @@ MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus, siz
         p.ks = 1;
         if (wide_split) {
             const int tiles = ((M + T::BM - 1) / T::BM) * ((N + T::BN - 1) / T::BN);
-            const int occ = kernel_occupancy(mmq_q4k_wide_kernel<4, 1, 8>, T::NT);
+            const int occ = kernel_occupancy<mmq_q4k_wide_kernel<4, 1, 8>, T::NT>();
             p.ks = mmq_ksplit(tiles, occ, num_cus, K / QK_K);
             while (p.ks > 1 && (size_t)p.ks * M * N > max_part_elems) p.ks--;
         }

@@ -14,6 +14,8 @@
 //             ascending order, product then sum).
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include "attn.hpp"
 #include "common.hpp"
 #include "formats.hpp"
@@ -507,14 +509,22 @@ bool dc_shape(int dtype, int topk, int ffn, DcShape& sh) {
 template <class F, int SEG, int NPASS, int MAXQ>
 hipError_t launch_dc(const DcShape& sh, const uint8_t* w, size_t eb, int E, const float* gu, const int* ids,
                      const float* wts, int T, int topk, int ffn, int d, float* out, hipStream_t s, int num_cus) {
-    static int occ = -1;
-    if (occ < 0) {
+    // resident workgroups per CU at this launch's dynamic LDS size, cached per
+    // instantiation and LDS size (lds << 16 | occupancy; the grid only spreads
+    // whole output rows over workgroups, so it never changes a result)
+    static std::atomic<long long> cached{-1};
+    long long c = cached.load(std::memory_order_relaxed);
+    int occ;
+    if (c >= 0 && (c >> 16) == (long long)sh.lds) {
+        occ = (int)(c & 0xffff);
+    } else {
         int o = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, moe_down_combine_kernel<F, SEG, NPASS, MAXQ>, 64 * DC_NW,
                                                          sh.lds) != hipSuccess ||
             o < 1)
             o = 1;
-        occ = o;
+        occ = o > 0xffff ? 0xffff : o;
+        cached.store(((long long)sh.lds << 16) | occ, std::memory_order_relaxed);
     }
     const int need = (d + DC_NW - 1) / DC_NW;
     int cap = num_cus * occ / T;

@@ -18,8 +18,14 @@
  *       5801; fuel-dispatch/src/kernel.rs:168-173, 482-488): frq_qmatmul.
  *
  * Work is enqueued on the device's stream and is asynchronous unless stated;
- * frq_sync waits for it.  Calls on one device handle must not overlap from
- * several threads (the handle owns one activation workspace).
+ * frq_sync waits for it.  Thread safety (the trait seam is Send + Sync,
+ * fuel-backend-contract/src/quantized.rs:29): every entry point that enqueues
+ * work on a device, or touches its stream or workspace, holds that device
+ * handle's lock, so calls from several threads on one handle, or on storages
+ * of one handle, take turns on the host and their work runs in call order on
+ * the handle's one stream.  A call's results do not depend on which calls
+ * came before it in the process (frq_qmatmul_plan reports the kernels a
+ * QMatMul runs; they follow from the call alone).
  */
 #ifndef FUEL_ROCM_H
 #define FUEL_ROCM_H
@@ -147,15 +153,21 @@ int frq_qmatmul(frq_device *dev, int quant_type, size_t batch, size_t m, size_t 
                 float *out_dev, size_t out_bytes);
 /* frq_qmatmul without any device allocation.  No counterpart in the
  * reference: for callers that cannot allocate (code under HIP graph capture,
- * tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
- * checks and results as frq_qmatmul; the quantized activation rows and the
- * split-K partial sums live in a fixed 32 MiB device array per GPU instead
- * of the handle's growable workspace (the K split is lowered until the
- * partials fit).  A call whose quantized rows need more (about 1.14 * rows *
- * k bytes for the k-quants, 1.125 * rows * k for Q8_0) fails with status 4
- * (workspace).  Calls share that array: calls that overlap on one GPU (two
- * streams, two threads) race, as does one that overlaps an frq_qmatmul_noalloc
- * on another handle of the same GPU. */
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments
+ * and checks as frq_qmatmul; the quantized activation rows and the split-K
+ * partial sums live in a fixed 32 MiB device array per GPU instead of the
+ * handle's growable workspace.  Results are bit-identical to frq_qmatmul's
+ * when the plan's split-K partials fit beside the quantized rows; when they
+ * do not, the K split is lowered until they fit (for 128 or more rows of
+ * 16-byte aligned Q4_K blocks that can also select the wide-tile kernel), so
+ * the f32 sums are added in another order and the results agree with
+ * frq_qmatmul's within the path's tolerance (1e-3 of the output norm), not
+ * in bits; frq_qmatmul_plan with noalloc = 1 reports the plan taken.  A call
+ * whose quantized rows need more (about 1.14 * rows * k bytes for the
+ * k-quants, 1.125 * rows * k for Q8_0) fails with status 4 (workspace).
+ * Calls share that array: calls on one handle take turns (the handle's
+ * lock), but calls that overlap on one GPU through two handles, or on two
+ * streams, race. */
 int frq_qmatmul_noalloc(frq_device *dev, int quant_type, size_t batch, size_t m, size_t n, size_t k,
                         const float *act_dev, size_t act_bytes, const uint32_t *w_dev, size_t w_bytes,
                         float *out_dev, size_t out_bytes);
@@ -325,6 +337,19 @@ int frq_argmax_embed(frq_device *dev, const float *logits_dev, size_t vocab, con
  * :629-658), written in the reference byte layout [rows, k/blk] blocks. */
 int frq_quantize_q8k(frq_device *dev, const float *x_dev, size_t rows, size_t k, void *blocks_dev);
 int frq_quantize_q8_0(frq_device *dev, const float *x_dev, size_t rows, size_t k, void *blocks_dev);
+/* The kernels frq_qmatmul (noalloc = 0) or frq_qmatmul_noalloc (noalloc = 1)
+ * runs for `rows` activation rows of an [n, k] weight of quant_type whose
+ * blocks start at w_dev (only its 16-byte alignment matters): *path is 0
+ * (the fused quantize + mat-vec, one row), 1 (the mat-vec over 2-4 rows
+ * quantized in LDS), 2 (the few-row int8-MFMA kernel) or 3 (the tiled
+ * int8-MFMA GEMM); for path 3 *kind is the tile kernel and *ksplit the number
+ * of K splits summed in split order, else -1 and 1.  Build-internal tap with
+ * no counterpart in the reference: the plan (and so the f32 summation order)
+ * is a function of these arguments and the device's CU count alone, which
+ * the reference's bit_stable_on_same_hardware (fuel-dispatch/src/fused.rs:
+ * 1319-1330) requires. */
+int frq_qmatmul_plan(frq_device *dev, int quant_type, size_t rows, size_t n, size_t k, const void *w_dev,
+                     int noalloc, int *path, int *kind, int *ksplit);
 /* Per-(row m, weight row n, block b) integer sums of the block dot product
  * (vec_dot_unopt's integer stage): isum/msum [m, n, k/blk] int32.  The
  * activations are quantized on the device from x_dev first. */

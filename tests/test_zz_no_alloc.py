@@ -63,3 +63,44 @@ def test_noalloc_refuses_beyond_its_scratch(ndev):
     assert rc == 4, rc
     assert b"scratch" in L.frq_last_error()
     assert np.all(out.numpy() == 7.0)
+
+
+# shapes whose split-K partials, in frq_qmatmul's plan, do not fit the fixed
+# array beside the quantized rows (Q6_K at 512 rows of K = 32768: 19 MB of
+# rows plus two 8 MB partial sets); the planner says which of them bind
+CAP_CANDIDATES = [(O.Q6K, 512, 4096, 32768), (O.Q6K, 256, 8192, 32768), (O.Q4K, 512, 4096, 32768),
+                  (O.Q6K, 384, 8192, 16384)]
+
+
+def test_noalloc_lowered_split_within_tolerance(ndev):
+    """When the plan's partials do not fit, frq_qmatmul_noalloc lowers the K
+    split (frq_qmatmul_plan with noalloc = 1 shows it): the f32 sums are then
+    added in another order, so the outputs agree with frq_qmatmul's within the
+    path's tolerance (1e-3 of the output norm) rather than in bits."""
+    L = lib()
+    bound = 0
+    for dt, m, n, k in CAP_CANDIDATES:
+        wf = F.fill_normal(ndev, (n, k), seed=5, stream=n, std=0.02)
+        q = ndev.qzeros(n * k, dt)
+        q.quantize(wf)
+        del wf
+        reg = F.qmatmul_plan(ndev, dt, m, n, k, q.device_ptr())
+        fixed = F.qmatmul_plan(ndev, dt, m, n, k, q.device_ptr(), noalloc=True)
+        say("noalloc cap", dt, m, n, k, "plans", reg, fixed)
+        if fixed == reg:
+            continue
+        assert fixed[0] == reg[0] == "tiled_mfma" and fixed[2] < reg[2]
+        bound += 1
+        xd = F.fill_normal(ndev, (m, k), seed=6, stream=m)
+        nb = n * (k // 256) * O.TYPE_SIZE[dt]
+        want = ndev.alloc((m, n), np.float32)
+        got = ndev.alloc((m, n), np.float32)
+        for fn, out in ((L.frq_qmatmul, want), (L.frq_qmatmul_noalloc, got)):
+            F._native.check(fn(ndev.handle, dt, 1, m, n, k, C.c_void_p(xd.ptr), xd.nbytes, C.c_void_p(q.device_ptr()),
+                               nb, C.c_void_p(out.ptr), out.nbytes))
+        ndev.synchronize()
+        a, b = got.numpy(), want.numpy()
+        err = float(np.abs(a - b).max() / np.linalg.norm(b))
+        say("  rel diff", err)
+        assert np.all(np.isfinite(a)) and err <= 1e-3
+    assert bound >= 1, "no candidate shape binds the fixed scratch"
