@@ -66,10 +66,11 @@ def test_noalloc_refuses_beyond_its_scratch(ndev):
 
 
 # shapes whose split-K partials, in frq_qmatmul's plan, do not fit the fixed
-# array beside the quantized rows (Q6_K at 512 rows of K = 32768: 19 MB of
-# rows plus two 8 MB partial sets); the planner says which of them bind
-CAP_CANDIDATES = [(O.Q6K, 512, 4096, 32768), (O.Q6K, 256, 8192, 32768), (O.Q4K, 512, 4096, 32768),
-                  (O.Q6K, 384, 8192, 16384)]
+# array beside the quantized rows: one row tile of very long rows (Q6_K at 128
+# rows of K = 131072: 19 MB of quantized rows plus 8 splits of 2 MB partials;
+# Q4_K wide tiles at 256 rows of K = 98304: 29 MB of rows plus 2-4 splits of
+# 4 MB); the planner says which of them bind on this GPU
+CAP_CANDIDATES = [(O.Q6K, 128, 4096, 131072), (O.Q4K, 256, 4096, 98304)]
 
 
 def test_noalloc_lowered_split_within_tolerance(ndev):
