@@ -718,6 +718,48 @@ def cpu_leg(target_s: float):
     }
 
 
+def cpu_config1_leg(target_s: float):
+    """BASELINE config 1 on fuel's CPU path itself: matmul<BlockQ8_0> (the
+    oracle restatement with the AVX2 vec_dot_q8_0_q8_0, avx.rs:72-88) of
+    x [1, 4096] ~ N(0, 1) against W [4096, 4096] ~ N(0, 0.02) quantized by
+    BlockQ8_0::from_float, on the host cores; median of repeated calls, the
+    weights rotated over enough copies to exceed twice the host's last-level
+    cache."""
+    import oracle as O
+
+    threads = int(os.environ.get("RAYON_NUM_THREADS") or os.environ.get("OMP_NUM_THREADS") or 0)
+    if threads <= 0:
+        threads = len(os.sched_getaffinity(0))
+    k = n = 4096
+    nbytes = algo_bytes(k, n, 34, 32)
+    llc = host_llc_bytes()
+    copies = min(16, max(CPU_COPIES, math.ceil(2 * llc / nbytes)))
+    w = O.quantize(O.Q8_0, O.normal((n, k), SEED, 300, std=0.02))
+    ws = [w] + [w.copy() for _ in range(copies - 1)]
+    x = O.normal((1, k), SEED, 301)
+    O.matmul(O.Q8_0, x, ws[0], avx2=True, threads=threads)
+    times = []
+    t_end = time.time() + target_s
+    i = 0
+    while time.time() < t_end or len(times) < 3:
+        t = time.perf_counter()
+        O.matmul(O.Q8_0, x, ws[i % copies], avx2=True, threads=threads)
+        times.append(time.perf_counter() - t)
+        i += 1
+    med = float(np.median(times))
+    return {
+        "value": round(nbytes / med / 1e9, 2),
+        "unit": "GB/s",
+        "us": round(med * 1e6, 2),
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{len(times)} calls of the Q8_0 [1,4096] x [4096,4096] QMatMul ({nbytes / 1e6:.2f} MB each, "
+                  f"weights rotated over {copies} copies), median {med * 1e6:.1f} us; oracle matmul<BlockQ8_0> "
+                  f"with the AVX2 vec_dot_q8_0_q8_0, {threads} OpenMP threads; "
+                  f"avx2={'yes' if O.have_avx2() else 'no (scalar)'}",
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -838,6 +880,10 @@ def main() -> int:
         c1_bytes = algo_bytes(4096, 4096, 34, 32)
         out["config1_q8_0_4096x4096"] = {"us": c1["us"], "GB_s": round(c1_bytes / c1["us"] / 1e3, 1),
                                          "hbm_frac": round(c1_bytes / c1["us"] / 1e3 / HBM_PEAK_GBS, 4)}
+        if not args.no_cpu:  # the same QMatMul on fuel's CPU path, on the host cores
+            c1cpu = cpu_config1_leg(min(3.0, args.cpu_seconds))
+            out["config1_q8_0_4096x4096"]["cpu_baseline"] = c1cpu
+            out["config1_q8_0_4096x4096"]["gpu_over_cpu"] = round(c1cpu["us"] / c1["us"], 1)
         say(f"[bench] config 1 {out['config1_q8_0_4096x4096']}")
     if not args.no_moe:
         out["moe"] = moe_leg()

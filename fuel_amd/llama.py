@@ -349,58 +349,69 @@ class LlamaDecoder:
         `parts` (a subset of STEP_PARTS) enqueues only those launches, for
         per-kernel timing; None enqueues the whole step."""
         cfg, L, h = self.cfg, self.L, self.dev.handle
-        d, f, eps = cfg.dim, cfg.ffn, cfg.eps
+        d, eps = cfg.dim, cfg.eps
         vp = C.c_void_p
         x = vp(self.x.ptr)
         on = (lambda p: True) if parts is None else (lambda p: p in parts)
-        for li, lw in enumerate(self.layers):
-            ag, fg = vp(self.attn_gain[li].ptr), vp(self.ffn_gain[li].ptr)
-            if not on("qkv"):
-                pass
-            elif self._pair(lw):
-                check(L.frq_qmatmul_fused_pair(h, 1, d, x, d, ag, eps, lw["dt_qk"], 2 * d, vp(lw["wqk"].ptr),
-                                               vp(self.qk.ptr), lw["dt_v"], d, vp(lw["wv"].ptr), vp(self.v.ptr)))
-            else:
-                check(L.frq_qmatmul_fused(h, lw["dt_qk"], 1, 2 * d, d, vp(lw["wqk"].ptr), x, d, None, ag, eps, 0,
-                                          vp(self.qk.ptr), 2 * d))
-                check(L.frq_qmatmul_fused(h, lw["dt_v"], 1, d, d, vp(lw["wv"].ptr), x, d, None, ag, eps, 0,
-                                          vp(self.v.ptr), d))
-            if not on("attention"):
-                pass
-            elif self.fuse_oproj:
-                check(L.frq_attention_decode_oproj(h, cfg.n_heads, cfg.head_dim, cfg.max_ctx, vp(self.qk.ptr),
-                                                   vp(self.v.ptr), vp(self.rcos.ptr), vp(self.rsin.ptr),
-                                                   vp(self.kc[li].ptr), vp(self.vc[li].ptr), vp(self.pos.ptr),
-                                                   self.scale, vp(self.work.ptr), self.work_bytes, lw["dt_o"],
-                                                   vp(lw["wo"].ptr), d, x))
-            else:
-                check(L.frq_attention_decode(h, cfg.n_heads, cfg.head_dim, cfg.max_ctx, vp(self.qk.ptr),
-                                             vp(self.v.ptr), vp(self.rcos.ptr), vp(self.rsin.ptr),
-                                             vp(self.kc[li].ptr), vp(self.vc[li].ptr), vp(self.pos.ptr), self.scale,
-                                             vp(self.work.ptr), self.work_bytes, vp(self.att.ptr)))
-                check(L.frq_qmatmul_fused(h, lw["dt_o"], 1, d, d, vp(lw["wo"].ptr), vp(self.att.ptr), d, None, None,
-                                          0.0, 1, x, d))
-            if self.fuse_glu:
-                up = lw["wgu"].ptr + f * (d // (32 if lw["dt_gu"] == N.Q8_0 else 256)) * N_TYPE_SIZE[lw["dt_gu"]]
-                if on("gate_up"):
-                    check(L.frq_qmatmul_fused_glu(h, lw["dt_gu"], 1, f, d, vp(lw["wgu"].ptr), vp(up), x, d, fg, eps,
-                                                  vp(self.gu.ptr), f))
-                if on("down"):
-                    check(L.frq_qmatmul_fused(h, lw["dt_down"], 1, d, f, vp(lw["wd"].ptr), vp(self.gu.ptr), f, None,
-                                              None, 0.0, 1, x, d))
-            else:
-                if on("gate_up"):
-                    check(L.frq_qmatmul_fused(h, lw["dt_gu"], 1, 2 * f, d, vp(lw["wgu"].ptr), x, d, None, fg, eps, 0,
-                                              vp(self.gu.ptr), 2 * f))
-                if on("down"):
-                    check(L.frq_qmatmul_fused(h, lw["dt_down"], 1, d, f, vp(lw["wd"].ptr), vp(self.gu.ptr), f,
-                                              vp(self.gu.ptr + 4 * f), None, 0.0, 1, x, d))
+        for li in range(len(self.layers)):
+            self.enqueue_layer(li, parts)
         if on("logits"):
             check(L.frq_qmatmul_fused(h, self.dt_out, 1, cfg.vocab, d, vp(self.wout.ptr), x, d, None,
                                       vp(self.final_gain.ptr), eps, 0, vp(self.logits.ptr), cfg.vocab))
         if on("argmax"):
             check(L.frq_argmax_embed(h, vp(self.logits.ptr), cfg.vocab, vp(self.embed.ptr), d, vp(self.tokens.ptr),
                                      cfg.max_ctx, vp(self.plen.ptr), vp(self.pos.ptr), x))
+
+    def enqueue_layer(self, li: int, parts=None) -> None:
+        """Layer li of the step (lazy.rs:7363-7440) on the residual x at
+        position pos: its five (or six) launches, `parts` as in enqueue_step."""
+        cfg, L, h = self.cfg, self.L, self.dev.handle
+        d, f, eps = cfg.dim, cfg.ffn, cfg.eps
+        vp = C.c_void_p
+        x = vp(self.x.ptr)
+        on = (lambda p: True) if parts is None else (lambda p: p in parts)
+        lw = self.layers[li]
+        ag, fg = vp(self.attn_gain[li].ptr), vp(self.ffn_gain[li].ptr)
+        if not on("qkv"):
+            pass
+        elif self._pair(lw):
+            check(L.frq_qmatmul_fused_pair(h, 1, d, x, d, ag, eps, lw["dt_qk"], 2 * d, vp(lw["wqk"].ptr),
+                                           vp(self.qk.ptr), lw["dt_v"], d, vp(lw["wv"].ptr), vp(self.v.ptr)))
+        else:
+            check(L.frq_qmatmul_fused(h, lw["dt_qk"], 1, 2 * d, d, vp(lw["wqk"].ptr), x, d, None, ag, eps, 0,
+                                      vp(self.qk.ptr), 2 * d))
+            check(L.frq_qmatmul_fused(h, lw["dt_v"], 1, d, d, vp(lw["wv"].ptr), x, d, None, ag, eps, 0,
+                                      vp(self.v.ptr), d))
+        if not on("attention"):
+            pass
+        elif self.fuse_oproj:
+            check(L.frq_attention_decode_oproj(h, cfg.n_heads, cfg.head_dim, cfg.max_ctx, vp(self.qk.ptr),
+                                               vp(self.v.ptr), vp(self.rcos.ptr), vp(self.rsin.ptr),
+                                               vp(self.kc[li].ptr), vp(self.vc[li].ptr), vp(self.pos.ptr),
+                                               self.scale, vp(self.work.ptr), self.work_bytes, lw["dt_o"],
+                                               vp(lw["wo"].ptr), d, x))
+        else:
+            check(L.frq_attention_decode(h, cfg.n_heads, cfg.head_dim, cfg.max_ctx, vp(self.qk.ptr),
+                                         vp(self.v.ptr), vp(self.rcos.ptr), vp(self.rsin.ptr),
+                                         vp(self.kc[li].ptr), vp(self.vc[li].ptr), vp(self.pos.ptr), self.scale,
+                                         vp(self.work.ptr), self.work_bytes, vp(self.att.ptr)))
+            check(L.frq_qmatmul_fused(h, lw["dt_o"], 1, d, d, vp(lw["wo"].ptr), vp(self.att.ptr), d, None, None,
+                                      0.0, 1, x, d))
+        if self.fuse_glu:
+            up = lw["wgu"].ptr + f * (d // (32 if lw["dt_gu"] == N.Q8_0 else 256)) * N_TYPE_SIZE[lw["dt_gu"]]
+            if on("gate_up"):
+                check(L.frq_qmatmul_fused_glu(h, lw["dt_gu"], 1, f, d, vp(lw["wgu"].ptr), vp(up), x, d, fg, eps,
+                                              vp(self.gu.ptr), f))
+            if on("down"):
+                check(L.frq_qmatmul_fused(h, lw["dt_down"], 1, d, f, vp(lw["wd"].ptr), vp(self.gu.ptr), f, None,
+                                          None, 0.0, 1, x, d))
+        else:
+            if on("gate_up"):
+                check(L.frq_qmatmul_fused(h, lw["dt_gu"], 1, 2 * f, d, vp(lw["wgu"].ptr), x, d, None, fg, eps, 0,
+                                          vp(self.gu.ptr), 2 * f))
+            if on("down"):
+                check(L.frq_qmatmul_fused(h, lw["dt_down"], 1, d, f, vp(lw["wd"].ptr), vp(self.gu.ptr), f,
+                                          vp(self.gu.ptr + 4 * f), None, 0.0, 1, x, d))
 
     def prefill(self, prompt) -> None:
         """The prompt as one batch (lazy.rs:7363-7446 at seq = M): every layer

@@ -72,31 +72,41 @@ class OracleLlama:
     def _mm(self, dt, x, w):
         return matmul(dt, x[None], w, avx2=True, threads=self.threads)[0]
 
-    def step(self, token: int, pos: int) -> np.ndarray:
-        """Logits [vocab] of `token` at position `pos` (the cache holds 0..pos-1)."""
+    def layer(self, li: int, x: np.ndarray, pos: int) -> np.ndarray:
+        """apply_layer li (lazy.rs:7363-7440) on the residual x [dim] of the
+        token at `pos`: appends its k, v to cache row pos, returns the new x."""
         cfg = self.cfg
         H, D = cfg.n_heads, cfg.head_dim
-        x = self.w["embed"][token].astype(np.float32).copy()
+        lw = self.w["layers"][li]
         cs, sn = self.cos[pos:pos + 1], self.sin[pos:pos + 1]
-        for li, lw in enumerate(self.w["layers"]):
-            dts = layer_dtypes(cfg, li)
-            xn = rms_norm(x, lw["attn_gain"], cfg.eps)
-            q = self._mm(dts["wq"], xn, lw["wq"])
-            k = self._mm(dts["wk"], xn, lw["wk"])
-            v = self._mm(dts["wv"], xn, lw["wv"])
-            q = rope(q.reshape(H, 1, D), cs, sn).reshape(H, D)
-            k = rope(k.reshape(H, 1, D), cs, sn).reshape(H, D)
-            self.kc[li, :, pos] = k.astype(np.float16).astype(np.float32)
-            self.vc[li, :, pos] = v.reshape(H, D).astype(np.float16).astype(np.float32)
-            a = attention_decode(q, self.kc[li], self.vc[li], pos + 1, float(self.scale)).reshape(-1)
-            x = (x + self._mm(dts["wo"], a, lw["wo"])).astype(np.float32)
-            xn = rms_norm(x, lw["ffn_gain"], cfg.eps)
-            g = self._mm(dts["wg"], xn, lw["wg"])
-            u = self._mm(dts["wu"], xn, lw["wu"])
-            h = (g / (np.float32(1.0) + np.exp(-g)) * u).astype(np.float32)
-            x = (x + self._mm(dts["wd"], h, lw["wd"])).astype(np.float32)
-        xn = rms_norm(x, self.w["final_gain"], cfg.eps)
+        dts = layer_dtypes(cfg, li)
+        xn = rms_norm(x, lw["attn_gain"], cfg.eps)
+        q = self._mm(dts["wq"], xn, lw["wq"])
+        k = self._mm(dts["wk"], xn, lw["wk"])
+        v = self._mm(dts["wv"], xn, lw["wv"])
+        q = rope(q.reshape(H, 1, D), cs, sn).reshape(H, D)
+        k = rope(k.reshape(H, 1, D), cs, sn).reshape(H, D)
+        self.kc[li, :, pos] = k.astype(np.float16).astype(np.float32)
+        self.vc[li, :, pos] = v.reshape(H, D).astype(np.float16).astype(np.float32)
+        a = attention_decode(q, self.kc[li], self.vc[li], pos + 1, float(self.scale)).reshape(-1)
+        x = (x + self._mm(dts["wo"], a, lw["wo"])).astype(np.float32)
+        xn = rms_norm(x, lw["ffn_gain"], cfg.eps)
+        g = self._mm(dts["wg"], xn, lw["wg"])
+        u = self._mm(dts["wu"], xn, lw["wu"])
+        h = (g / (np.float32(1.0) + np.exp(-g)) * u).astype(np.float32)
+        return (x + self._mm(dts["wd"], h, lw["wd"])).astype(np.float32)
+
+    def logits(self, x: np.ndarray) -> np.ndarray:
+        """The final RmsNorm (lazy.rs:7360) and the output projection."""
+        xn = rms_norm(x, self.w["final_gain"], self.cfg.eps)
         return self._mm(Q6K, xn, self.w["out"])
+
+    def step(self, token: int, pos: int) -> np.ndarray:
+        """Logits [vocab] of `token` at position `pos` (the cache holds 0..pos-1)."""
+        x = self.w["embed"][token].astype(np.float32).copy()
+        for li in range(len(self.w["layers"])):
+            x = self.layer(li, x, pos)
+        return self.logits(x)
 
     def prefill(self, tokens, workers: int = 16) -> np.ndarray:
         """The prompt as one batch (apply_layer at seq = M, lazy.rs:7363-7446):

@@ -437,6 +437,22 @@ def test_decoder_teacher_forced_logits(dev, small_decoder):
     assert rel_err(kc[:, :len(prompt)], ref.kc[1][:, :len(prompt)]) < DEC_TOL
 
 
+def test_decoder_teacher_forced_layers(dev, small_decoder):
+    """Per-layer parity at the north-star bound: after six forced steps, the
+    seventh position layer by layer with the CPU path teacher-forced on the
+    GPU's residual and caches (test_gpu_prefill.teacher_forced_layers)."""
+    from test_gpu_prefill import teacher_forced_layers
+
+    dec = small_decoder
+    ref = oracle_model(dec)
+    prompt = [7, 123, 45, 299, 0, 18, 250, 3]
+    dec.start(prompt)
+    for _ in range(6):
+        dec.enqueue_step()
+    assert dec.pos.numpy()[0] == 6
+    teacher_forced_layers(dec, ref, 6)
+
+
 def test_decoder_greedy_graph_replay(dev, small_decoder):
     """A captured step replays every position; tokens match the eager run's and
     the CPU path's greedy choices."""

@@ -228,3 +228,42 @@ def test_full_7b_decoder_prefill_and_steps(dev):
         assert err < FULL_TOL
         toks.append(int(dec.tokens_host()[p + 1]))
     assert dec.pos.numpy()[0] == 514
+    say("full 7B decoder: teacher-forced layers at pos 514")
+    teacher_forced_layers(dec, ref, 514)
+
+
+LAYER_TOL = 1e-3
+
+
+def teacher_forced_layers(dec, ref, p):
+    """One decode position, layer by layer, with the CPU path teacher-forced
+    on the GPU's state: before layer li the CPU takes the GPU's residual x and
+    the GPU's cache rows 0 .. p-1 of that layer, then both run apply_layer
+    (lazy.rs:7363-7440) once.  What is left between them is one layer's f32
+    ordering (and the rare Q8K / f16 rounding it flips), not 32 layers of it:
+    each layer's output -- its residual update x_out - x_in -- and the cache
+    row it appends agree within 1e-3 of the CPU update's norm, and so do the
+    logits of the GPU's final x.  The GPU's x then feeds the next layer."""
+    n_layers = dec.cfg.n_layers
+    worst = 0.0
+    for li in range(n_layers):
+        kc, vc = dec.kv_host(li)
+        ref.kc[li][:, :p] = kc[:, :p]
+        ref.vc[li][:, :p] = vc[:, :p]
+        x_in = dec.x.numpy()
+        x_cpu = ref.layer(li, x_in, p)
+        dec.enqueue_layer(li)
+        x_gpu = dec.x.numpy()
+        upd = x_cpu - x_in
+        err = float(np.abs(x_gpu - x_cpu).max() / np.linalg.norm(upd))
+        kc, vc = dec.kv_host(li)
+        ek, ev = rel_err(kc[:, p], ref.kc[li][:, p]), rel_err(vc[:, p], ref.vc[li][:, p])
+        worst = max(worst, err)
+        if li in (0, n_layers // 2, n_layers - 1) or err > LAYER_TOL / 4:
+            say(f"  layer {li}: update rel err {err:.2e}, cache row k {ek:.2e} v {ev:.2e}")
+        assert err <= LAYER_TOL and ek <= LAYER_TOL and ev <= LAYER_TOL, (li, err, ek, ev)
+    dec.enqueue_step(parts=("logits",))
+    lg = dec.logits.numpy()
+    el = rel_err(lg, ref.logits(dec.x.numpy()))
+    say(f"  worst layer update rel err {worst:.2e}; logits of the GPU's final x {el:.2e}")
+    assert el <= LAYER_TOL
