@@ -178,11 +178,14 @@ struct ActLds {
 
 __host__ __device__ constexpr int align16i(int x) { return (x + 15) & ~15; }
 
-__host__ __device__ inline ActLds act_lds_layout(int act_dtype, int K) {
+// qstride: bytes between the superblocks of a Q8K row in LDS (0: 256 + 16);
+// the weight format picks the stride its lanes' reads are bank-conflict free
+// with (formats.hpp, QSTRIDE).
+__host__ __device__ inline ActLds act_lds_layout(int act_dtype, int K, int qstride = 0) {
     ActLds l{};
     if (act_dtype == GGML_Q8K) {
         const int kb = K / QK_K;
-        l.qstride = QK_K + 16;
+        l.qstride = qstride ? qstride : QK_K + 16;
         l.off_d = align16i(kb * l.qstride);
         l.off_bs = align16i(l.off_d + 4 * kb);
         l.bytes = l.off_bs + 32 * kb;

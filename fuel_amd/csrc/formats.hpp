@@ -25,6 +25,11 @@ struct Q4K {
     static constexpr int BYTES = Q4K_BYTES;
     static constexpr int ELEMS = QK_K;
     static constexpr int ACT = GGML_Q8K;
+    // LDS bytes per activation superblock: lane c of block b reads 64
+    // contiguous bytes at 64c, so with 16 lanes served per cycle (blocks
+    // b..b+3) the 68-dword stride puts the 16 reads of a cycle on disjoint
+    // bank quads (4b + 16c mod 64)
+    static constexpr int QSTRIDE = QK_K + 16;
     struct Act {
         uint4 a[4];  // q8 of elements 64c + 0..63
         int bs_lo;   // bsums[4c] + bsums[4c+1]
@@ -96,6 +101,11 @@ struct Q6K {
     static constexpr int BYTES = Q6K_BYTES;
     static constexpr int ELEMS = QK_K;
     static constexpr int ACT = GGML_Q8K;
+    // lane c reads 16 bytes at 128 (c >> 1) + 16 (c & 1) + 32 qd: dword quads
+    // {0, 4, 32, 36} + stride * b.  A 68-dword stride (Q4K's) overlaps them for
+    // neighbouring blocks (two-way bank conflicts); 72 dwords (8 mod 64) keeps
+    // the 16 quads of a cycle disjoint
+    static constexpr int QSTRIDE = QK_K + 32;
     struct Act {
         uint4 a[4];  // q8 of the lane's 4 groups of 16
         int bs[4];   // bsums of those groups
@@ -181,6 +191,7 @@ struct Q80 {
     static constexpr int BYTES = Q8_0_BYTES;
     static constexpr int ELEMS = QK8_0;
     static constexpr int ACT = GGML_Q8_0;
+    static constexpr int QSTRIDE = 0;  // (Q8_0 rows: the blocks packed, 32 bytes apart)
     struct Act {
         uint4 a;
         float d;

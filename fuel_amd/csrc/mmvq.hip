@@ -132,7 +132,7 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
     const int gi = lane / F::LPB, c = lane % F::LPB;
     const int KB = K / F::ELEMS;
     const size_t row_bytes = (size_t)KB * F::BYTES;
-    const ActLds lay = act_lds_layout(F::ACT, K);
+    const ActLds lay = act_lds_layout(F::ACT, K, F::QSTRIDE);
     int8_t* s_qs = reinterpret_cast<int8_t*>(smem);
     float* s_d = reinterpret_cast<float*>(smem + lay.off_d);
     int16_t* s_bs = reinterpret_cast<int16_t*>(smem + lay.off_bs);
@@ -449,7 +449,7 @@ hipError_t launch_qmv_wg(const uint8_t* w, const float* x, float* y, int M, int 
             o = 1;
         occ = o;
     }
-    const size_t lds = (size_t)MR * act_lds_layout(F::ACT, K).bytes;
+    const size_t lds = (size_t)MR * act_lds_layout(F::ACT, K, F::QSTRIDE).bytes;
     if (lds > 65536) return hipErrorInvalidValue;
     const int groups = (N + RPW - 1) / RPW;  // (rows, or groups of RPW rows)
     const int need = (groups + NW - 1) / NW;
@@ -555,7 +555,9 @@ hipError_t launch_pair_spl(const uint8_t* w1, float* y1, int n1, const uint8_t* 
             v = 1;
         occ = v;
     }
-    const size_t lds = (size_t)act_lds_layout(F1::ACT, K).bytes;
+    const size_t lds1 = (size_t)act_lds_layout(F1::ACT, K, F1::QSTRIDE).bytes;
+    const size_t lds2 = (size_t)act_lds_layout(F2::ACT, K, F2::QSTRIDE).bytes;
+    const size_t lds = lds1 > lds2 ? lds1 : lds2;  // (each workgroup lays out its own format's row)
     if (lds > 65536) return hipErrorInvalidValue;
     // workgroups split in proportion to the bytes of the two matrices
     const double b1 = (double)n1 * F1::BYTES, b2 = (double)n2 * F2::BYTES;

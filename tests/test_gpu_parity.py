@@ -534,3 +534,67 @@ def test_storage_outlives_device_close(dev):
     x = O.normal((1, 256), seed=5, stream=2)
     got, _ = dev.load_quantized(O.Q4K, w.tobytes()).fwd((64, 256), dev.from_numpy(x))
     assert rel_err(got.numpy()[0], O.matmul(O.Q4K, x, w)[0]) < TOL
+
+
+# ---- the quantize inside the mat-vec, bit for bit ----
+
+def one_hot_q4k(k):
+    """Q4_K weights [k, k/256]: row n is 1.0 at element n and 0 elsewhere (d =
+    1, dmin = 0, every 6-bit scale 1, min 0), so y[n] = d_x * q8[n] of the
+    activation's Q8K block, one f32 product."""
+    kb = k // 256
+    b = np.zeros((k, kb), O.BLOCK_Q4K)
+    b["d"] = 0x3C00
+    b["scales"] = np.array([1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1], np.uint8)
+    n = np.arange(k)
+    e = n % 256
+    c, i = e // 64, e % 64
+    idx = 32 * c + (i % 32)
+    qs = b["qs"]
+    qs[n, n // 256, idx] = np.where(i < 32, 1, 16).astype(np.uint8)
+    return b
+
+
+def one_hot_q6k(k):
+    """Q6_K weights [k, k/256]: row n is 1.0 at element n (d = 1, every scale
+    1, code 33 there and 32 elsewhere)."""
+    kb = k // 256
+    b = np.zeros((k, kb), O.BLOCK_Q6K)
+    b["d"] = 0x3C00
+    b["scales"] = 1
+    b["qh"] = 0xAA  # the high two bits of code 32 (and 33) in every slot
+    n = np.arange(k)
+    e = n % 256
+    hh, r = e // 128, e % 128
+    qd, l = r // 32, r % 32
+    ql = b["ql"]
+    ql[n, n // 256, 64 * hh + l + 32 * (qd & 1)] = np.where(qd >> 1, 16, 1).astype(np.uint8)
+    return b
+
+
+@pytest.mark.parametrize("dt", [O.Q4K, O.Q6K])
+@pytest.mark.parametrize("k", [256, 4096, 11008, 12288])
+def test_matvec_fused_quantize_bit_exact(dev, dt, k):
+    """The Q8K quantize the mat-vec runs on its activation row inside each
+    workgroup (BlockQ8K::from_float, k_quants.rs:2230-2267), bit for bit:
+    against one-hot weights every output is d_x * q8 of one element, which
+    must equal the same product of the CPU path's Q8K block.  Rows: N(0, 1),
+    the integer closed form, first-index ties, a zero row, and 2 rows (the
+    several-row mat-vec)."""
+    w = one_hot_q4k(k) if dt == O.Q4K else one_hot_q6k(k)
+    rows = np.concatenate([acts(2, k, seed=k), special_rows(k)])
+    wd = dev.from_numpy(as_u32(w))
+    say("fused quantize", dt, k, rows.shape)
+    for m in (1, 2):
+        for r0 in range(0, rows.shape[0], m):
+            x = rows[r0:r0 + m]
+            if x.shape[0] < m:
+                continue
+            blk = O.quantize(O.Q8K, x)
+            # (+ 0: the sums start from +0, so a zero product of a negative d is +0)
+            want = (blk["d"][:, :, None] * blk["qs"].astype(np.float32)).reshape(m, k).astype(np.float32) + np.float32(0)
+            out = dev.alloc((m, k), np.float32)
+            F.qmatmul_f32_rocm_wrapper([dev.from_numpy(x), wd], [out], F.QMatMulParams(dt, 1, m, k, k))
+            got = out.numpy()
+            bad = np.nonzero(got.view(np.uint32) != want.view(np.uint32))
+            assert bad[0].size == 0, (m, r0, bad[1][:8], got[bad][:8], want[bad][:8])
