@@ -36,6 +36,11 @@ namespace frq {
 // activation row has arrived).
 // QMV_INDEXED_ROUTE: QMV_INDEXED with the expert of each launch row picked in
 // the workgroup from the token's router logits (route.hpp).
+// The 16-lane row quantize (act16_*) from this many rounds of the 64-lane one.
+#ifndef QMV_QUAD_MIN_ROUNDS
+#define QMV_QUAD_MIN_ROUNDS 3
+#endif
+
 enum QmvMode {
     QMV_PLAIN = 0,
     QMV_INDEXED = 1,
@@ -184,6 +189,15 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
     // 256-element activation chunks of a row of SPL slots, per wavefront
     constexpr int CHUNKS = SPL * (64 / F::LPB) * F::ELEMS / QK_K;
     constexpr int MAXQ = (CHUNKS + NW - 1) / NW;
+    // rows of more Q8K superblocks than the workgroup has wavefronts (K =
+    // 11008 at 16 wavefronts: three rounds of the 64-lane quantize): 16 lanes
+    // per superblock, four per wavefront, one round (q8.hpp, act16_*)
+    // (plain row loads only: with the SwiGLU input or the RMS norm the per-lane
+    // work of four times the elements on a quarter of the lanes measured slower)
+    constexpr bool QUAD = F::ACT == GGML_Q8K && MAXQ >= QMV_QUAD_MIN_ROUNDS && MR == 1 &&
+                          (MODE == QMV_PLAIN || MODE == QMV_FUSED_NOX);
+    constexpr int MAXQ4 = (CHUNKS + 4 * NW - 1) / (4 * NW);
+    ActRowPre16<QUAD ? MAXQ4 : 1> pre16;
     ActRowPre<MAXQ> pre;
     ActRowPre<(MR > 1 ? MAXQ : 1)> pre_more[(MR > 1 ? MR - 1 : 1)];  // (MR > 1: rows m+1 ..)
     AttnRowPre<MODE == QMV_ATTN ? MAXQ : 1> apre;
@@ -193,6 +207,11 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
     else if constexpr (MODE == QMV_ATTN) {
         apos = __float_as_int(attn_load_early(reinterpret_cast<const float*>(ix.attn_pos)));
         attn_row_load<NW, MAXQ>(x, ix.attn_nsplit, K, w, lane, apre);
+    } else if constexpr (QUAD) {
+        if (MODE != QMV_PLAIN && MODE != QMV_FUSED_NOX && xr2)
+            act16_row_load_swiglu<NW, MAXQ4>(xr, xr2, K, w, lane, pre16);
+        else
+            act16_row_load<NW, MAXQ4>(xr, K, w, lane, pre16);
     } else if (MODE != QMV_PLAIN && MODE != QMV_FUSED_NOX && xr2)
         act_row_load_swiglu<F::ACT, NW, MAXQ>(xr, xr2, K, w, lane, pre);
     else
@@ -258,10 +277,17 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
     if ((MODE == QMV_FUSED || MODE == QMV_GLU) && ix.rms_gain) {
         // rms_norm_last_dim (sum of squares over the whole row, spread over the
         // wavefronts) and the affine gain, before quantization
-        act_row_rms_norm<F::ACT, NW, MAXQ>(pre, ix.rms_gain, ix.rms_eps, K, w, lane,
-                                           [&](float v) { return block_sum_waves<NW>(v, s_red, w, lane); });
+        if constexpr (QUAD)
+            act16_row_rms_norm<NW, MAXQ4>(pre16, ix.rms_gain, ix.rms_eps, K, w, lane,
+                                          [&](float v) { return block_sum_waves<NW>(v, s_red, w, lane); });
+        else
+            act_row_rms_norm<F::ACT, NW, MAXQ>(pre, ix.rms_gain, ix.rms_eps, K, w, lane,
+                                               [&](float v) { return block_sum_waves<NW>(v, s_red, w, lane); });
     }
-    act_row_quantize<F::ACT, NW, MAXQ>(pre, K, s_qs, lay.qstride, s_d, s_bs, w, lane);
+    if constexpr (QUAD)
+        act16_row_quantize<NW, MAXQ4>(pre16, K, s_qs, lay.qstride, s_d, s_bs, w, lane);
+    else
+        act_row_quantize<F::ACT, NW, MAXQ>(pre, K, s_qs, lay.qstride, s_d, s_bs, w, lane);
     if constexpr (MR > 1) {
 #pragma unroll
         for (int i = 1; i < MR; i++) {

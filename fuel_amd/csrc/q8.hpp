@@ -43,43 +43,51 @@ __device__ __forceinline__ int quad_sum(int v) {
     return v;
 }
 
+// One code of BlockQ8K::from_float: (iscale * x).round().min(127) as i8
+// (k_quants.rs:2253) -- half-away rounding, the NaN of inf * 0 taken to 127
+// by min (NaN-ignoring), -inf saturating to -128.  The argument is within
+// 128 (1 + 2^-23) in magnitude unless it is infinite or NaN, so the two
+// clamps and the conversion are the saturating cast exactly.
+__device__ __forceinline__ int q8k_code(float v) { return (int)fmaxf(fminf(roundf(v), 127.0f), -128.0f); }
+
+__device__ __forceinline__ uint32_t pack_i8x4(const int* q) {
+    return (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) | ((uint32_t)(q[2] & 0xff) << 16) |
+           ((uint32_t)(q[3] & 0xff) << 24);
+}
+
 // `v` = elements 4*lane..4*lane+3 of the superblock, already loaded.
 // The reference keeps the first element of largest |x| (strict '<' scan, so
 // NaN and 0 never win): amax = max |x| ignoring NaN, then the first lane (by
 // ballot) and first slot in it with |x| == amax supplies the signed value.
+// Branch-free: the codes are formed for every superblock and an all-zero
+// (amax == 0) one is replaced by zeros and d = 0 at the end.
 __device__ __forceinline__ Q8KWave q8k_quantize_vals(const float4 v, int lane) {
     const float xv[4] = {v.x, v.y, v.z, v.w};
     float m = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) m = fmaxf(m, fabsf(xv[i]));
     const float amax = wave_max_nonneg(m);
-    int q[4];
-    float d;
-    if (amax == 0.0f) {
-        q[0] = q[1] = q[2] = q[3] = 0;
-        d = 0.0f;
-    } else {
-        float mine = 0.0f;
-        bool has = false;
+    const bool zero = amax == 0.0f;
+    float mine = 0.0f;
+    bool has = false;
 #pragma unroll
-        for (int i = 3; i >= 0; i--)
-            if (fabsf(xv[i]) == amax) {
-                mine = xv[i];
-                has = true;
-            }
-        const unsigned long long ballot = __ballot(has);
-        const int first = __builtin_ctzll(ballot);
-        const float bval = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), first));
-        const float iscale = -128.0f / bval;
-#pragma unroll
-        for (int i = 0; i < 4; i++) q[i] = sat_i8(fminf(roundf(iscale * xv[i]), 127.0f));
-        d = 1.0f / iscale;
+    for (int i = 3; i >= 0; i--) {
+        const bool hit = fabsf(xv[i]) == amax;
+        mine = hit ? xv[i] : mine;
+        has = has || hit;
     }
+    // (no lane at all only for an all-NaN superblock, amax = 0: lane 63 then)
+    const unsigned long long ballot = __ballot(has) | (1ull << 63);
+    const int first = __builtin_ctzll(ballot);
+    const float bval = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), first));
+    const float iscale = -128.0f / bval;
+    int q[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) q[i] = q8k_code(iscale * xv[i]);
     Q8KWave r;
-    r.bsum = quad_sum(q[0] + q[1] + q[2] + q[3]);
-    r.packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) | ((uint32_t)(q[2] & 0xff) << 16) |
-               ((uint32_t)(q[3] & 0xff) << 24);
-    r.d = d;
+    r.bsum = zero ? 0 : quad_sum(q[0] + q[1] + q[2] + q[3]);
+    r.packed = zero ? 0u : pack_i8x4(q);
+    r.d = zero ? 0.0f : 1.0f / iscale;
     return r;
 }
 
@@ -234,6 +242,171 @@ __device__ __forceinline__ void act_row_rms_norm(ActRowPre<MAXQ>& p, const float
         p.v[i].y = (p.v[i].y * rinv) * g[i].y;
         p.v[i].z = (p.v[i].z * rinv) * g[i].z;
         p.v[i].w = (p.v[i].w * rinv) * g[i].w;
+    }
+}
+
+// ---- Q8K rows with 16 lanes per superblock ----
+// For long rows (more superblocks than a workgroup has wavefronts) the row is
+// held four superblocks per wavefront: lanes 16g .. 16g+15 of wavefront w own
+// superblock 4 (w + NW i) + g, lane l holding its elements 16 (l & 15) ..
+// +16 (four float4, 64 contiguous bytes).  The maximum and the first index of
+// the maximum are reduced within the 16-lane DPP row, with no readlanes, and a
+// lane's 16 elements are exactly one of the superblock's 16-element groups, so
+// its bsum needs no reduction at all.  The values are those of
+// q8k_quantize_vals: the same maximum (order-free), the same first element
+// (the smallest element index among the |x| == amax), the same iscale,
+// rounding, saturation and d.
+template <int MAXQ4>
+struct ActRowPre16 {
+    float4 v[MAXQ4][4];
+};
+
+template <int NW>
+__device__ __forceinline__ int act16_chunk(int w, int i, int lane) {
+    return 4 * (w + NW * i) + (lane >> 4);
+}
+// element offset of float4 j of lane `lane` in chunk ch (clamped into the row)
+__device__ __forceinline__ int act16_elem(int ch, int nchunks, int lane, int j) {
+    return (ch < nchunks ? ch : nchunks - 1) * QK_K + 16 * (lane & 15) + 4 * j;
+}
+
+template <int NW, int MAXQ4>
+__device__ __forceinline__ void act16_row_load(const float* __restrict__ x, int K, int w, int lane,
+                                               ActRowPre16<MAXQ4>& p) {
+    const int nchunks = K / QK_K;
+#pragma unroll
+    for (int i = 0; i < MAXQ4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) p.v[i][j] = load_f4_early(x + act16_elem(act16_chunk<NW>(w, i, lane), nchunks, lane, j));
+}
+
+template <int NW, int MAXQ4>
+__device__ __forceinline__ void act16_row_load_swiglu(const float* __restrict__ g, const float* __restrict__ u, int K,
+                                                      int w, int lane, ActRowPre16<MAXQ4>& p) {
+    ActRowPre16<MAXQ4> pu;
+    act16_row_load<NW, MAXQ4>(g, K, w, lane, p);
+    act16_row_load<NW, MAXQ4>(u, K, w, lane, pu);
+#pragma unroll
+    for (int i = 0; i < MAXQ4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            p.v[i][j].x = silu_mul(p.v[i][j].x, pu.v[i][j].x);
+            p.v[i][j].y = silu_mul(p.v[i][j].y, pu.v[i][j].y);
+            p.v[i][j].z = silu_mul(p.v[i][j].z, pu.v[i][j].z);
+            p.v[i][j].w = silu_mul(p.v[i][j].w, pu.v[i][j].w);
+        }
+}
+
+template <int NW, int MAXQ4, class BlockSum>
+__device__ __forceinline__ void act16_row_rms_norm(ActRowPre16<MAXQ4>& p, const float* __restrict__ gain, float eps,
+                                                   int K, int w, int lane, BlockSum block_sum) {
+    const int nchunks = K / QK_K;
+    float4 g[MAXQ4][4];
+#pragma unroll
+    for (int i = 0; i < MAXQ4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            g[i][j] = *reinterpret_cast<const float4*>(gain + act16_elem(act16_chunk<NW>(w, i, lane), nchunks, lane, j));
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MAXQ4; i++) {
+        const bool live = act16_chunk<NW>(w, i, lane) < nchunks;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float4 v = live ? p.v[i][j] : make_float4(0.f, 0.f, 0.f, 0.f);
+            ss = fmaf(v.x, v.x, ss);
+            ss = fmaf(v.y, v.y, ss);
+            ss = fmaf(v.z, v.z, ss);
+            ss = fmaf(v.w, v.w, ss);
+        }
+    }
+    const float total = block_sum(dpp_wave_sum(ss));
+    const float rinv = 1.0f / sqrtf(total * (1.0f / (float)K) + eps);
+#pragma unroll
+    for (int i = 0; i < MAXQ4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            p.v[i][j].x = (p.v[i][j].x * rinv) * g[i][j].x;
+            p.v[i][j].y = (p.v[i][j].y * rinv) * g[i][j].y;
+            p.v[i][j].z = (p.v[i][j].z * rinv) * g[i][j].z;
+            p.v[i][j].w = (p.v[i][j].w * rinv) * g[i][j].w;
+        }
+}
+
+// DPP steps over one 16-lane row (every lane of the row ends with the result)
+__device__ __forceinline__ float row16_max(float v) {
+#define FRQ_DPP_MAX(ctrl) \
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false)))
+    FRQ_DPP_MAX(0xB1);   // quad_perm [1,0,3,2]
+    FRQ_DPP_MAX(0x4E);   // quad_perm [2,3,0,1]
+    FRQ_DPP_MAX(0x141);  // row_half_mirror
+    FRQ_DPP_MAX(0x140);  // row_mirror
+#undef FRQ_DPP_MAX
+    return v;
+}
+__device__ __forceinline__ int row16_min(int v) {
+#define FRQ_DPP_MIN(ctrl) v = min(v, __builtin_amdgcn_update_dpp(0, v, ctrl, 0xF, 0xF, false))
+    FRQ_DPP_MIN(0xB1);
+    FRQ_DPP_MIN(0x4E);
+    FRQ_DPP_MIN(0x141);
+    FRQ_DPP_MIN(0x140);
+#undef FRQ_DPP_MIN
+    return v;
+}
+
+// One superblock held by a 16-lane row: lane l16 owns elements 16 l16 .. +16.
+// Writes the lane's 16 quantized bytes, its group's bsum and (lane 0 of the
+// row) d into the LDS row at superblock ch.
+__device__ __forceinline__ void q8k_quantize16_store(const float4 (&v)[4], int ch, int8_t* qs, int qstride, float* dv,
+                                                     int16_t* bsums, int l16) {
+    float xv[16];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        xv[4 * j] = v[j].x;
+        xv[4 * j + 1] = v[j].y;
+        xv[4 * j + 2] = v[j].z;
+        xv[4 * j + 3] = v[j].w;
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; e++) m = fmaxf(m, fabsf(xv[e]));
+    const float amax = row16_max(m);
+    // first element of |x| == amax: key = 2 * (element index) + sign bit,
+    // minimized over the row (1023 when this lane has none); |x| == amax > 0
+    // makes x = +-amax exactly
+    int key = 1023;
+#pragma unroll
+    for (int e = 15; e >= 0; e--) {
+        const int k = 2 * (16 * l16 + e) + (int)(__builtin_bit_cast(uint32_t, xv[e]) >> 31);
+        key = fabsf(xv[e]) == amax ? k : key;
+    }
+    key = row16_min(key);
+    const float bval = (key & 1) ? -amax : amax;
+    const bool zero = amax == 0.0f;
+    const float iscale = -128.0f / bval;
+    int q[16];
+    int bsum = 0;
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+        q[e] = q8k_code(iscale * xv[e]);
+        bsum += q[e];
+    }
+    uint32_t pk[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) pk[j] = zero ? 0u : pack_i8x4(q + 4 * j);
+    *reinterpret_cast<uint4*>(qs + (size_t)ch * qstride + 16 * l16) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    bsums[ch * 16 + l16] = (int16_t)(zero ? 0 : bsum);
+    if (l16 == 0) dv[ch] = zero ? 0.0f : 1.0f / iscale;
+}
+
+template <int NW, int MAXQ4>
+__device__ __forceinline__ void act16_row_quantize(const ActRowPre16<MAXQ4>& p, int K, int8_t* qs, int qstride,
+                                                   float* dv, int16_t* bsums, int w, int lane) {
+    const int nchunks = K / QK_K;
+#pragma unroll
+    for (int i = 0; i < MAXQ4; i++) {
+        const int ch = act16_chunk<NW>(w, i, lane);
+        if (ch < nchunks) q8k_quantize16_store(p.v[i], ch, qs, qstride, dv, bsums, lane & 15);
     }
 }
 
