@@ -1190,6 +1190,7 @@ enum MmqKind {
     MMQ_Q6K_128,
     MMQ_Q4K_WIDE,      // 64 x 128, eight wavefronts side by side in N (16-byte aligned Q4_K blocks)
     MMQ_Q6K_WIDE,      // 64 x 128, the same for Q6_K
+    MMQ_Q4K_WIDE32,    // 32 x 64, the wide-tile kernel with four wavefronts (grids of few 64 x 128 tiles)
 };
 
 #define FRQ_MMQ_KINDS(X)                          \
@@ -1206,6 +1207,7 @@ enum MmqKind {
 
 bool mmq_supported(int dtype) { return dtype == GGML_Q4K || dtype == GGML_Q6K; }
 
+
 MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus, size_t max_part_elems) {
     MmqPlan p{};
     // 144-byte Q4_K blocks at a 16-byte aligned base allow the LDS DMA staging
@@ -1215,6 +1217,11 @@ MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus, siz
     const int base = dtype == GGML_Q4K ? MMQ_Q4K_32 : MMQ_Q6K_32;
     p.kind = M >= 128 ? base + 2 : M >= 64 ? base + 1 : base;
     if (dma && M >= 64) p.kind = M >= 128 ? MMQ_Q4K_DMA_128 : MMQ_Q4K_DMA_64;
+    // Q6_K: 32-row tiles up to 64 rows, 128-row tiles above (a 96-row call in
+    // one partly empty 128-row tile: 4096x4096 22.6 -> 19.3 us, 4096x11008
+    // 54.1 -> 36.5, 11008x4096 41.7 -> 33.0, 4096x32000 109.3 -> 72.8 against
+    // two 64-row tiles)
+    if (dtype == GGML_Q6K) p.kind = M > 64 ? MMQ_Q6K_128 : MMQ_Q6K_32;
     switch (p.kind) {
 #define FRQ_PLAN(kind, F, RT, CT, WM, WN, DMA) \
     case kind: plan_cfg<F, RT, CT, WM, WN, DMA>(M, N, K, num_cus, p); break;
@@ -1222,32 +1229,68 @@ MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus, siz
 #undef FRQ_PLAN
         default: break;
     }
+    // (Q6_K: at most four splits; six measured slower, 4096x4096 M = 33 15.9
+    // against 15.3 us, 11008x4096 28.2 against 28.1)
+    if (dtype == GGML_Q6K && p.ks > 4) p.ks = 4;
     while (p.ks > 1 && (size_t)p.ks * M * N > max_part_elems) p.ks--;
-    // from 128 rows, when the tiles fill the chip without a K split, the
-    // wide-tile kernels (Q4_K: two MFMAs per product instead of three; both:
-    // the DMA ring out of the compiler's sight; Q4_K measured 19-25% faster at
-    // M = 512 on the 7B shapes)
-    // (and for 33-384 rows of long rows, K >= 8192, K-split like the plane
-    // kernels: 11008x4096 at M = 33 26.2 -> 24.3 us, M = 96 41.5 -> 33.3,
-    // M = 128 36.9 -> 34.9, M = 160 57.6 -> 42.9, M = 250 61.4 -> 53.9,
-    // M = 256 61.3 -> 52.0, M = 384 75.6 -> 71.2 (at 511 rows two splits
-    // lose: 79.1 against 81.3 us),
-    // 11008x8192 M = 40 42.9 -> 33.8, M = 64 44.3 -> 35.2; at K = 4096 the
-    // plane kernels' split stays faster, 23.1 against 26.0 us at 4096x4096
-    // M = 128, and below 33 rows it is no faster)
-    const bool wide_split = dma && M >= 33 && M <= 384 && K >= 32 * QK_K;
-    if ((dma && M >= 128 && p.ks == 1) || wide_split) {
-        using T = WideTile<4, 1, 8>;
-        p.kind = MMQ_Q4K_WIDE;
-        p.ks = 1;
-        if (wide_split) {
-            const int tiles = ((M + T::BM - 1) / T::BM) * ((N + T::BN - 1) / T::BN);
-            const int occ = kernel_occupancy<mmq_q4k_wide_kernel<4, 1, 8>, T::NT>();
-            p.ks = mmq_ksplit(tiles, occ, num_cus, K / QK_K);
-            while (p.ks > 1 && (size_t)p.ks * M * N > max_part_elems) p.ks--;
+    // Q4_K at a 16-byte aligned base from 33 rows: the wide-tile kernel (two
+    // MFMAs per product instead of three, the DMA ring out of the compiler's
+    // sight; 19-25% faster than the plane kernels at M = 512 on the 7B shapes),
+    // in one of two tiles by how its 64 x 128 tiles fill the chip (t8 of them
+    // against C CUs; two resident per CU):
+    // * long rows (K >= 8192) from 128 rows: 64 x 128 with a K split of up to
+    //   four, as many as one round of resident workgroups holds (11008x4096
+    //   M = 128 25.3 against 26.5 us with eight splits, M = 512 62.9 against
+    //   65.1 us unsplit);
+    // * 0.8 C <= t8 <= C, or t8 >= 1.25 C: 64 x 128, no K split (4096x32000
+    //   at M = 64 29.8 against 35.0 us with two splits and 37.8 us in 32 x 64
+    //   tiles);
+    // * otherwise, grids well short of one workgroup per CU or just past it
+    //   (two on a few CUs), 32 x 64 tiles of four wavefronts, four resident
+    //   per CU, K split while they are short of one round (long rows: four
+    //   splits below 3 C tiles).  Against the previous plan (the plane kernels
+    //   below 128 rows, 64 x 128 above): 4096x4096 M = 64 14.6 -> 12.3 us,
+    //   M = 128 19.4 -> 15.2, M = 256 25.3 -> 19.0, M = 384 26.9 -> 25.5;
+    //   4096x11008 M = 64 25.2 -> 20.1, M = 128 27.5 -> 26.1, M = 160 38.4 ->
+    //   31.4; 11008x4096 M = 64 22.3 -> 19.4 (graph replays, weights rotated
+    //   over 1.2 GB, split-K reduce included).
+    if (dma && M >= 33) {
+        using T8 = WideTile<4, 1, 8>;
+        using T4 = WideTile<2, 1, 4>;
+        const int KB = K / QK_K, C = num_cus;
+        const bool long_rows = K >= 32 * QK_K;
+        const int t8 = ((M + T8::BM - 1) / T8::BM) * ((N + T8::BN - 1) / T8::BN);
+        auto clamp_ks = [&](int ks) {
+            if (ks > 4) ks = 4;
+            if (ks > KB / 2) ks = KB / 2;
+            return ks > 1 ? ks : 1;
+        };
+        if (long_rows && M >= 128) {
+            const int occ = kernel_occupancy<mmq_q4k_wide_kernel<4, 1, 8>, T8::NT>();
+            p.kind = MMQ_Q4K_WIDE;
+            p.ks = clamp_ks(occ * C / t8);
+        } else if ((t8 >= 4 * C / 5 && t8 <= C) || t8 >= 5 * C / 4) {
+            p.kind = MMQ_Q4K_WIDE;
+            p.ks = 1;
+        } else {
+            const int t4 = ((M + T4::BM - 1) / T4::BM) * ((N + T4::BN - 1) / T4::BN);
+            p.kind = MMQ_Q4K_WIDE32;
+            if (long_rows) p.ks = clamp_ks((3 * C + t4 - 1) / t4);
+            else p.ks = t4 >= 3 * C / 4 ? 1 : clamp_ks((2 * C + t4 - 1) / t4);
+        }
+        while (p.ks > 1 && (size_t)p.ks * M * N > max_part_elems) p.ks--;
+    }
+    // Q6_K from 128 rows without a K split, or from 33 rows when its 64 x 128
+    // tiles fill 0.8-1 workgroups per CU (4096x32000 at M = 33-64: 64 -> 40 us
+    // against the 32-row plane tiles): the wide-tile kernel
+    if (dtype == GGML_Q6K && M >= 33) {
+        using T6 = WideTile6<4, 8>;
+        const int t8 = ((M + T6::BM - 1) / T6::BM) * ((N + T6::BN - 1) / T6::BN);
+        if ((M >= 128 && p.ks == 1) || (t8 >= 4 * num_cus / 5 && t8 <= num_cus)) {
+            p.kind = MMQ_Q6K_WIDE;
+            p.ks = 1;
         }
     }
-    if (dtype == GGML_Q6K && M >= 128 && p.ks == 1) p.kind = MMQ_Q6K_WIDE;
     p.part_elems = p.ks > 1 ? (size_t)p.ks * M * N : 0;
     return p;
 }
@@ -1262,6 +1305,7 @@ hipError_t launch_mmq(const MmqPlan& plan, int dtype, const uint8_t* w, ActView 
 #undef FRQ_LAUNCH
         case MMQ_Q4K_WIDE: return launch_wide<4, 1, 8>(w, act, y, M, N, K, ldy, s, out_mode, plan.ks, part);
         case MMQ_Q6K_WIDE: return launch_wide6<4, 8>(w, act, y, M, N, K, ldy, s, out_mode);
+        case MMQ_Q4K_WIDE32: return launch_wide<2, 1, 4>(w, act, y, M, N, K, ldy, s, out_mode, plan.ks, part);
         default: return hipErrorInvalidValue;
     }
 }

@@ -391,13 +391,16 @@ def test_qmatmul_mfma_rows(dev, dt, m):
 
 @pytest.mark.parametrize("dt", [O.Q4K, O.Q6K])
 @pytest.mark.parametrize("k,n", SHAPES_7B)
-@pytest.mark.parametrize("m", [16, 24, 32, 48, 128, 200, 512])
+@pytest.mark.parametrize("m", [16, 24, 32, 48, 96, 128, 160, 200, 512])
 def test_qmatmul_mfma_7b_shapes(dev, dt, k, n, m):
     """M = 32 / 128 / 512 rows at the four 7B shapes (the
-    43-superblock rows of K = 11008, split K, the 128 x 64 tiles, the LDS-DMA
-    staging), 16 / 24 rows (the tiled kernel's partly empty 32-row tiles
-    for the wide matrices, the skinny kernel at N = 4096) and 48 / 200 rows
-    (the wide tiles with a K split at K = 11008), against the oracle."""
+    43-superblock rows of K = 11008, split K, the LDS-DMA staging), 16 / 24
+    rows (the tiled kernel's partly empty 32-row tiles for the wide matrices,
+    the skinny kernel at N = 4096), and 48 / 96 / 160 / 200 rows: Q4_K's 32 x
+    64 and 64 x 128 wide tiles with and without a K split (ragged row tiles,
+    a 4096x11008 grid just past one workgroup per CU at 160 rows), Q6_K's
+    partly empty 128-row plane tiles at 96 rows and its wide tiles at 48 rows
+    of 4096x32000, against the oracle."""
     say("mfma", dt, "m", m, k, n)
     wq = weights(dt, n, k)
     x = acts(m, k)
@@ -413,10 +416,11 @@ def test_qmatmul_mfma_7b_shapes(dev, dt, k, n, m):
 @pytest.mark.parametrize("dt", [O.Q4K, O.Q6K])
 @pytest.mark.parametrize("m,n,k", [(130, 8200, 256), (200, 4100, 512), (333, 3000, 768), (129, 9000, 1280)])
 def test_qmatmul_wide_tiles(dev, dt, m, n, k):
-    """Q4_K / Q6_K from 128 rows when the tiles fill the chip without a K
-    split: the wide-tile kernels (64-row x 128-column workgroups, one to five
-    superblocks through the two-slot LDS ring, a ragged last row tile and
-    column tile), f32 and f16 outputs, against the oracle."""
+    """Q4_K / Q6_K from 128 rows with short rows: the wide-tile kernels (Q4_K
+    in 32 x 64 tiles for the first three grids and 64 x 128 for the fourth,
+    Q6_K in 64 x 128; one to five superblocks through the two-slot LDS ring,
+    a ragged last row tile and column tile), f32 and f16 outputs, against the
+    oracle."""
     say("wide", dt, m, n, k)
     wq = weights(dt, n, k)
     x = acts(m, k)
