@@ -248,14 +248,18 @@ __device__ __forceinline__ void act_row_rms_norm(ActRowPre<MAXQ>& p, const float
 // ---- Q8K rows with 16 lanes per superblock ----
 // For long rows (more superblocks than a workgroup has wavefronts) the row is
 // held four superblocks per wavefront: lanes 16g .. 16g+15 of wavefront w own
-// superblock 4 (w + NW i) + g, lane l holding its elements 16 (l & 15) ..
-// +16 (four float4, 64 contiguous bytes).  The maximum and the first index of
-// the maximum are reduced within the 16-lane DPP row, with no readlanes, and a
-// lane's 16 elements are exactly one of the superblock's 16-element groups, so
-// its bsum needs no reduction at all.  The values are those of
-// q8k_quantize_vals: the same maximum (order-free), the same first element
-// (the smallest element index among the |x| == amax), the same iscale,
-// rounding, saturation and d.
+// superblock 4 (w + NW i) + g, lane t = l & 15 holding float4 j (j < 4) at
+// elements 64 j + 4 t .. +3.  A load instruction (float4 j of every lane) then
+// reads 256 contiguous bytes per superblock; with each lane's 16 elements
+// contiguous instead (64 bytes a lane) every instruction touched four times
+// the cache lines, and the row's loads took most of the activation stage
+// (11008x4096: the quantize done 3.7 us after the wavefront started).  The
+// maximum and the first index of the maximum are reduced within the 16-lane
+// DPP row, with no readlanes; a 16-element bsum group is float4 j of four
+// neighbouring lanes (a quad), summed exactly by two DPP steps.  The values
+// are those of q8k_quantize_vals: the same maximum (order-free), the same
+// first element (the smallest element index among the |x| == amax), the same
+// iscale, rounding, saturation and d.
 template <int MAXQ4>
 struct ActRowPre16 {
     float4 v[MAXQ4][4];
@@ -267,7 +271,7 @@ __device__ __forceinline__ int act16_chunk(int w, int i, int lane) {
 }
 // element offset of float4 j of lane `lane` in chunk ch (clamped into the row)
 __device__ __forceinline__ int act16_elem(int ch, int nchunks, int lane, int j) {
-    return (ch < nchunks ? ch : nchunks - 1) * QK_K + 16 * (lane & 15) + 4 * j;
+    return (ch < nchunks ? ch : nchunks - 1) * QK_K + 64 * j + 4 * (lane & 15);
 }
 
 template <int NW, int MAXQ4>
@@ -354,9 +358,10 @@ __device__ __forceinline__ int row16_min(int v) {
     return v;
 }
 
-// One superblock held by a 16-lane row: lane l16 owns elements 16 l16 .. +16.
-// Writes the lane's 16 quantized bytes, its group's bsum and (lane 0 of the
-// row) d into the LDS row at superblock ch.
+// One superblock held by a 16-lane row: lane l16 owns float4 j at elements
+// 64 j + 4 l16 .. +3.  Writes the lane's 16 quantized bytes, the bsums of its
+// quad's four groups (lane 4a of the quad) and (lane 0 of the row) d into the
+// LDS row at superblock ch.
 __device__ __forceinline__ void q8k_quantize16_store(const float4 (&v)[4], int ch, int8_t* qs, int qstride, float* dv,
                                                      int16_t* bsums, int l16) {
     float xv[16];
@@ -376,8 +381,8 @@ __device__ __forceinline__ void q8k_quantize16_store(const float4 (&v)[4], int c
     // makes x = +-amax exactly
     int key = 1023;
 #pragma unroll
-    for (int e = 15; e >= 0; e--) {
-        const int k = 2 * (16 * l16 + e) + (int)(__builtin_bit_cast(uint32_t, xv[e]) >> 31);
+    for (int e = 15; e >= 0; e--) {  // (element index 64 (e / 4) + 4 l16 + e % 4 grows with e)
+        const int k = 2 * (64 * (e >> 2) + 4 * l16 + (e & 3)) + (int)(__builtin_bit_cast(uint32_t, xv[e]) >> 31);
         key = fabsf(xv[e]) == amax ? k : key;
     }
     key = row16_min(key);
@@ -385,17 +390,18 @@ __device__ __forceinline__ void q8k_quantize16_store(const float4 (&v)[4], int c
     const bool zero = amax == 0.0f;
     const float iscale = -128.0f / bval;
     int q[16];
-    int bsum = 0;
 #pragma unroll
-    for (int e = 0; e < 16; e++) {
-        q[e] = q8k_code(iscale * xv[e]);
-        bsum += q[e];
+    for (int e = 0; e < 16; e++) q[e] = q8k_code(iscale * xv[e]);
+    int8_t* row = qs + (size_t)ch * qstride;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        *reinterpret_cast<uint32_t*>(row + 64 * j + 4 * l16) = zero ? 0u : pack_i8x4(q + 4 * j);
+        // group 4 j + l16 / 4: float4 j of the quad's four lanes
+        int g = q[4 * j] + q[4 * j + 1] + q[4 * j + 2] + q[4 * j + 3];
+        g += __builtin_amdgcn_update_dpp(0, g, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+        g += __builtin_amdgcn_update_dpp(0, g, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+        if ((l16 & 3) == 0) bsums[ch * 16 + 4 * j + (l16 >> 2)] = (int16_t)(zero ? 0 : g);
     }
-    uint32_t pk[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) pk[j] = zero ? 0u : pack_i8x4(q + 4 * j);
-    *reinterpret_cast<uint4*>(qs + (size_t)ch * qstride + 16 * l16) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-    bsums[ch * 16 + l16] = (int16_t)(zero ? 0 : bsum);
     if (l16 == 0) dv[ch] = zero ? 0.0f : 1.0f / iscale;
 }
 
