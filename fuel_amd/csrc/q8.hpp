@@ -47,8 +47,15 @@ __device__ __forceinline__ int quad_sum(int v) {
 // (k_quants.rs:2253) -- half-away rounding, the NaN of inf * 0 taken to 127
 // by min (NaN-ignoring), -inf saturating to -128.  The argument is within
 // 128 (1 + 2^-23) in magnitude unless it is infinite or NaN, so the two
-// clamps and the conversion are the saturating cast exactly.
-__device__ __forceinline__ int q8k_code(float v) { return (int)fmaxf(fminf(roundf(v), 127.0f), -128.0f); }
+// clamps and the conversion are the saturating cast exactly.  The rounding is
+// v + copysign(0.49999997, v) (0.49999997 the float below 0.5) truncated by
+// the conversion: the sum's truncation equals roundf(v) for every float with
+// |v| <= 129 (checked over all of them), and infinities and NaN pass through
+// the sum unchanged.
+__device__ __forceinline__ int q8k_code(float v) {
+    const float r = v + copysignf(0.49999997f, v);
+    return (int)fmaxf(fminf(r, 127.0f), -128.0f);
+}
 
 __device__ __forceinline__ uint32_t pack_i8x4(const int* q) {
     return (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) | ((uint32_t)(q[2] & 0xff) << 16) |
@@ -281,7 +288,13 @@ __device__ __forceinline__ void act16_row_load(const float* __restrict__ x, int 
 #pragma unroll
     for (int i = 0; i < MAXQ4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) p.v[i][j] = load_f4_early(x + act16_elem(act16_chunk<NW>(w, i, lane), nchunks, lane, j));
+        for (int j = 0; j < 4; j++) {
+#ifdef ACT16_PLAIN_LOADS
+            p.v[i][j] = *reinterpret_cast<const float4*>(x + act16_elem(act16_chunk<NW>(w, i, lane), nchunks, lane, j));
+#else
+            p.v[i][j] = load_f4_early(x + act16_elem(act16_chunk<NW>(w, i, lane), nchunks, lane, j));
+#endif
+        }
 }
 
 template <int NW, int MAXQ4>
@@ -348,6 +361,16 @@ __device__ __forceinline__ float row16_max(float v) {
 #undef FRQ_DPP_MAX
     return v;
 }
+__device__ __forceinline__ float row16_fmin(float v) {
+#define FRQ_DPP_FMIN(ctrl) \
+    v = fminf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false)))
+    FRQ_DPP_FMIN(0xB1);
+    FRQ_DPP_FMIN(0x4E);
+    FRQ_DPP_FMIN(0x141);
+    FRQ_DPP_FMIN(0x140);
+#undef FRQ_DPP_FMIN
+    return v;
+}
 __device__ __forceinline__ int row16_min(int v) {
 #define FRQ_DPP_MIN(ctrl) v = min(v, __builtin_amdgcn_update_dpp(0, v, ctrl, 0xF, 0xF, false))
     FRQ_DPP_MIN(0xB1);
@@ -372,22 +395,33 @@ __device__ __forceinline__ void q8k_quantize16_store(const float4 (&v)[4], int c
         xv[4 * j + 2] = v[j].z;
         xv[4 * j + 3] = v[j].w;
     }
-    float m = 0.0f;
+    // largest and smallest element (NaN ignored, both against 0): the largest
+    // |x| is the larger of pmax and -nmin, and it decides the signed value
+    // unless +amax and -amax both occur
+    float pmax = 0.0f, nmin = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 16; e++) m = fmaxf(m, fabsf(xv[e]));
-    const float amax = row16_max(m);
-    // first element of |x| == amax: key = 2 * (element index) + sign bit,
-    // minimized over the row (1023 when this lane has none); |x| == amax > 0
-    // makes x = +-amax exactly
-    int key = 1023;
-#pragma unroll
-    for (int e = 15; e >= 0; e--) {  // (element index 64 (e / 4) + 4 l16 + e % 4 grows with e)
-        const int k = 2 * (64 * (e >> 2) + 4 * l16 + (e & 3)) + (int)(__builtin_bit_cast(uint32_t, xv[e]) >> 31);
-        key = fabsf(xv[e]) == amax ? k : key;
+    for (int e = 0; e < 16; e++) {
+        pmax = fmaxf(pmax, xv[e]);
+        nmin = fminf(nmin, xv[e]);
     }
-    key = row16_min(key);
-    const float bval = (key & 1) ? -amax : amax;
+    pmax = row16_max(pmax);
+    nmin = row16_fmin(nmin);
+    const float amax = fmaxf(pmax, -nmin);
     const bool zero = amax == 0.0f;
+    float bval = pmax > -nmin ? pmax : nmin;
+    if (pmax == -nmin && !zero) {  // (uniform over the 16-lane row)
+        // first element of |x| == amax: key = 2 * (element index) + sign bit,
+        // minimized over the row (1023 when this lane has none); |x| == amax >
+        // 0 makes x = +-amax exactly
+        int key = 1023;
+#pragma unroll
+        for (int e = 15; e >= 0; e--) {  // (element index 64 (e / 4) + 4 l16 + e % 4 grows with e)
+            const int k = 2 * (64 * (e >> 2) + 4 * l16 + (e & 3)) + (int)(__builtin_bit_cast(uint32_t, xv[e]) >> 31);
+            key = fabsf(xv[e]) == amax ? k : key;
+        }
+        key = row16_min(key);
+        bval = (key & 1) ? -amax : amax;
+    }
     const float iscale = -128.0f / bval;
     int q[16];
 #pragma unroll
