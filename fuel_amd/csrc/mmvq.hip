@@ -36,11 +36,6 @@ namespace frq {
 // activation row has arrived).
 // QMV_INDEXED_ROUTE: QMV_INDEXED with the expert of each launch row picked in
 // the workgroup from the token's router logits (route.hpp).
-// Modes (bit MODE) whose workgroups issue all activation loads before any
-// weight load (see qmv_body).
-#ifndef QMV_XBAR_MASK
-#define QMV_XBAR_MASK ((1 << 0) | (1 << 2) | (1 << 6))
-#endif
 // The 16-lane row quantize (act16_*) from this many rounds of the 64-lane one.
 #ifndef QMV_QUAD_MIN_ROUNDS
 #define QMV_QUAD_MIN_ROUNDS 3
@@ -230,14 +225,18 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
     }
     __builtin_amdgcn_sched_barrier(0);  // the activation loads go out ahead of the weight loads
     // Every wavefront's activation loads go out before any weight row of the
-    // workgroup is requested: a barrier between them (not for the 16-lane
-    // quantize's rows, whose activation loads then hold back the weight stream:
-    // 11008x4096 unchanged; nor with a silu input).  Graph replays, weights
-    // rotated over 1.2 GB: Q4_K 4096x4096 4.65 -> 3.93 us, 4096x11008 7.32 ->
-    // 6.70, 4096x32000 14.70 -> 14.29; Q6_K 5.52 -> 5.09, 9.69 -> 9.30, 22.07 ->
+    // workgroup is requested: a barrier between them, in the plain and fused
+    // modes with rows quantized by 64 lanes.  Graph replays, weights rotated
+    // over 1.2 GB: Q4_K 4096x4096 4.65 -> 3.93 us, 4096x11008 7.32 -> 6.70,
+    // 4096x32000 14.70 -> 14.29; Q6_K 5.52 -> 5.09, 9.69 -> 9.30, 22.07 ->
     // 21.64; with the RMS norm 4096x4096 5.83 -> 5.41, 4096x8192 7.05 -> 6.83.
-    if constexpr (((QMV_XBAR_MASK >> MODE) & 1) && !QUAD && MR == 1) {
-        __builtin_amdgcn_s_barrier();
+    // Measured and left out: the 16-lane quantize's rows (11008x4096 8.56 ->
+    // 8.87 us: their four times larger share of activation loads then holds
+    // back the weight stream), the silu input (10.44 -> 11.49 us at K =
+    // 11008), the GLU mode and the attention merge (unchanged).
+    constexpr bool XBAR = !QUAD && MR == 1 && (MODE == QMV_PLAIN || MODE == QMV_FUSED || MODE == QMV_FUSED_NOX);
+    if constexpr (XBAR) {
+        if (!xr2) __builtin_amdgcn_s_barrier();  // (uniform: no silu input)
         __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (MODE == QMV_INDEXED_ROUTE) {

@@ -288,13 +288,7 @@ __device__ __forceinline__ void act16_row_load(const float* __restrict__ x, int 
 #pragma unroll
     for (int i = 0; i < MAXQ4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-#ifdef ACT16_PLAIN_LOADS
-            p.v[i][j] = *reinterpret_cast<const float4*>(x + act16_elem(act16_chunk<NW>(w, i, lane), nchunks, lane, j));
-#else
-            p.v[i][j] = load_f4_early(x + act16_elem(act16_chunk<NW>(w, i, lane), nchunks, lane, j));
-#endif
-        }
+        for (int j = 0; j < 4; j++) p.v[i][j] = load_f4_early(x + act16_elem(act16_chunk<NW>(w, i, lane), nchunks, lane, j));
 }
 
 template <int NW, int MAXQ4>
