@@ -120,11 +120,16 @@ struct Q6K {
                                     int c, Act& r) {
         const int hh = c >> 1, l0 = 16 * (c & 1);
         const int8_t* q = qs + (size_t)b * qstride + 128 * hh + l0;
-        const int16_t* bs = bsums + (size_t)b * 16 + 8 * hh + (c & 1);
+        // bsums 8hh .. 8hh+7 in one 16-byte read (four 2-byte reads, 32 bytes
+        // apart per block, put four blocks on one bank); group 8hh + (c&1) + 2qd
+        // is the low (c even) or high half of word qd
+        const uint4 bq = *reinterpret_cast<const uint4*>(bsums + (size_t)b * 16 + 8 * hh);
+        const uint32_t bw[4] = {bq.x, bq.y, bq.z, bq.w};
+        const uint32_t bsh = 16u * (uint32_t)(c & 1);
 #pragma unroll
         for (int qd = 0; qd < 4; qd++) {
             r.a[qd] = *reinterpret_cast<const uint4*>(q + 32 * qd);
-            r.bs[qd] = bs[2 * qd];
+            r.bs[qd] = (int)(int16_t)(uint16_t)(bw[qd] >> bsh);
         }
         r.d = dv[b];
     }
