@@ -656,16 +656,24 @@ __device__ __forceinline__ int bytes_times_p(uint32_t q, uint32_t f2) {
     return __builtin_bit_cast(int, p);
 }
 
-template <int RT, int CT, int NW>
-__global__ __launch_bounds__(64 * NW) void mmq_q4k_wide_kernel(const uint8_t* __restrict__ W, ActView act,
-                                                               float* __restrict__ y, int M, int N, int K, int ldy,
-                                                               int mt, int nt, int ks, int out_mode) {
+// KG > 1: KG groups of NW wavefronts share the tile, group g taking every
+// KG-th superblock of the split (its own two LDS slots), and the groups' f32
+// tiles are added through LDS in group order at the end -- a K split inside
+// the workgroup, more wavefronts per tile without partials in memory or a
+// reduce launch.  Every wavefront runs the same number of iterations (a group
+// with no superblock left in the last one only waits at its barrier).
+template <int RT, int CT, int NW, int KG = 1>
+__global__ __launch_bounds__(64 * NW * KG) void mmq_q4k_wide_kernel(const uint8_t* __restrict__ W, ActView act,
+                                                                    float* __restrict__ y, int M, int N, int K,
+                                                                    int ldy, int mt, int nt, int ks, int out_mode) {
     using T = WideTile<RT, CT, NW>;
     constexpr int BM = T::BM, BN = T::BN;
-    __shared__ __align__(16) uint8_t sB0[T::LBUF], sB1[T::LBUF];
+    __shared__ __align__(16) uint8_t sB0[KG][T::LBUF], sB1[KG][T::LBUF];
 
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = KG > 1 ? wave_all / NW : 0;  // (wave-uniform)
+    const int wave = wave_all - grp * NW;        // within the group
     const int KB = K / QK_K;
     const uint32_t row_bytes = (uint32_t)KB * Q4K_BYTES;
     const int l16 = lane & 15, kb = lane >> 4;
@@ -768,12 +776,14 @@ __global__ __launch_bounds__(64 * NW) void mmq_q4k_wide_kernel(const uint8_t* __
             for (int i = 0; i < 4; i++) facc[r][c][i] = 0.0f;
 
     const int b1 = be;
-    const uint32_t slot0 = lds_addr(sB0), slot1 = lds_addr(sB1);
-    if (bs < be) issue(bs, slot0);
+    const uint32_t slot0 = lds_addr(sB0[grp]), slot1 = lds_addr(sB1[grp]);
+    // this group's superblocks: bs + grp, bs + grp + KG, ... (< be)
+    const int iters = (be - bs + KG - 1) / KG;
+    if (bs + grp < be) issue(bs + grp, slot0);
 
     auto iter = [&](auto kr, int b) __attribute__((always_inline)) {
         constexpr int KR = decltype(kr)::value;
-        const uint8_t* A = KR == 0 ? sB0 : sB1;
+        const uint8_t* A = KR == 0 ? sB0[grp] : sB1[grp];
         const uint8_t* Wl = A + T::OW;
         const uint8_t* S = A + T::OS;
         const float* D = reinterpret_cast<const float*>(A + T::OD);
@@ -782,9 +792,11 @@ __global__ __launch_bounds__(64 * NW) void mmq_q4k_wide_kernel(const uint8_t* __
         compiler_fence();
         __builtin_amdgcn_s_barrier();
         compiler_fence();
-        // the other slot was read in iteration b-1, which every wavefront has
-        // left: b+1's DMA runs while b is multiplied
-        if (b + 1 < b1) issue(b + 1, KR == 0 ? slot1 : slot0);
+        // the other slot was read in the previous iteration, which every
+        // wavefront has left: the group's next superblock's DMA runs while b is
+        // multiplied
+        if (b + KG < b1) issue(b + KG, KR == 0 ? slot1 : slot0);
+        if (KG > 1 && b >= b1) return;  // (this group has no superblock left)
         // column headers: d, dmin, the 6-bit scales split as 8 a + b, the mins
         float d[CT], dmin[CT];
         uint32_t aw[CT][2], bw[CT][2], mw[CT];
@@ -857,9 +869,39 @@ __global__ __launch_bounds__(64 * NW) void mmq_q4k_wide_kernel(const uint8_t* __
             }
         }
     };
-    for (int b = bs; b < b1; b += 2) {
+    for (int it = 0; it < iters; it += 2) {
+        const int b = bs + grp + it * KG;
         iter(std::integral_constant<int, 0>{}, b);
-        if (b + 1 < b1) iter(std::integral_constant<int, 1>{}, b + 1);
+        if (it + 1 < iters) iter(std::integral_constant<int, 1>{}, b + KG);
+    }
+
+    if constexpr (KG > 1) {
+        // groups 1.. hand their tiles to group 0 through the (now free) slots
+        constexpr int TILE = RT * CT * 4;
+        static_assert((KG - 1) * NW * 64 * TILE * 4 <= KG * T::LBUF, "reduction fits the first slots");
+        float* red = reinterpret_cast<float*>(&sB0[0][0]);
+        __syncthreads();
+        if (grp > 0) {
+            float* dst = red + ((size_t)((grp - 1) * NW + wave) * TILE) * 64 + lane;
+#pragma unroll
+            for (int r = 0; r < RT; r++)
+#pragma unroll
+                for (int c = 0; c < CT; c++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) dst[64 * ((r * CT + c) * 4 + i)] = facc[r][c][i];
+        }
+        __syncthreads();
+        if (grp > 0) return;
+#pragma unroll
+        for (int g = 1; g < KG; g++) {
+            const float* src = red + ((size_t)((g - 1) * NW + wave) * TILE) * 64 + lane;
+#pragma unroll
+            for (int r = 0; r < RT; r++)
+#pragma unroll
+                for (int c = 0; c < CT; c++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) facc[r][c][i] += src[64 * ((r * CT + c) * 4 + i)];
+        }
     }
 
 #pragma unroll
@@ -1073,19 +1115,20 @@ __global__ void mmq_reduce_kernel(const float* __restrict__ part, float* __restr
 }
 
 // The wide Q4_K kernel, over ks K splits (ks > 1: into part[ks][M][N], then
-// mmq_reduce_kernel adds them in split order into y).
-template <int RT, int CT, int NW>
+// mmq_reduce_kernel adds them in split order into y), KG wavefront groups per
+// tile.
+template <int RT, int CT, int NW, int KG = 1>
 hipError_t launch_wide(const uint8_t* w, ActView act, float* y, int M, int N, int K, int ldy, hipStream_t s,
                        int out_mode, int ks = 1, float* part = nullptr) {
     using T = WideTile<RT, CT, NW>;
     const int mt = (M + T::BM - 1) / T::BM, nt = (N + T::BN - 1) / T::BN;
     if (ks > 1 && !part) return hipErrorInvalidValue;
     if (ks > 1)
-        hipLaunchKernelGGL((mmq_q4k_wide_kernel<RT, CT, NW>), dim3(mt * nt * ks), dim3(T::NT), 0, s, w, act, part, M,
-                           N, K, N, mt, nt, ks, 0);
+        hipLaunchKernelGGL((mmq_q4k_wide_kernel<RT, CT, NW, KG>), dim3(mt * nt * ks), dim3(T::NT * KG), 0, s, w, act,
+                           part, M, N, K, N, mt, nt, ks, 0);
     else
-        hipLaunchKernelGGL((mmq_q4k_wide_kernel<RT, CT, NW>), dim3(mt * nt), dim3(T::NT), 0, s, w, act, y, M, N, K,
-                           ldy, mt, nt, 1, out_mode);
+        hipLaunchKernelGGL((mmq_q4k_wide_kernel<RT, CT, NW, KG>), dim3(mt * nt), dim3(T::NT * KG), 0, s, w, act, y, M,
+                           N, K, ldy, mt, nt, 1, out_mode);
     if (ks > 1) {
         const size_t total = (size_t)M * N;
         hipLaunchKernelGGL(mmq_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, y, M, N,
@@ -1191,6 +1234,8 @@ enum MmqKind {
     MMQ_Q4K_WIDE,      // 64 x 128, eight wavefronts side by side in N (16-byte aligned Q4_K blocks)
     MMQ_Q6K_WIDE,      // 64 x 128, the same for Q6_K
     MMQ_Q4K_WIDE32,    // 32 x 64, the wide-tile kernel with four wavefronts (grids of few 64 x 128 tiles)
+    MMQ_Q4K_WIDE_KG2,    // 64 x 128, two groups of eight wavefronts splitting K inside the workgroup
+    MMQ_Q4K_WIDE32_KG2,  // 32 x 64, two groups of four wavefronts
 };
 
 #define FRQ_MMQ_KINDS(X)                          \
@@ -1238,17 +1283,21 @@ MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus, siz
     // sight; 19-25% faster than the plane kernels at M = 512 on the 7B shapes),
     // in one of two tiles by how its 64 x 128 tiles fill the chip (t8 of them
     // against C CUs; two resident per CU):
-    // * long rows (K >= 8192) from 128 rows: 64 x 128 with a K split of up to
-    //   four, as many as one round of resident workgroups holds (11008x4096
-    //   M = 128 25.3 against 26.5 us with eight splits, M = 512 62.9 against
-    //   65.1 us unsplit);
-    // * 0.8 C <= t8 <= C, or t8 >= 1.25 C: 64 x 128, no K split (4096x32000
-    //   at M = 64 29.8 against 35.0 us with two splits and 37.8 us in 32 x 64
-    //   tiles);
+    // * long rows (K >= 8192) from 128 rows while t8 < 0.8 C: 64 x 128 with a
+    //   K split of up to four, as many as one round of resident workgroups
+    //   holds (11008x4096 M = 128 25.3 against 26.5 us with eight splits);
+    // * 0.8 C <= t8 <= C (long rows from 128 rows: up to 1.25 C): 64 x 128
+    //   with two wavefront groups splitting K inside the workgroup (11008x4096
+    //   M = 512 57.4 against 61.5 us with two splits in memory, 4096x4096 M =
+    //   512 25.1 against 26.4 us with one group, 4096x32000 M = 64 equal);
+    // * t8 >= 1.25 C: 64 x 128, no K split (4096x32000 at M = 64 29.8 against
+    //   35.0 us with two splits and 37.8 us in 32 x 64 tiles);
     // * otherwise, grids well short of one workgroup per CU or just past it
     //   (two on a few CUs), 32 x 64 tiles of four wavefronts, four resident
     //   per CU, K split while they are short of one round (long rows: four
-    //   splits below 3 C tiles).  Against the previous plan (the plane kernels
+    //   splits below 3 C tiles); at most one per CU with short rows, two
+    //   wavefront groups per tile (4096x4096 M = 128 15.2 -> 12.8 us, M = 64
+    //   12.5 -> 11.7 with two splits).  Against the previous plan (the plane kernels
     //   below 128 rows, 64 x 128 above): 4096x4096 M = 64 14.6 -> 12.3 us,
     //   M = 128 19.4 -> 15.2, M = 256 25.3 -> 19.0, M = 384 26.9 -> 25.5;
     //   4096x11008 M = 64 25.2 -> 20.1, M = 128 27.5 -> 26.1, M = 160 38.4 ->
@@ -1265,18 +1314,27 @@ MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus, siz
             if (ks > KB / 2) ks = KB / 2;
             return ks > 1 ? ks : 1;
         };
-        if (long_rows && M >= 128) {
+        if (long_rows && M >= 128 && t8 < 4 * C / 5) {
             const int occ = kernel_occupancy<mmq_q4k_wide_kernel<4, 1, 8>, T8::NT>();
             p.kind = MMQ_Q4K_WIDE;
             p.ks = clamp_ks(occ * C / t8);
-        } else if ((t8 >= 4 * C / 5 && t8 <= C) || t8 >= 5 * C / 4) {
+        } else if ((t8 >= 4 * C / 5 && t8 <= C) || (long_rows && M >= 128 && t8 < 5 * C / 4)) {
+            p.kind = MMQ_Q4K_WIDE_KG2;
+            p.ks = 1;
+        } else if (t8 >= 5 * C / 4) {
             p.kind = MMQ_Q4K_WIDE;
             p.ks = 1;
         } else {
             const int t4 = ((M + T4::BM - 1) / T4::BM) * ((N + T4::BN - 1) / T4::BN);
             p.kind = MMQ_Q4K_WIDE32;
-            if (long_rows) p.ks = clamp_ks((3 * C + t4 - 1) / t4);
-            else p.ks = t4 >= 3 * C / 4 ? 1 : clamp_ks((2 * C + t4 - 1) / t4);
+            if (long_rows) {
+                p.ks = clamp_ks((3 * C + t4 - 1) / t4);
+            } else if (t4 <= C) {
+                p.kind = MMQ_Q4K_WIDE32_KG2;
+                p.ks = t4 >= 3 * C / 4 ? 1 : clamp_ks((C + t4 - 1) / t4);
+            } else {
+                p.ks = 1;
+            }
         }
         while (p.ks > 1 && (size_t)p.ks * M * N > max_part_elems) p.ks--;
     }
@@ -1306,6 +1364,9 @@ hipError_t launch_mmq(const MmqPlan& plan, int dtype, const uint8_t* w, ActView 
         case MMQ_Q4K_WIDE: return launch_wide<4, 1, 8>(w, act, y, M, N, K, ldy, s, out_mode, plan.ks, part);
         case MMQ_Q6K_WIDE: return launch_wide6<4, 8>(w, act, y, M, N, K, ldy, s, out_mode);
         case MMQ_Q4K_WIDE32: return launch_wide<2, 1, 4>(w, act, y, M, N, K, ldy, s, out_mode, plan.ks, part);
+        case MMQ_Q4K_WIDE_KG2: return launch_wide<4, 1, 8, 2>(w, act, y, M, N, K, ldy, s, out_mode, plan.ks, part);
+        case MMQ_Q4K_WIDE32_KG2:
+            return launch_wide<2, 1, 4, 2>(w, act, y, M, N, K, ldy, s, out_mode, plan.ks, part);
         default: return hipErrorInvalidValue;
     }
 }

@@ -397,8 +397,10 @@ def test_qmatmul_mfma_7b_shapes(dev, dt, k, n, m):
     43-superblock rows of K = 11008, split K, the LDS-DMA staging), 16 / 24
     rows (the tiled kernel's partly empty 32-row tiles for the wide matrices,
     the skinny kernel at N = 4096), and 48 / 96 / 160 / 200 rows: Q4_K's 32 x
-    64 and 64 x 128 wide tiles with and without a K split (ragged row tiles,
-    a 4096x11008 grid just past one workgroup per CU at 160 rows), Q6_K's
+    64 and 64 x 128 wide tiles with and without a K split in memory, with one
+    or two wavefront groups splitting K inside the workgroup (4096x4096 at 48
+    and 128 rows, 512 rows of 4096x4096 and 11008x4096; ragged row tiles, a
+    4096x11008 grid just past one workgroup per CU at 160 rows), Q6_K's
     partly empty 128-row plane tiles at 96 rows and its wide tiles at 48 rows
     of 4096x32000, against the oracle."""
     say("mfma", dt, "m", m, k, n)
