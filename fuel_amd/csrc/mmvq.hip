@@ -231,9 +231,10 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
     // 4096x32000 14.70 -> 14.29; Q6_K 5.52 -> 5.09, 9.69 -> 9.30, 22.07 ->
     // 21.64; with the RMS norm 4096x4096 5.83 -> 5.41, 4096x8192 7.05 -> 6.83.
     // Measured and left out: the 16-lane quantize's rows (11008x4096 8.56 ->
-    // 8.87 us: their four times larger share of activation loads then holds
-    // back the weight stream), the silu input (10.44 -> 11.49 us at K =
-    // 11008), the GLU mode and the attention merge (unchanged).
+    // 8.87 us: a 44 KB row does not stay in L2 between launches and arrives
+    // from memory behind every CU's weight requests either way, so the
+    // barrier only delays the weight stream), the silu input (10.44 -> 11.49
+    // us at K = 11008), the GLU mode and the attention merge (unchanged).
     constexpr bool XBAR = !QUAD && MR == 1 && (MODE == QMV_PLAIN || MODE == QMV_FUSED || MODE == QMV_FUSED_NOX);
     if constexpr (XBAR) {
         if (!xr2) __builtin_amdgcn_s_barrier();  // (uniform: no silu input)
