@@ -223,6 +223,16 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
             act_row_load<F::ACT, NW, MAXQ>(x + (size_t)mi * K, K, w, lane, pre_more[i - 1]);
         }
     }
+    // QMV_FUSED: the RMS gains with the activation row, ahead of the weight
+    // rows.  Loaded after them (in the norm, as the GLU mode still does), the
+    // norm waited for the first weight rows' arrival as well: Q4_K 4096x4096
+    // with the norm 5.28 -> 4.50 us, 4096x8192 6.79 -> 6.21 (the two-matrix
+    // launch and the 32000-row Q6_K one unchanged; the GLU launch measured
+    // 0.08 us slower so).  Without a norm these loads read the activation row
+    // again and are never used.
+    constexpr bool RMS_EARLY = MODE == QMV_FUSED && !QUAD;
+    ActRowPre<RMS_EARLY ? MAXQ : 1> gpre;
+    if constexpr (RMS_EARLY) act_row_gain_load<F::ACT, NW, MAXQ>(ix.rms_gain ? ix.rms_gain : xr, K, w, lane, gpre);
     __builtin_amdgcn_sched_barrier(0);  // the activation loads go out ahead of the weight loads
     // Every wavefront's activation loads go out before any weight row of the
     // workgroup is requested: a barrier between them, in the plain and fused
@@ -274,7 +284,22 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
     // rows >= n_split live in the second matrix (row - n_split)
     auto wrow = [&](int r) { return r < n_split ? W + (size_t)r * row_bytes : W2 + (size_t)(r - n_split) * row_bytes; };
     typename F::Raw ra[SPL], rb[SPL];
-    float resa = 0.0f, resb = 0.0f;  // residual values, loaded ahead of their row's weights
+    // Residual values y[r] of the accumulate epilogue.  In the modes without
+    // a prologue (QMV_FUSED_NOX, QMV_ATTN) every call issues one vector load
+    // per row (y[r], or the activation row's first element when there is no
+    // residual): under a branch, the compiler's waits after the join counted
+    // as if the load had not been issued, so the quantize waited for the
+    // first weight row; and the first one, wave-uniform and ahead of every
+    // store, became a scalar-cache load that the quantize's LDS wait then
+    // waited for (Q4_K 4096x4096 with the residual add 4.46 -> 4.23 us).
+    // With the RMS norm (QMV_FUSED) the extra load measured 0.15-0.2 us
+    // slower, so there it stays a plain load under the branch.
+    constexpr bool RES_VEC = MODE == QMV_ATTN || MODE == QMV_FUSED_NOX;
+    auto ldres = [&](int r, float cur) -> float {
+        if constexpr (RES_VEC) return attn_load_early(acc_out ? yr + r : xr);
+        else return acc_out ? yr[r] : cur;
+    };
+    float resa = 0.0f, resb = 0.0f;
     static_assert(RPW == 1 || (SPL == 1 && 64 / F::LPB == 16), "row groups: one slot set of 16 blocks");
     constexpr int SB = (64 / F::LPB) / RPW;              // block slots per row of a group
     const int rsub = RPW > 1 ? gi / SB : 0;              // this lane's row within the group
@@ -282,23 +307,24 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
     {  // (every lane, unconditionally: a wavefront without rows loads the last row and never uses it)
         const int rr = RPW > 1 ? row * RPW + rsub : row;
         const int r0 = rr < N ? rr : N - 1;
-        if (acc_out) resa = yr[r0];
         qmv_load_row<F, SPL>(wrow(r0), gb, c, KB, ra);
         if constexpr (MODE == QMV_GLU && SPL <= 2) qmv_load_row<F, SPL>(W2 + (size_t)r0 * row_bytes, gb, c, KB, rb);
+        resa = ldres(r0, resa);
     }
     if constexpr (MODE == QMV_ATTN) {
         __builtin_amdgcn_sched_barrier(0);  // the merge's waits come after the first row's loads are out
         attn_row_merge<NW, MAXQ>(apre, ix.attn_nsplit, apos >= 0 && apos < ix.attn_max_ctx, pre);
     }
-    if ((MODE == QMV_FUSED || MODE == QMV_GLU) && ix.rms_gain) {
+    if constexpr ((MODE == QMV_FUSED || MODE == QMV_GLU) && !QUAD) {  // (16-lane rows take neither mode)
         // rms_norm_last_dim (sum of squares over the whole row, spread over the
         // wavefronts) and the affine gain, before quantization
-        if constexpr (QUAD)
-            act16_row_rms_norm<NW, MAXQ4>(pre16, ix.rms_gain, ix.rms_eps, K, w, lane,
-                                          [&](float v) { return block_sum_waves<NW>(v, s_red, w, lane); });
-        else
-            act_row_rms_norm<F::ACT, NW, MAXQ>(pre, ix.rms_gain, ix.rms_eps, K, w, lane,
-                                               [&](float v) { return block_sum_waves<NW>(v, s_red, w, lane); });
+        if (ix.rms_gain) {
+            const auto bsum = [&](float v) { return block_sum_waves<NW>(v, s_red, w, lane); };
+            if constexpr (RMS_EARLY)
+                act_row_rms_norm<F::ACT, NW, MAXQ>(pre, gpre, ix.rms_eps, K, w, lane, bsum);
+            else
+                act_row_rms_norm<F::ACT, NW, MAXQ>(pre, ix.rms_gain, ix.rms_eps, K, w, lane, bsum);
+        }
     }
     if constexpr (QUAD)
         act16_row_quantize<NW, MAXQ4>(pre16, K, s_qs, lay.qstride, s_d, s_bs, w, lane);
@@ -384,7 +410,7 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
             int ngrp = row + nw;
             int lg = ngrp < ng ? ngrp : row;
             int lr = lg * RPW + rsub < N ? lg * RPW + rsub : N - 1;
-            if (acc_out) resb = yr[lr];
+            resb = ldres(lr, resb);
             qmv_load_row<F, SPL>(wrow(lr), gb, c, KB, rb);
             float t = qmv_row<F, SPL, RPW>(ra, s_qs, lay.qstride, s_d, s_bs, gb, c, KB);
             int my = row * RPW + rsub;
@@ -394,7 +420,7 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
             ngrp = row + nw;
             lg = ngrp < ng ? ngrp : row;
             lr = lg * RPW + rsub < N ? lg * RPW + rsub : N - 1;
-            if (acc_out) resa = yr[lr];
+            resa = ldres(lr, resa);
             qmv_load_row<F, SPL>(wrow(lr), gb, c, KB, ra);
             t = qmv_row<F, SPL, RPW>(rb, s_qs, lay.qstride, s_d, s_bs, gb, c, KB);
             my = row * RPW + rsub;
@@ -413,7 +439,7 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
                 if (row < N) emit(ra, row, resa);
                 return;
             }
-            if (acc_out) resb = yr[nrow];
+            resb = ldres(nrow, resb);
             qmv_load_row<F, SPL>(wrow(nrow), gi, c, KB, rb);
             emit(ra, row, resa);
             row = nrow;
@@ -422,7 +448,7 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
                 emit(rb, row, resb);
                 return;
             }
-            if (acc_out) resa = yr[nrow];
+            resa = ldres(nrow, resa);
             qmv_load_row<F, SPL>(wrow(nrow), gi, c, KB, ra);
             emit(rb, row, resb);
             row = nrow;
@@ -434,14 +460,14 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
     while (row < N) {
         int nrow = row + nw;
         int lrow = nrow < N ? nrow : row;
-        if (acc_out) resb = yr[lrow];
+        resb = ldres(lrow, resb);
         qmv_load_row<F, SPL>(wrow(lrow), gi, c, KB, rb);
         emit(ra, row, resa);
         row = nrow;
         if (row >= N) break;
         nrow = row + nw;
         lrow = nrow < N ? nrow : row;
-        if (acc_out) resa = yr[lrow];
+        resa = ldres(lrow, resa);
         qmv_load_row<F, SPL>(wrow(lrow), gi, c, KB, ra);
         emit(rb, row, resb);
         row = nrow;

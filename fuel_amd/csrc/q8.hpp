@@ -225,13 +225,13 @@ __device__ __forceinline__ void act_row_load_swiglu(const float* __restrict__ g,
 // on a row held by the workgroup: y = (x * (1 / sqrt(sum(x^2) * (1/K) + eps)))
 // * gain.  block_sum(v) sums one value per wavefront (lane 63) over the
 // workgroup; the sum of squares is a tree here, sequential in the reference.
+// `g` holds the gains of the lane's elements (act_row_gain_load, or the
+// overload below that loads them itself).
 template <int ACT, int NW, int MAXQ, class BlockSum>
-__device__ __forceinline__ void act_row_rms_norm(ActRowPre<MAXQ>& p, const float* __restrict__ gain, float eps, int K,
+__device__ __forceinline__ void act_row_rms_norm(ActRowPre<MAXQ>& p, const ActRowPre<MAXQ>& gp, float eps, int K,
                                                  int w, int lane, BlockSum block_sum) {
     const int nchunks = (K + QK_K - 1) / QK_K;
-    float4 g[MAXQ];  // gains, loaded unconditionally like the row
-#pragma unroll
-    for (int i = 0; i < MAXQ; i++) g[i] = *reinterpret_cast<const float4*>(gain + act_elem(w + NW * i, nchunks, K, lane));
+    const float4* g = gp.v;
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < MAXQ; i++) {  // dead lanes / chunks count as zeros
@@ -250,6 +250,27 @@ __device__ __forceinline__ void act_row_rms_norm(ActRowPre<MAXQ>& p, const float
         p.v[i].z = (p.v[i].z * rinv) * g[i].z;
         p.v[i].w = (p.v[i].w * rinv) * g[i].w;
     }
+}
+
+// The gains of the lane's elements, loaded unconditionally like the row and,
+// like it, as relaxed atomic loads: the compiler keeps them ahead of the
+// weight rows' loads, so that the norm waits for the gains and the row only
+// (the in-order vmcnt counter would otherwise make it wait for the first
+// weight rows as well).
+template <int ACT, int NW, int MAXQ>
+__device__ __forceinline__ void act_row_gain_load(const float* __restrict__ gain, int K, int w, int lane,
+                                                  ActRowPre<MAXQ>& g) {
+    act_row_load<ACT, NW, MAXQ>(gain, K, w, lane, g);
+}
+
+template <int ACT, int NW, int MAXQ, class BlockSum>
+__device__ __forceinline__ void act_row_rms_norm(ActRowPre<MAXQ>& p, const float* __restrict__ gain, float eps, int K,
+                                                 int w, int lane, BlockSum block_sum) {
+    const int nchunks = (K + QK_K - 1) / QK_K;
+    ActRowPre<MAXQ> g;
+#pragma unroll
+    for (int i = 0; i < MAXQ; i++) g.v[i] = *reinterpret_cast<const float4*>(gain + act_elem(w + NW * i, nchunks, K, lane));
+    act_row_rms_norm<ACT, NW, MAXQ>(p, g, eps, K, w, lane, block_sum);
 }
 
 // ---- Q8K rows with 16 lanes per superblock ----
@@ -304,42 +325,6 @@ __device__ __forceinline__ void act16_row_load_swiglu(const float* __restrict__ 
             p.v[i][j].y = silu_mul(p.v[i][j].y, pu.v[i][j].y);
             p.v[i][j].z = silu_mul(p.v[i][j].z, pu.v[i][j].z);
             p.v[i][j].w = silu_mul(p.v[i][j].w, pu.v[i][j].w);
-        }
-}
-
-template <int NW, int MAXQ4, class BlockSum>
-__device__ __forceinline__ void act16_row_rms_norm(ActRowPre16<MAXQ4>& p, const float* __restrict__ gain, float eps,
-                                                   int K, int w, int lane, BlockSum block_sum) {
-    const int nchunks = K / QK_K;
-    float4 g[MAXQ4][4];
-#pragma unroll
-    for (int i = 0; i < MAXQ4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            g[i][j] = *reinterpret_cast<const float4*>(gain + act16_elem(act16_chunk<NW>(w, i, lane), nchunks, lane, j));
-    float ss = 0.0f;
-#pragma unroll
-    for (int i = 0; i < MAXQ4; i++) {
-        const bool live = act16_chunk<NW>(w, i, lane) < nchunks;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const float4 v = live ? p.v[i][j] : make_float4(0.f, 0.f, 0.f, 0.f);
-            ss = fmaf(v.x, v.x, ss);
-            ss = fmaf(v.y, v.y, ss);
-            ss = fmaf(v.z, v.z, ss);
-            ss = fmaf(v.w, v.w, ss);
-        }
-    }
-    const float total = block_sum(dpp_wave_sum(ss));
-    const float rinv = 1.0f / sqrtf(total * (1.0f / (float)K) + eps);
-#pragma unroll
-    for (int i = 0; i < MAXQ4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            p.v[i][j].x = (p.v[i][j].x * rinv) * g[i][j].x;
-            p.v[i][j].y = (p.v[i][j].y * rinv) * g[i][j].y;
-            p.v[i][j].z = (p.v[i][j].z * rinv) * g[i][j].z;
-            p.v[i][j].w = (p.v[i][j].w * rinv) * g[i][j].w;
         }
 }
 
