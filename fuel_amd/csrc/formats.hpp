@@ -58,6 +58,14 @@ struct Q4K {
         r.q0 = *reinterpret_cast<const uint4*>(blk + 16 + 32 * c);
         r.q1 = *reinterpret_cast<const uint4*>(blk + 32 + 32 * c);
     }
+    // The same pieces through a buffer resource of the row (a scalar base and
+    // size) at a 32-bit offset: qmv_load_row's long rows.
+    static constexpr bool BUF = true;
+    __device__ static void load_buf(__amdgpu_buffer_rsrc_t R, uint32_t off, int c, Raw& r) {
+        r.hd = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(R, off, 0, 0));
+        r.q0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(R, off + 16u + 32u * (uint32_t)c, 0, 0));
+        r.q1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(R, off + 32u + 32u * (uint32_t)c, 0, 0));
+    }
     __device__ static void dot(const Raw& r, const Act& x, int c, int& isum, int& msum, float& dw, float& dmw) {
         // 12 packed bytes -> 8 six-bit scales and 8 mins (get_scale_min_k4,
         // utils.rs:50-60) as four words of bytes.
@@ -97,6 +105,7 @@ struct Q4K {
 // is scales[8hh + 2qd + (c&1)].  Each 16-byte piece is one unaligned load.
 // ------------------------------------------------------------------------
 struct Q6K {
+    static constexpr bool BUF = false;  // (row loads through plain pointers only)
     static constexpr int LPB = 4;
     static constexpr int BYTES = Q6K_BYTES;
     static constexpr int ELEMS = QK_K;
@@ -192,6 +201,7 @@ struct Q6K {
 // 0 or 2 mod 4.)
 // ------------------------------------------------------------------------
 struct Q80 {
+    static constexpr bool BUF = false;  // (row loads through plain pointers only)
     static constexpr int LPB = 2;
     static constexpr int BYTES = Q8_0_BYTES;
     static constexpr int ELEMS = QK8_0;

@@ -36,6 +36,12 @@ namespace frq {
 // activation row has arrived).
 // QMV_INDEXED_ROUTE: QMV_INDEXED with the expert of each launch row picked in
 // the workgroup from the token's router logits (route.hpp).
+// QMV_GLU_RMS: QMV_GLU with the RMS norm and no second input, fixed at
+// compile time (the decode step's gate|up launch).  With the choices made at
+// run time the compiler's waits after each join assume the loads of either
+// side (its norm waited for the first weight rows; gate|up 4096x11008 12.22
+// -> 11.85 us with this instantiation and the store-free ring below).  The
+// same for QMV_FUSED measured no faster (the q|k + v pair and the logits).
 // The 16-lane row quantize (act16_*) from this many rounds of the 64-lane one.
 #ifndef QMV_QUAD_MIN_ROUNDS
 #define QMV_QUAD_MIN_ROUNDS 3
@@ -49,7 +55,8 @@ enum QmvMode {
     QMV_ATTN = 4,
     QMV_GLU = 5,
     QMV_FUSED_NOX = 6,
-    QMV_INDEXED_ROUTE = 7
+    QMV_INDEXED_ROUTE = 7,
+    QMV_GLU_RMS = 9
 };
 
 // Activation stage of QMV_ATTN: lane `lane`'s four elements of chunk
@@ -170,15 +177,19 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
         xr = x + (size_t)(m / ix.x_div) * ix.ldx;
         if (ix.w2) n_split = ix.n_split;
     }
-    if constexpr (MODE == QMV_FUSED || MODE == QMV_GLU || MODE == QMV_FUSED_NOX) {
+    constexpr bool IS_FUSED = MODE == QMV_FUSED;
+    constexpr bool IS_GLU = MODE == QMV_GLU || MODE == QMV_GLU_RMS;
+    constexpr bool RMS_CT = MODE == QMV_GLU_RMS;  // (norm, no second input)
+    if constexpr (IS_FUSED || IS_GLU || MODE == QMV_FUSED_NOX) {
         const size_t xo = (size_t)m * ix.ldx;
         xr = x + xo;
-        if (ix.x2) xr2 = ix.x2 + xo;
+        if constexpr (!RMS_CT)
+            if (ix.x2) xr2 = ix.x2 + xo;
     }
-    if constexpr (MODE == QMV_GLU) W2 = ix.w2;  // (n_split stays N: wrow() reads gate rows)
+    if constexpr (IS_GLU) W2 = ix.w2;  // (n_split stays N: wrow() reads gate rows)
     float* yr = y + (size_t)m * ldy;
     uint16_t* yh = reinterpret_cast<uint16_t*>(y) + (size_t)m * ldy;  // QMV_HALF
-    const bool acc_out = (MODE == QMV_FUSED || MODE == QMV_ATTN || MODE == QMV_FUSED_NOX) && ix.accumulate;
+    const bool acc_out = (IS_FUSED || MODE == QMV_ATTN || MODE == QMV_FUSED_NOX) && ix.accumulate;
     auto store = [&](int r, float v) {
         if constexpr (MODE == QMV_HALF) yh[r] = f32_to_f16_rne(v);
         else yr[r] = v;
@@ -208,11 +219,10 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
         apos = __float_as_int(attn_load_early(reinterpret_cast<const float*>(ix.attn_pos)));
         attn_row_load<NW, MAXQ>(x, ix.attn_nsplit, K, w, lane, apre);
     } else if constexpr (QUAD) {
-        if (MODE != QMV_PLAIN && MODE != QMV_FUSED_NOX && xr2)
-            act16_row_load_swiglu<NW, MAXQ4>(xr, xr2, K, w, lane, pre16);
-        else
-            act16_row_load<NW, MAXQ4>(xr, K, w, lane, pre16);
-    } else if (MODE != QMV_PLAIN && MODE != QMV_FUSED_NOX && xr2)
+        act16_row_load<NW, MAXQ4>(xr, K, w, lane, pre16);  // (plain and prologue-free modes only)
+    } else if constexpr (MODE == QMV_PLAIN || MODE == QMV_FUSED_NOX || RMS_CT) {
+        act_row_load<F::ACT, NW, MAXQ>(xr, K, w, lane, pre);
+    } else if (xr2)
         act_row_load_swiglu<F::ACT, NW, MAXQ>(xr, xr2, K, w, lane, pre);
     else
         act_row_load<F::ACT, NW, MAXQ>(xr, K, w, lane, pre);
@@ -223,16 +233,16 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
             act_row_load<F::ACT, NW, MAXQ>(x + (size_t)mi * K, K, w, lane, pre_more[i - 1]);
         }
     }
-    // QMV_FUSED: the RMS gains with the activation row, ahead of the weight
-    // rows.  Loaded after them (in the norm, as the GLU mode still does), the
-    // norm waited for the first weight rows' arrival as well: Q4_K 4096x4096
-    // with the norm 5.28 -> 4.50 us, 4096x8192 6.79 -> 6.21 (the two-matrix
-    // launch and the 32000-row Q6_K one unchanged; the GLU launch measured
-    // 0.08 us slower so).  Without a norm these loads read the activation row
-    // again and are never used.
-    constexpr bool RMS_EARLY = MODE == QMV_FUSED && !QUAD;
+    // The RMS gains with the activation row, ahead of the weight rows (QMV_FUSED
+    // and the compile-time norm modes).  Loaded after them (in the norm, as
+    // the QMV_GLU mode still does), the norm waited for the first weight
+    // rows' arrival as well: Q4_K 4096x4096 with the norm 5.28 -> 4.50 us,
+    // 4096x8192 6.79 -> 6.21.  Without a norm (QMV_FUSED) these loads read
+    // the activation row again and are never used.
+    constexpr bool RMS_EARLY = (MODE == QMV_FUSED || RMS_CT) && !QUAD;
     ActRowPre<RMS_EARLY ? MAXQ : 1> gpre;
-    if constexpr (RMS_EARLY) act_row_gain_load<F::ACT, NW, MAXQ>(ix.rms_gain ? ix.rms_gain : xr, K, w, lane, gpre);
+    if constexpr (RMS_EARLY)
+        act_row_gain_load<F::ACT, NW, MAXQ>(RMS_CT || ix.rms_gain ? ix.rms_gain : xr, K, w, lane, gpre);
     __builtin_amdgcn_sched_barrier(0);  // the activation loads go out ahead of the weight loads
     // Every wavefront's activation loads go out before any weight row of the
     // workgroup is requested: a barrier between them, in the plain and fused
@@ -245,7 +255,7 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
     // from memory behind every CU's weight requests either way, so the
     // barrier only delays the weight stream), the silu input (10.44 -> 11.49
     // us at K = 11008), the GLU mode and the attention merge (unchanged).
-    constexpr bool XBAR = !QUAD && MR == 1 && (MODE == QMV_PLAIN || MODE == QMV_FUSED || MODE == QMV_FUSED_NOX);
+    constexpr bool XBAR = !QUAD && MR == 1 && (MODE == QMV_PLAIN || IS_FUSED || MODE == QMV_FUSED_NOX);
     if constexpr (XBAR) {
         if (!xr2) __builtin_amdgcn_s_barrier();  // (uniform: no silu input)
         __builtin_amdgcn_sched_barrier(0);
@@ -308,17 +318,17 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
         const int rr = RPW > 1 ? row * RPW + rsub : row;
         const int r0 = rr < N ? rr : N - 1;
         qmv_load_row<F, SPL>(wrow(r0), gb, c, KB, ra);
-        if constexpr (MODE == QMV_GLU && SPL <= 2) qmv_load_row<F, SPL>(W2 + (size_t)r0 * row_bytes, gb, c, KB, rb);
+        if constexpr (IS_GLU && SPL <= 2) qmv_load_row<F, SPL>(W2 + (size_t)r0 * row_bytes, gb, c, KB, rb);
         resa = ldres(r0, resa);
     }
     if constexpr (MODE == QMV_ATTN) {
         __builtin_amdgcn_sched_barrier(0);  // the merge's waits come after the first row's loads are out
         attn_row_merge<NW, MAXQ>(apre, ix.attn_nsplit, apos >= 0 && apos < ix.attn_max_ctx, pre);
     }
-    if constexpr ((MODE == QMV_FUSED || MODE == QMV_GLU) && !QUAD) {  // (16-lane rows take neither mode)
+    if constexpr ((IS_FUSED || IS_GLU) && !QUAD) {  // (16-lane rows take none of these modes)
         // rms_norm_last_dim (sum of squares over the whole row, spread over the
         // wavefronts) and the affine gain, before quantization
-        if (ix.rms_gain) {
+        if (RMS_CT || ix.rms_gain) {
             const auto bsum = [&](float v) { return block_sum_waves<NW>(v, s_red, w, lane); };
             if constexpr (RMS_EARLY)
                 act_row_rms_norm<F::ACT, NW, MAXQ>(pre, gpre, ix.rms_eps, K, w, lane, bsum);
@@ -357,7 +367,7 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
         }
     };
 
-    if constexpr (MODE == QMV_GLU && SPL <= 2) {
+    if constexpr (IS_GLU && SPL <= 2) {
         // Two output rows in flight: the gate and up rows of the wavefront's
         // next row (rc, rd, or ra, rb) load while this row's pair is reduced
         // (the pair of the first row was requested before the quantize).
@@ -365,6 +375,26 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
         // wider rows keep the one-row ring below (the four rows' registers
         // would halve occupancy or spill).
         typename F::Raw rc[SPL], rd[SPL];
+        // The outputs are kept in lanes (the wavefront's k-th row in lane k)
+        // and stored after the loop: with a store inside it, whose registers
+        // the next rows' address arithmetic then reused, the compiler waited
+        // for the store -- and so, the counter being in order, for the pair
+        // whose loads were issued before it -- at the top of every
+        // iteration, which left one pair in flight instead of two.  The
+        // launcher splits the rows so that no wavefront has more than 64.
+        if ((N - row + nw - 1) / nw > 64) {  // (never, by the launcher's split)
+            for (int r = row; r < N; r += nw)
+                if (lane == 63) store(r, __builtin_nanf(""));
+            return;
+        }
+        float keep = 0.0f;
+        int kept = 0;
+        const int row0 = row;
+        auto put = [&](float v) {
+            const float t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+            keep = lane == kept ? t : keep;
+            kept++;
+        };
         while (row < N) {
             int nrow = row + nw;
             int lrow = nrow < N ? nrow : row;
@@ -372,20 +402,29 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
             qmv_load_row<F, SPL>(W2 + (size_t)lrow * row_bytes, gi, c, KB, rd);
             float tg = qmv_row<F, SPL>(ra, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
             float tu = qmv_row<F, SPL>(rb, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
-            if (lane == 63) store(row, silu_mul(tg, tu));
+            qmv_settle_row<F, SPL>(ra);
+            qmv_settle_row<F, SPL>(rb);
+            put(silu_mul(tg, tu));
             row = nrow;
-            if (row >= N) break;
+            if (row >= N) {  // (the re-issued pair settled too: the exit joins the loop's back edge)
+                qmv_settle_row<F, SPL>(rc);
+                qmv_settle_row<F, SPL>(rd);
+                break;
+            }
             nrow = row + nw;
             lrow = nrow < N ? nrow : row;
             qmv_load_row<F, SPL>(W + (size_t)lrow * row_bytes, gi, c, KB, ra);
             qmv_load_row<F, SPL>(W2 + (size_t)lrow * row_bytes, gi, c, KB, rb);
             tg = qmv_row<F, SPL>(rc, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
             tu = qmv_row<F, SPL>(rd, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
-            if (lane == 63) store(row, silu_mul(tg, tu));
+            qmv_settle_row<F, SPL>(rc);
+            qmv_settle_row<F, SPL>(rd);
+            put(silu_mul(tg, tu));
             row = nrow;
         }
+        if (lane < kept) store(row0 + lane * nw, keep);
         return;
-    } else if constexpr (MODE == QMV_GLU) {
+    } else if constexpr (IS_GLU) {
         // The ring alternates gate row r (ra) and up row r (rb): the up row's
         // loads are in flight while the gate row is reduced, the next gate
         // row's while the up row is.
@@ -527,6 +566,21 @@ hipError_t launch_qmv_wg(const uint8_t* w, const float* x, float* y, int M, int 
     const int gx = need < cap ? need : cap;
     QmvOpts o = ix;
     o.rows = M;
+    constexpr bool GLU = MODE == QMV_GLU || MODE == QMV_GLU_RMS;
+    const int chunk = 64 * gx * NW;  // (the GLU ring keeps at most 64 rows a wavefront)
+    if (GLU && N > chunk) {
+        const size_t row_bytes = (size_t)(K / F::ELEMS) * F::BYTES;
+        for (int r0 = 0; r0 < N; r0 += chunk) {
+            QmvOpts oc = o;
+            oc.w2 = o.w2 + (size_t)r0 * row_bytes;
+            const int n = N - r0 < chunk ? N - r0 : chunk;
+            hipLaunchKernelGGL((qmv_kernel<F, SPL, WG, MODE, RPW, MR>), dim3(gx, gy), dim3(WG), lds, s,
+                               w + (size_t)r0 * row_bytes, x, y + r0, n, K, ldy, oc);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     hipLaunchKernelGGL((qmv_kernel<F, SPL, WG, MODE, RPW, MR>), dim3(gx, gy), dim3(WG), lds, s, w, x, y, N, K, ldy, o);
     return hipGetLastError();
 }
@@ -536,10 +590,11 @@ hipError_t launch_qmv(const uint8_t* w, const float* x, float* y, int M, int N, 
                       hipStream_t s, int num_cus) {
     // (the GLU mode reduces two rows per output: at most 512 threads there)
     constexpr int WGN0 = qmv_wg<F, SPL>(), WGB0 = qmv_wg_big<F, SPL>();
-    constexpr int WGN = MODE == QMV_GLU && WGN0 > 512 ? 512 : WGN0;
-    constexpr int WGB = MODE == QMV_GLU && WGB0 > 512 ? 512 : WGB0;
+    constexpr bool GLU = MODE == QMV_GLU || MODE == QMV_GLU_RMS;
+    constexpr int WGN = GLU && WGN0 > 512 ? 512 : WGN0;
+    constexpr int WGB = GLU && WGB0 > 512 ? 512 : WGB0;
     // short rows (at most 8 of a wavefront step's 16 block slots): 2 or 4 rows per step
-    if constexpr (SPL == 1 && 64 / F::LPB == 16 && MODE != QMV_GLU && MODE != QMV_ATTN) {
+    if constexpr (SPL == 1 && 64 / F::LPB == 16 && !GLU && MODE != QMV_ATTN) {
         const int KB = K / F::ELEMS;
         if (KB <= 4) return launch_qmv_wg<F, 1, WGN, MODE, 4>(w, x, y, M, N, K, ldy, ix, s, num_cus);
         if (KB <= 8) return launch_qmv_wg<F, 1, WGN, MODE, 2>(w, x, y, M, N, K, ldy, ix, s, num_cus);
@@ -602,6 +657,17 @@ hipError_t launch_dtype(int dtype, const uint8_t* w, const float* x, float* y, i
         case GGML_Q4K: return launch_fmt<Q4K, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
         case GGML_Q6K: return launch_fmt<Q6K, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
         case GGML_Q8_0: return launch_fmt<Q80, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// The k-quant formats only (the compile-time norm modes).
+template <int MODE>
+hipError_t launch_dtype_kq(int dtype, const uint8_t* w, const float* x, float* y, int M, int N, int K, int ldy,
+                           const QmvOpts& ix, hipStream_t s, int num_cus) {
+    switch (dtype) {
+        case GGML_Q4K: return launch_fmt<Q4K, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
+        case GGML_Q6K: return launch_fmt<Q6K, MODE>(w, x, y, M, N, K, ldy, ix, s, num_cus);
         default: return hipErrorInvalidValue;
     }
 }
@@ -787,6 +853,8 @@ hipError_t launch_qmv_glu(int dtype, const uint8_t* w_gate, const uint8_t* w_up,
     QmvOpts g = o;
     g.w2 = w_up;
     g.accumulate = 0;
+    if (g.rms_gain && !g.x2 && dtype != GGML_Q8_0)
+        return launch_dtype_kq<QMV_GLU_RMS>(dtype, w_gate, x, y, M, N, K, ldy, g, s, num_cus);
     return launch_dtype<QMV_GLU>(dtype, w_gate, x, y, M, N, K, ldy, g, s, num_cus);
 }
 

@@ -6,6 +6,7 @@
 #include "common.hpp"
 #include "formats.hpp"
 
+
 namespace frq {
 
 // Workgroup size for many rows: 1024 threads while a row's raw weight
@@ -36,10 +37,44 @@ template <class F, int SPL>
 __device__ __forceinline__ void qmv_load_row(const uint8_t* __restrict__ wr, int gi, int c, int KB,
                                              typename F::Raw (&r)[SPL]) {
     constexpr int BPW = 64 / F::LPB;
+    if constexpr (F::BUF && SPL >= 3) {
+        // Rows of three or more slots (K > 8192) through a buffer resource of
+        // the row: a scalar base, 32-bit vector offsets that stay the same
+        // from row to row, no vector address arithmetic per row (Q4_K
+        // 11008x4096 8.55 -> 8.38 us, 4096 rows of K = 12288 9.06 -> 8.90;
+        // for one-slot rows it measured slower: 4096x11008 6.74 -> 7.2-7.4,
+        // 4096x32000 14.27 -> 14.6-14.7).  The row's size is the record
+        // count, so a stray offset reads zeros, not another row; word 3 as
+        // gfx9 raw buffers take it.
+        const __amdgpu_buffer_rsrc_t R =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(wr), (short)0, KB * F::BYTES, 0x00020000);
+#pragma unroll
+        for (int s = 0; s < SPL; s++) {
+            const int b = gi + BPW * s;
+            F::load_buf(R, (uint32_t)((b < KB ? b : KB - 1) * F::BYTES), c, r[s]);
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < SPL; s++) {
+            const int b = gi + BPW * s;
+            F::load(wr + (size_t)(b < KB ? b : KB - 1) * F::BYTES, c, r[s]);
+        }
+    }
+}
+
+// Marks a row's raw registers as used on every path.  qmv_row skips a slot
+// past the row's end with a branch, so after it the compiler counts that
+// slot's loads as possibly still in flight, and a ring that reuses the
+// registers then waits for everything issued after them (the whole next row)
+// before its next loads.  Used after the loads were consumed, this costs no
+// instruction and no wait.
+template <class F, int SPL>
+__device__ __forceinline__ void qmv_settle_row(const typename F::Raw (&r)[SPL]) {
 #pragma unroll
     for (int s = 0; s < SPL; s++) {
-        const int b = gi + BPW * s;
-        F::load(wr + (size_t)(b < KB ? b : KB - 1) * F::BYTES, c, r[s]);
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(&r[s]);
+#pragma unroll
+        for (int i = 0; i < (int)(sizeof(typename F::Raw) / 4); i++) asm volatile("" ::"v"(p[i]));
     }
 }
 

@@ -76,11 +76,13 @@ def test_qmatmul_fused_swiglu_residual(dev, dt, n, ffn):
 
 
 @pytest.mark.parametrize("dt,n,k,m,rms", [(O.Q4K, 11008, 4096, 1, True), (O.Q6K, 1000, 2048, 2, True),
-                                          (O.Q8_0, 300, 1024, 3, False), (O.Q4K, 513, 4096, 1, False)])
+                                          (O.Q8_0, 300, 1024, 3, False), (O.Q4K, 513, 4096, 1, False),
+                                          (O.Q4K, 270000, 256, 1, True)])
 def test_qmatmul_fused_glu(dev, dt, n, k, m, rms):
     """silu(gate . a) * (up . a) in one launch: the gate and up sums are the
     fused mat-vec's own (bit-identical), the product is silu_mul's; and the
-    CPU path (QMatMul gate and up, SiLU·mul) within 1e-3 of its norm."""
+    CPU path (QMatMul gate and up, SiLU·mul) within 1e-3 of its norm.  (270000
+    rows: more than 64 a wavefront, which the launcher splits over launches.)"""
     say("fused glu", dt, n, k, m, rms)
     wg = O.quantize(dt, O.normal((n, k), seed=n + k, stream=1, std=0.02))
     wu = O.quantize(dt, O.normal((n, k), seed=n + k, stream=2, std=0.02))
