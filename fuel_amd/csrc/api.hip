@@ -113,12 +113,29 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // row, which costs more than the tiles' partly empty rows once there are many
 // columns (4096x32000: M = 16 36.3 -> 31.1 us, M = 32 56.4 -> 33.6 us;
 // 4096x11008 M = 32 28.3 -> 21.3 us; at N = 4096 the skinny kernel stays
-// faster, 12.7 against 15.0 us at M = 32).
+// faster, 12.7 against 15.0 us at M = 32).  Q4_K at a 16-byte aligned base
+// (the wide-tile kernel) goes further: rows of at least MMQ_LONG_K elements
+// from MMQ_LONG_MIN_ROWS rows (a K split: 11008x4096 M = 24 17.1 -> 15.5 us,
+// M = 32 19.9 -> 15.6; at 16 rows the skinny kernel stays faster, 12.0
+// against 14.5 us), and shorter rows of >= MMQ_WIDE_N columns from
+// MMQ_FEW_MIN_ROWS rows (16-row tiles: 4096x11008 M = 8 15.7 -> 13.4 us,
+// 4096x32000 M = 8 29.3 -> 19.8, quantize launch included) -- from
+// MMQ_FEW_MIN_ROWS_XL rows with >= MMQ_XL_N columns, where they also beat
+// the 4-row mat-vec (4096x32000 M = 4 23.8 -> 20.1 us; at 2 rows the
+// mat-vec stays, 16.8 against about 18.5).
 constexpr size_t MMQ_MIN_ROWS = 33;
 constexpr size_t MMQ_WIDE_MIN_ROWS = 16;
 constexpr size_t MMQ_WIDE_N = 8192;
-bool tiled_rows(size_t rows, size_t n) {
-    return rows >= MMQ_MIN_ROWS || (rows >= MMQ_WIDE_MIN_ROWS && n >= MMQ_WIDE_N);
+constexpr size_t MMQ_LONG_MIN_ROWS = 24;
+constexpr size_t MMQ_LONG_K = 8192;
+constexpr size_t MMQ_FEW_MIN_ROWS = 5;
+constexpr size_t MMQ_FEW_MIN_ROWS_XL = 3;
+constexpr size_t MMQ_XL_N = 16384;
+bool tiled_rows(int t, const void* w, size_t rows, size_t n, size_t k) {
+    if (rows >= MMQ_MIN_ROWS || (rows >= MMQ_WIDE_MIN_ROWS && n >= MMQ_WIDE_N)) return true;
+    if (t != GGML_Q4K || ((uintptr_t)w & 15u) != 0) return false;
+    if (k >= MMQ_LONG_K) return rows >= MMQ_LONG_MIN_ROWS;
+    return n >= MMQ_WIDE_N && (rows >= MMQ_FEW_MIN_ROWS || (rows >= MMQ_FEW_MIN_ROWS_XL && n >= MMQ_XL_N));
 }
 
 // Byte size of the quantized-activation workspace for rows x k.
@@ -262,7 +279,7 @@ int plan_qmatmul(const frq_device* dev, int t, const uint8_t* w, size_t rows, si
         return fail(FRQ_UNSUPPORTED, "qmatmul: k=%zu exceeds %zu for dtype %d", k, kmax, t);
     // the tiled MFMA kernel addresses the weights with 32-bit offsets
     const bool w32 = n * (k / block_elems(t)) * type_size(t) <= 0xffffffffull;
-    if (tiled_rows(rows, n) && mmq_supported(t) && w32) {
+    if (tiled_rows(t, w, rows, n, k) && mmq_supported(t) && w32) {
         // many activation rows: quantize them once, then the int8-MFMA GEMM;
         // scratch: quantized rows, then the split-K partial sums the plan
         // needs (a fixed scratch region lowers the split until they fit)
@@ -343,7 +360,7 @@ bool fused_batch_plan(frq_device* dev, int t, const void* w, const ActSrc& src, 
     if (rows < 2 || vec_dot_type(t) != GGML_Q8K || k > (size_t)0x7fffffff || !quantize_src_supported(src, (int)k))
         return false;
     const bool w32 = n * (k / block_elems(t)) * type_size(t) <= 0xffffffffull;
-    if (tiled_rows(rows, n) && mmq_supported(t) && w32) {
+    if (tiled_rows(t, w, rows, n, k) && mmq_supported(t) && w32) {
         fb->mmq = true;
         fb->plan = mmq_plan(t, w, (int)rows, (int)n, (int)k, dev->num_cus);
     } else if (mmq_skinny_supported(t, (int)k)) {
@@ -381,7 +398,7 @@ int run_qmatmul_f16(frq_device* dev, int t, const uint8_t* w, const uint16_t* x,
     if (k > kmax && !skinny)
         return fail(FRQ_UNSUPPORTED, "qmatmul_f16: k=%zu exceeds %zu for dtype %d", k, kmax, t);
     const bool w32 = n * (k / block_elems(t)) * type_size(t) <= 0xffffffffull;
-    if (tiled_rows(rows, n) && mmq_supported(t) && w32) {
+    if (tiled_rows(t, w, rows, n, k) && mmq_supported(t) && w32) {
         const MmqPlan plan = mmq_plan(t, w, (int)rows, (int)n, (int)k, dev->num_cus);
         const size_t abytes = align256(act_bytes(GGML_Q8K, rows, k));
         int rc = ensure_ws(dev, abytes + plan.part_elems * sizeof(float));

@@ -1236,6 +1236,7 @@ enum MmqKind {
     MMQ_Q4K_WIDE32,    // 32 x 64, the wide-tile kernel with four wavefronts (grids of few 64 x 128 tiles)
     MMQ_Q4K_WIDE_KG2,    // 64 x 128, two groups of eight wavefronts splitting K inside the workgroup
     MMQ_Q4K_WIDE32_KG2,  // 32 x 64, two groups of four wavefronts
+    MMQ_Q4K_WIDE16_KG2,  // 16 x 64, two groups of four wavefronts
 };
 
 #define FRQ_MMQ_KINDS(X)                          \
@@ -1303,18 +1304,41 @@ MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus, siz
     //   4096x11008 M = 64 25.2 -> 20.1, M = 128 27.5 -> 26.1, M = 160 38.4 ->
     //   31.4; 11008x4096 M = 64 22.3 -> 19.4 (graph replays, weights rotated
     //   over 1.2 GB, split-K reduce included).
-    if (dma && M >= 33) {
+    // 16-32 rows (tiled on >= 8192 columns, and on rows of >= 8192 elements
+    // from 24 rows): the 32 x 64 tiles, or 16 x 64 at 16 rows -- long rows
+    // with a K split of up to four (11008x4096 M = 24 17.1 -> 15.5 us, M = 32
+    // 19.9 -> 15.6 against the skinny kernel), two wavefront groups while the
+    // tiles fit one per CU (4096x11008 M = 16 15.4 -> 12.0 us, M = 24 16.2 ->
+    // 13.5, M = 32 16.6 -> 14.1; a K split in memory measured slower there),
+    // one group above (4096x32000 M = 24 26.8 -> 21.6, M = 32 27.6 -> 23.4;
+    // 16 x 64 tiles with two groups at M = 16 27.1 -> 18.6 us) -- against the
+    // 32 x 64 plane kernel (graph replays, weights rotated over 1.2 GB, split-K
+    // reduce included).  The 16 x 64 tiles also take 3-15 rows of >= 8192
+    // columns (the caller's row rule): 4096x32000 M = 4 16.3 us, M = 8 16.8,
+    // M = 12 17.4 against 27 us for the 32 x 64 plane kernel.
+    if (dma && M >= 2) {
         using T8 = WideTile<4, 1, 8>;
         using T4 = WideTile<2, 1, 4>;
         const int KB = K / QK_K, C = num_cus;
         const bool long_rows = K >= 32 * QK_K;
         const int t8 = ((M + T8::BM - 1) / T8::BM) * ((N + T8::BN - 1) / T8::BN);
+        const int t4 = ((M + T4::BM - 1) / T4::BM) * ((N + T4::BN - 1) / T4::BN);
         auto clamp_ks = [&](int ks) {
             if (ks > 4) ks = 4;
             if (ks > KB / 2) ks = KB / 2;
             return ks > 1 ? ks : 1;
         };
-        if (long_rows && M >= 128 && t8 < 4 * C / 5) {
+        if (M <= 32) {
+            p.ks = 1;
+            if (long_rows) {
+                p.kind = MMQ_Q4K_WIDE32;
+                p.ks = clamp_ks((3 * C + t4 - 1) / t4);
+            } else if (M <= 16) {
+                p.kind = MMQ_Q4K_WIDE16_KG2;
+            } else {
+                p.kind = t4 <= C ? MMQ_Q4K_WIDE32_KG2 : MMQ_Q4K_WIDE32;
+            }
+        } else if (long_rows && M >= 128 && t8 < 4 * C / 5) {
             const int occ = kernel_occupancy<mmq_q4k_wide_kernel<4, 1, 8>, T8::NT>();
             p.kind = MMQ_Q4K_WIDE;
             p.ks = clamp_ks(occ * C / t8);
@@ -1325,7 +1349,6 @@ MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus, siz
             p.kind = MMQ_Q4K_WIDE;
             p.ks = 1;
         } else {
-            const int t4 = ((M + T4::BM - 1) / T4::BM) * ((N + T4::BN - 1) / T4::BN);
             p.kind = MMQ_Q4K_WIDE32;
             if (long_rows) {
                 p.ks = clamp_ks((3 * C + t4 - 1) / t4);
@@ -1367,6 +1390,8 @@ hipError_t launch_mmq(const MmqPlan& plan, int dtype, const uint8_t* w, ActView 
         case MMQ_Q4K_WIDE_KG2: return launch_wide<4, 1, 8, 2>(w, act, y, M, N, K, ldy, s, out_mode, plan.ks, part);
         case MMQ_Q4K_WIDE32_KG2:
             return launch_wide<2, 1, 4, 2>(w, act, y, M, N, K, ldy, s, out_mode, plan.ks, part);
+        case MMQ_Q4K_WIDE16_KG2:
+            return launch_wide<1, 1, 4, 2>(w, act, y, M, N, K, ldy, s, out_mode, plan.ks, part);
         default: return hipErrorInvalidValue;
     }
 }

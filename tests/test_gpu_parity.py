@@ -125,7 +125,9 @@ def test_qmatmul_small_batch(dev, dt, m, k, n):
     workgroup's wavefronts) or the mat-vec with several rows per workgroup —
     2 rows of the k-quants with K <= 4096 and 3-4 rows of wide ones (the
     8200- and 9001-column cases); Q8_0 at K = 4096 with 2-4 rows, and 5-8 rows
-    of wide matrices in two row groups: within the tolerance of the oracle,
+    of wide matrices in two row groups; Q4_K (16-byte aligned) on the wide-tile
+    int8-MFMA kernel for 5+ rows of >= 8192 columns and 24+ rows of 11008
+    elements: within the tolerance of the oracle,
     and independent of the other rows of the batch: the same rows in another
     order give every row the same bits."""
     say("small batch", dt, m, k, n)
