@@ -122,7 +122,11 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // 4096x32000 M = 8 29.3 -> 19.8, quantize launch included) -- from
 // MMQ_FEW_MIN_ROWS_XL rows with >= MMQ_XL_N columns, where they also beat
 // the 4-row mat-vec (4096x32000 M = 4 23.8 -> 20.1 us; at 2 rows the
-// mat-vec stays, 16.8 against about 18.5).
+// mat-vec stays, 16.8 against about 18.5).  Q6_K takes its wide-tile kernel
+// from MMQ_FEW_MIN_ROWS rows on matrices of >= MMQ_Q6K_WIDE_N columns and
+// rows shorter than MMQ_LONG_K (4096x32000 M = 8 40.7 -> 32.7 us; with
+// fewer columns its 16 x 64 tiles leave the chip short and the skinny kernel
+// stays).
 constexpr size_t MMQ_MIN_ROWS = 33;
 constexpr size_t MMQ_WIDE_MIN_ROWS = 16;
 constexpr size_t MMQ_WIDE_N = 8192;
@@ -131,8 +135,10 @@ constexpr size_t MMQ_LONG_K = 8192;
 constexpr size_t MMQ_FEW_MIN_ROWS = 5;
 constexpr size_t MMQ_FEW_MIN_ROWS_XL = 3;
 constexpr size_t MMQ_XL_N = 16384;
+constexpr size_t MMQ_Q6K_WIDE_N = 24576;
 bool tiled_rows(int t, const void* w, size_t rows, size_t n, size_t k) {
     if (rows >= MMQ_MIN_ROWS || (rows >= MMQ_WIDE_MIN_ROWS && n >= MMQ_WIDE_N)) return true;
+    if (t == GGML_Q6K) return rows >= MMQ_FEW_MIN_ROWS && n >= MMQ_Q6K_WIDE_N && k < MMQ_LONG_K;
     if (t != GGML_Q4K || ((uintptr_t)w & 15u) != 0) return false;
     if (k >= MMQ_LONG_K) return rows >= MMQ_LONG_MIN_ROWS;
     return n >= MMQ_WIDE_N && (rows >= MMQ_FEW_MIN_ROWS || (rows >= MMQ_FEW_MIN_ROWS_XL && n >= MMQ_XL_N));

@@ -1237,6 +1237,8 @@ enum MmqKind {
     MMQ_Q4K_WIDE_KG2,    // 64 x 128, two groups of eight wavefronts splitting K inside the workgroup
     MMQ_Q4K_WIDE32_KG2,  // 32 x 64, two groups of four wavefronts
     MMQ_Q4K_WIDE16_KG2,  // 16 x 64, two groups of four wavefronts
+    MMQ_Q6K_WIDE16,      // 16 x 64, the Q6_K wide-tile kernel with four wavefronts
+    MMQ_Q6K_WIDE32,      // 32 x 64, the same
 };
 
 #define FRQ_MMQ_KINDS(X)                          \
@@ -1364,6 +1366,15 @@ MmqPlan mmq_plan(int dtype, const void* w, int M, int N, int K, int num_cus, siz
     // Q6_K from 128 rows without a K split, or from 33 rows when its 64 x 128
     // tiles fill 0.8-1 workgroups per CU (4096x32000 at M = 33-64: 64 -> 40 us
     // against the 32-row plane tiles): the wide-tile kernel
+    // Q6_K at 5-32 rows of >= 24576 columns and rows of < 8192 elements (the
+    // caller's row rule): 16 x 64 or 32 x 64 wide tiles of four wavefronts, no
+    // K split -- 4096x32000 M = 8 35.9 -> 30.8 us, M = 16 35.8 -> 30.5, M = 32
+    // 35.9 -> 34.5 against the 32 x 64 plane kernel, 40.0 / 44.2 / 67.2 on
+    // the skinny kernel (graph replays, weights rotated over 1.2 GB)
+    if (dtype == GGML_Q6K && M <= 32 && N >= 24576 && K < 32 * QK_K) {
+        p.kind = M <= 16 ? MMQ_Q6K_WIDE16 : MMQ_Q6K_WIDE32;
+        p.ks = 1;
+    }
     if (dtype == GGML_Q6K && M >= 33) {
         using T6 = WideTile6<4, 8>;
         const int t8 = ((M + T6::BM - 1) / T6::BM) * ((N + T6::BN - 1) / T6::BN);
@@ -1392,6 +1403,8 @@ hipError_t launch_mmq(const MmqPlan& plan, int dtype, const uint8_t* w, ActView 
             return launch_wide<2, 1, 4, 2>(w, act, y, M, N, K, ldy, s, out_mode, plan.ks, part);
         case MMQ_Q4K_WIDE16_KG2:
             return launch_wide<1, 1, 4, 2>(w, act, y, M, N, K, ldy, s, out_mode, plan.ks, part);
+        case MMQ_Q6K_WIDE16: return launch_wide6<1, 4>(w, act, y, M, N, K, ldy, s, out_mode);
+        case MMQ_Q6K_WIDE32: return launch_wide6<2, 4>(w, act, y, M, N, K, ldy, s, out_mode);
         default: return hipErrorInvalidValue;
     }
 }

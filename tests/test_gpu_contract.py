@@ -204,26 +204,29 @@ def test_wide_tiles_long_rows_k_split(dev, m):
     assert err16 <= TOL_F16
 
 
-@pytest.mark.parametrize("m,k,n", [(3, 4096, 32000), (4, 4096, 16400), (8, 4096, 11008), (13, 4096, 11008),
-                                   (16, 4096, 11008), (20, 4096, 11008), (28, 4096, 32000), (24, 11008, 4096),
-                                   (29, 11008, 4096)])
-def test_wide_tiles_3_to_32_rows(dev, m, k, n):
+@pytest.mark.parametrize("dt,m,k,n", [(O.Q4K, 3, 4096, 32000), (O.Q4K, 4, 4096, 16400), (O.Q4K, 8, 4096, 11008),
+                                      (O.Q4K, 13, 4096, 11008), (O.Q4K, 16, 4096, 11008), (O.Q4K, 20, 4096, 11008),
+                                      (O.Q4K, 28, 4096, 32000), (O.Q4K, 24, 11008, 4096), (O.Q4K, 29, 11008, 4096),
+                                      (O.Q6K, 5, 4096, 32000), (O.Q6K, 16, 4096, 32000), (O.Q6K, 27, 2048, 25000)])
+def test_wide_tiles_3_to_32_rows(dev, dt, m, k, n):
     """Q4_K at 3-32 rows on the wide-tile kernel: 16 x 64 tiles with two
     wavefront groups (3-16 rows, ragged columns at 16400), 32 x 64 tiles with
     and without them (ragged rows), and rows of 11008 elements from 24 rows
-    with a K split; f32 and f16 outputs against the oracle."""
-    wq = O.quantize(O.Q4K, O.normal((n, k), seed=13, stream=m, std=0.02))
+    with a K split; Q6_K at 5-32 rows of >= 24576 columns on its wide-tile
+    kernel in 16 x 64 and 32 x 64 tiles (ragged rows and columns); f32 and
+    f16 outputs against the oracle."""
+    wq = O.quantize(dt, O.normal((n, k), seed=13, stream=m, std=0.02))
     x = O.normal((m, k), seed=14, stream=m)
-    qs = dev.load_quantized(O.Q4K, wq.tobytes())
-    path, kind, ks = F.qmatmul_plan(dev, O.Q4K, m, n, k, qs.device_ptr())
-    say("wide tiles m", m, "k", k, "n", n, "plan", path, kind, ks)
+    qs = dev.load_quantized(dt, wq.tobytes())
+    path, kind, ks = F.qmatmul_plan(dev, dt, m, n, k, qs.device_ptr())
+    say("wide tiles dt", dt, "m", m, "k", k, "n", n, "plan", path, kind, ks)
     assert path == "tiled_mfma"
     y, _ = qs.fwd((n, k), dev.from_numpy(x))
-    err = rel_err(y.numpy(), O.matmul(O.Q4K, x, wq))
+    err = rel_err(y.numpy(), O.matmul(dt, x, wq))
     say("  rel_err", err)
     assert err <= TOL
     x16 = O.f32_to_f16_bits(x)
     y16, _ = qs.fwd((n, k), dev.from_numpy(x16.view(np.float16)))
-    err16 = rel_err(O.f16_bits_to_f32(y16.numpy().view(np.uint16)), O.f16_bits_to_f32(O.matmul_f16(O.Q4K, x16, wq)))
+    err16 = rel_err(O.f16_bits_to_f32(y16.numpy().view(np.uint16)), O.f16_bits_to_f32(O.matmul_f16(dt, x16, wq)))
     say("  f16 rel_err", err16)
     assert err16 <= TOL_F16
