@@ -126,7 +126,10 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // from MMQ_FEW_MIN_ROWS rows on matrices of >= MMQ_Q6K_WIDE_N columns and
 // rows shorter than MMQ_LONG_K (4096x32000 M = 8 40.7 -> 32.7 us; with
 // fewer columns its 16 x 64 tiles leave the chip short and the skinny kernel
-// stays).
+// stays), and its 32-row plane tiles with a K split on rows of >= MMQ_LONG_K
+// elements from MMQ_LONG_MIN_ROWS rows (11008x4096 M = 32 26.4 -> 22.0 us
+// against the skinny kernel, quantize launch excluded; 21.2 against 19.7 at
+// 16 rows).
 constexpr size_t MMQ_MIN_ROWS = 33;
 constexpr size_t MMQ_WIDE_MIN_ROWS = 16;
 constexpr size_t MMQ_WIDE_N = 8192;
@@ -138,7 +141,8 @@ constexpr size_t MMQ_XL_N = 16384;
 constexpr size_t MMQ_Q6K_WIDE_N = 24576;
 bool tiled_rows(int t, const void* w, size_t rows, size_t n, size_t k) {
     if (rows >= MMQ_MIN_ROWS || (rows >= MMQ_WIDE_MIN_ROWS && n >= MMQ_WIDE_N)) return true;
-    if (t == GGML_Q6K) return rows >= MMQ_FEW_MIN_ROWS && n >= MMQ_Q6K_WIDE_N && k < MMQ_LONG_K;
+    if (t == GGML_Q6K)
+        return k < MMQ_LONG_K ? rows >= MMQ_FEW_MIN_ROWS && n >= MMQ_Q6K_WIDE_N : rows >= MMQ_LONG_MIN_ROWS;
     if (t != GGML_Q4K || ((uintptr_t)w & 15u) != 0) return false;
     if (k >= MMQ_LONG_K) return rows >= MMQ_LONG_MIN_ROWS;
     return n >= MMQ_WIDE_N && (rows >= MMQ_FEW_MIN_ROWS || (rows >= MMQ_FEW_MIN_ROWS_XL && n >= MMQ_XL_N));

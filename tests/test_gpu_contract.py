@@ -207,14 +207,16 @@ def test_wide_tiles_long_rows_k_split(dev, m):
 @pytest.mark.parametrize("dt,m,k,n", [(O.Q4K, 3, 4096, 32000), (O.Q4K, 4, 4096, 16400), (O.Q4K, 8, 4096, 11008),
                                       (O.Q4K, 13, 4096, 11008), (O.Q4K, 16, 4096, 11008), (O.Q4K, 20, 4096, 11008),
                                       (O.Q4K, 28, 4096, 32000), (O.Q4K, 24, 11008, 4096), (O.Q4K, 29, 11008, 4096),
-                                      (O.Q6K, 5, 4096, 32000), (O.Q6K, 16, 4096, 32000), (O.Q6K, 27, 2048, 25000)])
+                                      (O.Q6K, 5, 4096, 32000), (O.Q6K, 16, 4096, 32000), (O.Q6K, 27, 2048, 25000),
+                                      (O.Q6K, 26, 11008, 4096)])
 def test_wide_tiles_3_to_32_rows(dev, dt, m, k, n):
     """Q4_K at 3-32 rows on the wide-tile kernel: 16 x 64 tiles with two
     wavefront groups (3-16 rows, ragged columns at 16400), 32 x 64 tiles with
     and without them (ragged rows), and rows of 11008 elements from 24 rows
     with a K split; Q6_K at 5-32 rows of >= 24576 columns on its wide-tile
-    kernel in 16 x 64 and 32 x 64 tiles (ragged rows and columns); f32 and
-    f16 outputs against the oracle."""
+    kernel in 16 x 64 and 32 x 64 tiles (ragged rows and columns), and rows of
+    11008 elements from 24 rows on the 32-row plane tiles with a K split; f32
+    and f16 outputs against the oracle."""
     wq = O.quantize(dt, O.normal((n, k), seed=13, stream=m, std=0.02))
     x = O.normal((m, k), seed=14, stream=m)
     qs = dev.load_quantized(dt, wq.tobytes())
