@@ -445,20 +445,34 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
         // lane stores its row
         const int ng = (N + RPW - 1) / RPW;
         const bool seg_last = (lane & (64 / RPW - 1)) == 64 / RPW - 1;
-        while (row < ng) {
+        // (a wavefront's last group issues no further loads, as below: Q4_K
+        // 2048x12288 5.16 -> 5.00 us, 768x2048 2.82 -> 2.77; the MoE layer
+        // unchanged)
+        auto finish = [&](const typename F::Raw(&r)[SPL], float res, int g) {
+            const float t = qmv_row<F, SPL, RPW>(r, s_qs, lay.qstride, s_d, s_bs, gb, c, KB);
+            const int my = g * RPW + rsub;
+            if (seg_last && my < N) store(my, acc_out ? res + t : t);
+        };
+        if (row >= ng) return;
+        while (true) {
             int ngrp = row + nw;
-            int lg = ngrp < ng ? ngrp : row;
-            int lr = lg * RPW + rsub < N ? lg * RPW + rsub : N - 1;
+            if (ngrp >= ng) {
+                finish(ra, resa, row);
+                return;
+            }
+            int lr = ngrp * RPW + rsub < N ? ngrp * RPW + rsub : N - 1;
             resb = ldres(lr, resb);
             qmv_load_row<F, SPL>(wrow(lr), gb, c, KB, rb);
             float t = qmv_row<F, SPL, RPW>(ra, s_qs, lay.qstride, s_d, s_bs, gb, c, KB);
             int my = row * RPW + rsub;
             if (seg_last && my < N) store(my, acc_out ? resa + t : t);
             row = ngrp;
-            if (row >= ng) break;
             ngrp = row + nw;
-            lg = ngrp < ng ? ngrp : row;
-            lr = lg * RPW + rsub < N ? lg * RPW + rsub : N - 1;
+            if (ngrp >= ng) {
+                finish(rb, resb, row);
+                return;
+            }
+            lr = ngrp * RPW + rsub < N ? ngrp * RPW + rsub : N - 1;
             resa = ldres(lr, resa);
             qmv_load_row<F, SPL>(wrow(lr), gb, c, KB, ra);
             t = qmv_row<F, SPL, RPW>(rb, s_qs, lay.qstride, s_d, s_bs, gb, c, KB);
@@ -466,7 +480,6 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
             if (seg_last && my < N) store(my, acc_out ? resb + t : t);
             row = ngrp;
         }
-        return;
     }
     // Two-row ring: the next row's loads are in flight while a row is
     // reduced.  A wavefront's last row issues no further loads (a
