@@ -296,13 +296,15 @@ def test_attention_decode_sequence(dev):
 @pytest.mark.parametrize("H,max_ctx,pos,dt,n", [(32, 768, 700, O.Q4K, 4096), (32, 1024, 0, O.Q6K, 4096),
                                                  (32, 768, 768, O.Q4K, 4096), (2, 64, 0, O.Q6K, 300),
                                                  (2, 2048, 1500, O.Q8_0, 512), (4, 1024, 1023, O.Q4K, 1000),
-                                                 (2, 64, 64, O.Q4K, 256)])
+                                                 (2, 64, 64, O.Q4K, 256), (64, 512, 300, O.Q4K, 1000),
+                                                 (128, 256, 100, O.Q6K, 512)])
 def test_attention_decode_oproj(dev, H, max_ctx, pos, dt, n):
     """Attention + o-projection + residual equals frq_attention_decode then
     the fused QMatMul with accumulate, bit for bit (same caches, appends and
-    outputs): 8 splits (32 heads: the merge inside the mat-vec, two
-    launches), 64 and 128 splits (the merge kernel into the workspace tail),
-    and an out-of-range pos (NaN attention, no append) on both paths."""
+    outputs): 8, 4 and 2 splits (32, 64 and 128 heads: the merge inside the
+    mat-vec, two launches), 64 and 128 splits (the merge kernel into the
+    workspace tail), and an out-of-range pos (NaN attention, no append) on
+    both paths."""
     say("attention oproj", H, max_ctx, pos, dt, n)
     k = H * 128
     rng = np.random.default_rng(pos + H)
