@@ -376,10 +376,26 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
         }
     }
     __syncthreads();
+    // With one activation row the lane's activation slices are the same for
+    // every weight row: the GLU ring (rows of one or two slots) and Q8_0 rows
+    // of up to four slots read them from LDS once and keep them in registers
+    // (GLU 4096x22016 11.80 -> 11.45 us, Q8_0 4096x4096 5.91 -> 5.76,
+    // 2048x8192 5.90 -> 5.64).  Elsewhere it measured slower, the compiler
+    // scheduling the rows' loads and waits differently around them (Q4_K
+    // 4096x11008 6.65 -> 7.05 us, fused RMS 4096x8192 6.03 -> 6.87, Q6_K
+    // 4096x32000 21.6 -> 22.4; rows of three slots twice as slow).
+    constexpr bool XREG = MR == 1 && RPW == 1 &&
+                          ((IS_GLU && SPL <= 2) || (F::BYTES == Q8_0_BYTES && SPL <= 4));
+    typename F::Act xa[XREG ? SPL : 1];
+    if constexpr (XREG) qmv_load_acts<F, SPL>(s_qs, lay.qstride, s_d, s_bs, gb, c, KB, xa);
+    auto rowdot = [&](const typename F::Raw(&r)[SPL]) __attribute__((always_inline)) -> float {
+        if constexpr (XREG) return qmv_row_x<F, SPL, RPW>(r, xa, gb, c, KB);
+        else return qmv_row<F, SPL, RPW>(r, s_qs, lay.qstride, s_d, s_bs, gb, c, KB);
+    };
     // a row's sums against every activation row of the workgroup, stored
     auto emit = [&](const typename F::Raw(&r)[SPL], int row, float res) __attribute__((always_inline)) {
         if constexpr (MR == 1) {
-            const float t = qmv_row<F, SPL>(r, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
+            const float t = rowdot(r);
             if (lane == 63) store(row, acc_out ? res + t : t);
         } else {
 #pragma unroll
@@ -426,8 +442,8 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
             int lrow = nrow < N ? nrow : row;
             qmv_load_row<F, SPL>(W + (size_t)lrow * row_bytes, gi, c, KB, rc);
             qmv_load_row<F, SPL>(W2 + (size_t)lrow * row_bytes, gi, c, KB, rd);
-            float tg = qmv_row<F, SPL>(ra, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
-            float tu = qmv_row<F, SPL>(rb, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
+            float tg = rowdot(ra);
+            float tu = rowdot(rb);
             qmv_settle_row<F, SPL>(ra);
             qmv_settle_row<F, SPL>(rb);
             put(silu_mul(tg, tu));
@@ -441,8 +457,8 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
             lrow = nrow < N ? nrow : row;
             qmv_load_row<F, SPL>(W + (size_t)lrow * row_bytes, gi, c, KB, ra);
             qmv_load_row<F, SPL>(W2 + (size_t)lrow * row_bytes, gi, c, KB, rb);
-            tg = qmv_row<F, SPL>(rc, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
-            tu = qmv_row<F, SPL>(rd, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
+            tg = rowdot(rc);
+            tu = rowdot(rd);
             qmv_settle_row<F, SPL>(rc);
             qmv_settle_row<F, SPL>(rd);
             put(silu_mul(tg, tu));
@@ -456,11 +472,11 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
         // row's while the up row is.
         while (row < N) {
             qmv_load_row<F, SPL>(W2 + (size_t)row * row_bytes, gi, c, KB, rb);
-            const float tg = qmv_row<F, SPL>(ra, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
+            const float tg = rowdot(ra);
             const int nrow = row + nw;
             const int lrow = nrow < N ? nrow : row;
             qmv_load_row<F, SPL>(W + (size_t)lrow * row_bytes, gi, c, KB, ra);
-            const float tu = qmv_row<F, SPL>(rb, s_qs, lay.qstride, s_d, s_bs, gi, c, KB);
+            const float tu = rowdot(rb);
             if (lane == 63) store(row, silu_mul(tg, tu));
             row = nrow;
         }
@@ -475,7 +491,7 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
         // 2048x12288 5.16 -> 5.00 us, 768x2048 2.82 -> 2.77; the MoE layer
         // unchanged)
         auto finish = [&](const typename F::Raw(&r)[SPL], float res, int g) {
-            const float t = qmv_row<F, SPL, RPW>(r, s_qs, lay.qstride, s_d, s_bs, gb, c, KB);
+            const float t = rowdot(r);
             const int my = g * RPW + rsub;
             if (seg_last && my < N) store(my, acc_out ? res + t : t);
         };
@@ -489,7 +505,7 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
             int lr = ngrp * RPW + rsub < N ? ngrp * RPW + rsub : N - 1;
             resb = ldres(lr, resb);
             qmv_load_row<F, SPL>(wrow(lr), gb, c, KB, rb);
-            float t = qmv_row<F, SPL, RPW>(ra, s_qs, lay.qstride, s_d, s_bs, gb, c, KB);
+            float t = rowdot(ra);
             int my = row * RPW + rsub;
             if (seg_last && my < N) store(my, acc_out ? resa + t : t);
             row = ngrp;
@@ -501,7 +517,7 @@ __device__ __forceinline__ void qmv_body(const uint8_t* __restrict__ W, const fl
             lr = ngrp * RPW + rsub < N ? ngrp * RPW + rsub : N - 1;
             resa = ldres(lr, resa);
             qmv_load_row<F, SPL>(wrow(lr), gb, c, KB, ra);
-            t = qmv_row<F, SPL, RPW>(rb, s_qs, lay.qstride, s_d, s_bs, gb, c, KB);
+            t = rowdot(rb);
             my = row * RPW + rsub;
             if (seg_last && my < N) store(my, acc_out ? resb + t : t);
             row = ngrp;

@@ -78,6 +78,43 @@ __device__ __forceinline__ void qmv_settle_row(const typename F::Raw (&r)[SPL]) 
     }
 }
 
+// The lane's activation slices of its block slots, read from LDS once: with
+// one activation row they are the same for every weight row, so the rings
+// keep them in registers (qmv_row_x) instead of reading them again per row.
+// A slot past the row's end reads the last block (never used).
+template <class F, int SPL>
+__device__ __forceinline__ void qmv_load_acts(const int8_t* s_qs, int qstride, const float* s_d, const int16_t* s_bs,
+                                              int gi, int c, int KB, typename F::Act (&xa)[SPL]) {
+    constexpr int BPW = 64 / F::LPB;
+#pragma unroll
+    for (int s = 0; s < SPL; s++) {
+        const int b = gi + BPW * s;
+        F::load_act(s_qs, qstride, s_d, s_bs, b < KB ? b : KB - 1, c, xa[s]);
+    }
+}
+
+// qmv_row with the activation slices in registers (the same arithmetic in
+// the same order: the same bits).
+template <class F, int SPL, int RPW = 1>
+__device__ __forceinline__ float qmv_row_x(const typename F::Raw (&r)[SPL], const typename F::Act (&xa)[SPL], int gi,
+                                           int c, int KB) {
+    constexpr int BPW = 64 / F::LPB;
+    float acc = 0.0f;
+#pragma unroll
+    for (int s = 0; s < SPL; s++) {
+        const int b = gi + BPW * s;
+        if (b < KB) {
+            int isum, msum;
+            float dw, dmw;
+            F::dot(r[s], xa[s], c, isum, msum, dw, dmw);
+            acc = fmaf(dw * xa[s].d, (float)isum, acc);
+            acc = fmaf(-(dmw * xa[s].d), (float)msum, acc);
+        }
+    }
+    if constexpr (RPW == 1) return dpp_wave_sum(acc);
+    else return dpp_seg_sum<RPW>(acc);
+}
+
 // Row dot product of one weight row (raw registers) with the LDS activation;
 // the f32 total is valid in lane 63 (RPW > 1: each 64/RPW-lane segment holds
 // its own row, total in the segment's last lane).
