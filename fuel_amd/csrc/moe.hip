@@ -422,8 +422,8 @@ __global__ __launch_bounds__(64 * DC_NW) void moe_down_combine_kernel(const uint
     __syncthreads();
 
     // 4. output rows, a two-row register ring: the next row's loads are in
-    //    flight while a row is reduced (past the last row a wavefront re-reads
-    //    its current row rather than branching around the loads)
+    //    flight while a row is reduced; a wavefront's last row issues no
+    //    further loads (a wave-uniform exit, as in the mat-vec rings)
     auto reduce_row = [&](int nn, const typename F::Raw(&rr)[NPASS]) {
         float y[NPASS];
 #pragma unroll
@@ -462,14 +462,22 @@ __global__ __launch_bounds__(64 * DC_NW) void moe_down_combine_kernel(const uint
     };
     const int stride = gridDim.x * DC_NW;
     typename F::Raw rb[NPASS];
-    while (n < d) {
+    if (n >= d) return;
+    while (true) {
         int nn = n + stride;
-        load_row(nn < d ? nn : n, rb);
+        if (nn >= d) {
+            reduce_row(n, raw);
+            return;
+        }
+        load_row(nn, rb);
         reduce_row(n, raw);
         n = nn;
-        if (n >= d) break;
         nn = n + stride;
-        load_row(nn < d ? nn : n, raw);
+        if (nn >= d) {
+            reduce_row(n, rb);
+            return;
+        }
+        load_row(nn, raw);
         reduce_row(n, rb);
         n = nn;
     }
