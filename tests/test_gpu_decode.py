@@ -113,7 +113,8 @@ def test_qmatmul_fused_glu(dev, dt, n, k, m, rms):
     (O.Q4K, 8192, 4096, 2, "rms"), (O.Q6K, 4096, 4096, 17, "rms"), (O.Q4K, 8192, 4096, 128, "rms"),
     (O.Q6K, 1000, 4096, 33, "rms"), (O.Q4K, 22016, 4096, 512, "rms"),
     (O.Q4K, 4096, 11008, 3, "swiglu"), (O.Q6K, 4096, 11008, 64, "swiglu"), (O.Q4K, 4096, 11008, 512, "swiglu"),
-    (O.Q6K, 4096, 4096, 40, "plain"), (O.Q4K, 4096, 4096, 512, "plain"), (O.Q4K, 700, 2048, 5, "plain")])
+    (O.Q6K, 4096, 4096, 40, "plain"), (O.Q4K, 4096, 4096, 512, "plain"), (O.Q4K, 700, 2048, 5, "plain"),
+    (O.Q4K, 22016, 4096, 8, "rms"), (O.Q4K, 4096, 11008, 24, "swiglu"), (O.Q6K, 32000, 4096, 8, "rms")])
 def test_qmatmul_fused_batched(dev, dt, n, k, m, mode):
     """Several rows through the fused entry point (the batched prompt pass):
     the rows formed by the prologue (RMS norm x gain, the SwiGLU product of
